@@ -1,0 +1,225 @@
+"""Headline benchmark: one decode step of a random-init Qwen3-0.6B-shape model (28 layers,
+hidden 1024, 16/8 heads, head_dim 128, SwiGLU 3072, vocab 151936, tied embeddings) at batch
+64 with 2048-token contexts, on one MI355X.
+
+A step is one iteration of the decode token loop: build the decode batch (host + one device
+kernel), the 28-layer forward (every op a HIP kernel), greedy sampling, tokens back to the
+host. The request state is rolled back after each step so every timed step has identical
+work (context 2049). Prints one JSON line with:
+  value        decode tokens/s of the whole step
+  roofline     the decode-attention kernel (dominant: ~93% of the step's bytes), its average
+               launch duration measured with HIP events on the launch stream, algorithmic
+               bytes per launch (K + V rows read + kv_indices + q + o) / duration, vs 8 TB/s
+  cpu_baseline the CPU oracle (fp32 torch restatement of the step) on a bounded sample
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "deterministic-inference_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--context", type=int, default=2048)
+    ap.add_argument("--mode", default="nondet", choices=["nondet", "dvr", "batch_invariant"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--attn-reps", type=int, default=4)
+    return ap.parse_args()
+
+
+class DecodeWorkload:
+    """64 running requests with 2048-token prefixes whose KV is synthetic (N(0,1) bf16 in
+    page-shuffled slots); each decode step feeds one token per request at position 2048."""
+
+    def __init__(self, batch, context, mode, seed=0):
+        import torch
+        from sid.config import EngineConfig, Mode, SamplingParams
+        from sid.engine.model_runner import ModelRunner
+        from sid.engine.request import Request
+
+        self.torch = torch
+        pool = batch * (context + 16) + 4096
+        self.cfg = EngineConfig(mode=Mode(mode), kv_pool_tokens=pool, max_reqs=batch + 2,
+                                max_seq_len=context + 64, max_decode_batch=batch, seed=seed)
+        self.runner = ModelRunner(self.cfg, "cuda")
+        kv = self.kv = self.runner.kv_cache
+        g = torch.Generator(device="cuda").manual_seed(seed + 1)
+        for pool_t in kv.k_pools + kv.v_pools:
+            pool_t.copy_(torch.randn(pool_t.shape, generator=g, device="cuda").to(pool_t.dtype))
+        # page-shuffled slot assignment (page size 16)
+        slots = kv.alloc(batch * context)
+        pages = slots.view(-1, 16)[torch.randperm(batch * context // 16,
+                                                  generator=torch.Generator().manual_seed(seed))]
+        slots = pages.reshape(batch, context)
+        vocab = self.runner.mcfg.vocab_size
+        gen = torch.Generator().manual_seed(seed + 2)
+        self.reqs = []
+        for i in range(batch):
+            r = Request(i, torch.randint(0, vocab, (context,), generator=gen).tolist(),
+                        SamplingParams(max_new_tokens=1 << 20, ignore_eos=True),
+                        self.runner.mcfg.eos_token_ids)
+            r.req_row = kv.alloc_row()
+            kv.write_row(r.req_row, 0, slots[i])
+            r.output_ids.append(int(torch.randint(0, vocab, (1,), generator=gen)))
+            self.reqs.append(r)
+        self.invariant = self.cfg.mode == Mode.BATCH_INVARIANT
+
+    def build(self):
+        from sid.engine.batch import build_decode_batch
+        return build_decode_batch(self.reqs, self.kv, "cuda", self.invariant)
+
+    def step(self):
+        fb = self.build()
+        logits = self.runner.forward(fb)
+        toks = self.runner.sample(fb, logits).tolist()
+        # roll the state back: release this step's slots (LIFO: the next step reuses them)
+        rows = [r.req_row for r in self.reqs]
+        pos = [r.kv_len for r in self.reqs]
+        self.kv.free(self.kv.req_to_token[rows, pos])
+        return toks
+
+
+def time_steps(wl, steps, warmup):
+    torch = wl.torch
+    for _ in range(warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        wl.step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def attention_roofline(wl, reps):
+    """Average duration of the decode-attention launch at this step's real shape, HIP events
+    on torch's current stream (the launch stream), over reps x 28 layer pools."""
+    torch = wl.torch
+    fb = wl.build()
+    mcfg = wl.runner.mcfg
+    attn = wl.runner.decode_attn
+    q = torch.randn(len(wl.reqs), mcfg.num_q_heads, mcfg.head_dim, device="cuda").to(torch.bfloat16)
+    scale = mcfg.head_dim ** -0.5
+    # warm
+    for layer in range(mcfg.num_layers):
+        kp, vp = wl.kv.layer(layer)
+        attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len, scale,
+                     wl.invariant)
+    torch.cuda.synchronize()
+    pairs = []
+    for _ in range(reps):
+        for layer in range(mcfg.num_layers):
+            kp, vp = wl.kv.layer(layer)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len,
+                         scale, wl.invariant)
+            e.record()
+            pairs.append((s, e))
+    torch.cuda.synchronize()
+    avg_ms = sum(s.elapsed_time(e) for s, e in pairs) / len(pairs)
+    rows = int(fb.kv_indptr[-1].item())
+    b = len(wl.reqs)
+    bytes_launch = (rows * mcfg.num_kv_heads * mcfg.head_dim * 2 * 2   # K + V rows
+                    + rows * 4                                           # kv_indices
+                    + 2 * b * mcfg.num_q_heads * mcfg.head_dim * 2)      # q in, o out
+    wl.kv.free(wl.kv.req_to_token[[r.req_row for r in wl.reqs], [r.kv_len for r in wl.reqs]])
+    achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "decode_stage1_kernel (split-KV flash decode, 1 split at B=64)",
+            "avg_launch_us": round(avg_ms * 1e3, 2), "bytes_per_launch": bytes_launch,
+            "launches_timed": len(pairs)}
+
+
+def cpu_baseline(wl):
+    """The CPU oracle (oracle/qwen3.py) on the same batch: embedding + 1 layer + head and
+    embedding + 2 layers + head are timed; a full step is t1 + 27 * (t2 - t1)."""
+    import torch
+    from oracle.qwen3 import forward_ref
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    fb = wl.build()
+    w = wl.runner.model.w
+    wc = {"embed": w["embed"].cpu(), "norm": w["norm"].cpu(), "lm_head": w["embed"].cpu(),
+          "layers": [{k: v.cpu() for k, v in w["layers"][i].items()} for i in range(2)]}
+    used = fb.kv_indices.long()
+    rows = used.numel()
+    kp = [wl.kv.k_pools[i][used].cpu() for i in range(2)]
+    vp = [wl.kv.v_pools[i][used].cpu() for i in range(2)]
+    indptr = fb.kv_indptr.cpu()
+    batch = {"mode": "decode", "input_ids": fb.input_ids.cpu(), "positions": fb.positions.cpu(),
+             "out_slots": (indptr[1:] - 1).long(), "kv_indptr": indptr,
+             "kv_indices": torch.arange(rows, dtype=torch.int32),
+             "sample_indices": torch.arange(len(wl.reqs))}
+    wl.kv.free(wl.kv.req_to_token[[r.req_row for r in wl.reqs], [r.kv_len for r in wl.reqs]])
+    mcfg = wl.runner.mcfg
+
+    def timed(layers):
+        t0 = time.perf_counter()
+        forward_ref(wc, mcfg, kp, vp, batch, layers=layers)
+        return time.perf_counter() - t0
+
+    timed(1)  # warm
+    t1 = timed(1)
+    t2 = timed(2)
+    per_layer = max(t2 - t1, 1e-9)
+    step = t1 + (mcfg.num_layers - 1) * per_layer
+    return {"value": round(len(wl.reqs) / step, 3), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"oracle/qwen3.py forward_ref on the same B={len(wl.reqs)} x ctx "
+                       f"{rows // len(wl.reqs)} decode batch: embedding+1 layer+head "
+                       f"({t1:.2f}s) and +2 layers ({t2:.2f}s) timed, full step = t1 + "
+                       f"{mcfg.num_layers - 1} x (t2 - t1) = {step:.2f}s")}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only (the decode path is single-GPU, as in "
+              "the reference); --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    wl = DecodeWorkload(args.batch, args.context, args.mode)
+    sec = time_steps(wl, args.steps, args.warmup)
+    roof = attention_roofline(wl, args.attn_reps)
+    base = None if args.no_cpu_baseline else cpu_baseline(wl)
+    b = args.batch
+    out = {
+        "metric": "decode tokens/s, Qwen3-0.6B shape bs=64; decode-attn HBM GB/s (% of peak)",
+        "value": round(b / sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: random-init weights ~N(0,0.02), random token ids, N(0,1) KV prefixes",
+        "config": {"workload": f"Qwen3-0.6B-shape decode step, batch {b}, context "
+                               f"{args.context}+1, greedy, {args.mode} split policy",
+                   "batch": b, "context": args.context, "layers": wl.runner.mcfg.num_layers,
+                   "mode": args.mode},
+        "roofline": roof,
+        "cpu_baseline": base,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,85 @@
+// Shared helpers for the sid HIP kernels (gfx950 / CDNA4, wave64).
+//
+// Everything here is device-agnostic plumbing: bf16 <-> fp32 conversion with
+// round-to-nearest-even (the rounding torch uses for bf16 tensors), wave64 DPP
+// lane exchanges, the thread-local error string returned through the C-ABI,
+// and launch checking.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdarg>
+
+#include "../../include/sid_hip.h"
+
+namespace sid {
+
+typedef uint16_t bf16_t;  // raw bf16 bits; the C-ABI passes bf16 tensors as void*
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_v;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_v;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_v;
+
+__device__ __forceinline__ float bf16_lo(uint32_t packed) {
+  return __uint_as_float(packed << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t packed) {
+  return __uint_as_float(packed & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(bf16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16_t>(u >> 16);
+}
+
+// Round an fp32 value to the nearest bf16 and return it as fp32.
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f32(f32_to_bf16(f));
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// DPP lane exchanges inside a row of 16 lanes. The control words are the
+// GCN/CDNA DPP encodings: quad_perm [1,0,3,2] swaps neighbours, quad_perm
+// [2,3,0,1] swaps pairs, row_half_mirror reverses each group of 8 lanes,
+// row_ror:8 rotates a 16-lane row by 8 (an exchange of the two halves).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;
+constexpr int DPP_QUAD_XOR2 = 0x4E;
+constexpr int DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_ROR8 = 0x128;
+
+// Full-wave exchange for lanes farther apart than a DPP row (ds_bpermute).
+__device__ __forceinline__ float lane_xor(float v, int mask) {
+  const int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
+}
+
+__host__ __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Thread-local error message for the C-ABI (read back via sid_last_error()).
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+
+}  // namespace sid
+
+#define SID_REQUIRE(cond, ...)                 \
+  do {                                         \
+    if (!(cond)) {                             \
+      ::sid::set_error(__VA_ARGS__);           \
+      return SID_ERR_INVALID;                  \
+    }                                          \
+  } while (0)

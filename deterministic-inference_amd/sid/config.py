@@ -1,0 +1,100 @@
+"""Engine, model and sampling configuration (same fields and defaults as sid/config.py).
+
+Modes:
+  nondet          fast path only; the decode attention split count follows the batch size,
+                  so a request's output depends on its co-tenants.
+  dvr             decode-verify-rollback: the nondet fast path plus fixed-shape G x W verify
+                  passes that make is_deterministic requests reproducible.
+  batch_invariant fixed 256-token attention splits; deterministic by construction.
+"""
+
+from __future__ import annotations
+
+import enum
+from dataclasses import dataclass
+from typing import Optional
+
+
+class Mode(str, enum.Enum):
+    NONDET = "nondet"
+    DVR = "dvr"
+    BATCH_INVARIANT = "batch_invariant"
+
+
+# Padding token of verify windows and dummy verify sequences (sid/config.py:26).
+DUMMY_TOKEN_ID = 32
+
+
+@dataclass
+class ModelConfig:
+    model_path: str = "random:qwen3-0.6b"
+    num_layers: int = 28
+    hidden_size: int = 1024
+    num_q_heads: int = 16
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate_size: int = 3072
+    vocab_size: int = 151936
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    max_position_embeddings: int = 40960
+    tie_word_embeddings: bool = True
+    eos_token_ids: tuple = (151645, 151643)
+
+    @property
+    def q_size(self) -> int:
+        return self.num_q_heads * self.head_dim
+
+    @property
+    def kv_size(self) -> int:
+        return self.num_kv_heads * self.head_dim
+
+
+@dataclass
+class EngineConfig:
+    # "random:<name>" builds a random-init Qwen3-0.6B-shape model (no download); a directory
+    # path loads config.json + safetensors from disk.
+    model_path: str = "random:qwen3-0.6b"
+    mode: Mode = Mode.DVR
+    dtype: str = "bfloat16"
+
+    kv_pool_tokens: int = 256 * 1024
+    max_reqs: int = 256
+    max_seq_len: int = 32768
+    max_prompt_len: int = 16384
+
+    max_prefill_tokens: int = 8192
+    max_decode_batch: int = 256
+
+    dvr_window_size: int = 32
+    dvr_group_size: int = 4
+
+    max_kv_splits: int = 32
+    invariant_split_size: int = 256
+
+    decode_backend: str = "hip"  # "hip" split-KV kernel | "extend" (extend kernel, debugging)
+
+    device: str = "cuda"
+    seed: int = 0  # random-init weight seed
+    num_layers: Optional[int] = None  # override (smaller random models for tests)
+    vocab_size: Optional[int] = None
+
+
+@dataclass
+class SamplingParams:
+    temperature: float = 0.0
+    top_k: int = -1
+    top_p: float = 1.0
+    max_new_tokens: int = 128
+    seed: int = 42
+    is_deterministic: bool = False
+    stop_token_ids: Optional[list] = None
+    ignore_eos: bool = False
+
+    def __post_init__(self):
+        if self.temperature < 0:
+            raise ValueError("temperature must be >= 0")
+        if not (0.0 < self.top_p <= 1.0):
+            raise ValueError("top_p must be in (0, 1]")
+        if self.max_new_tokens < 1:
+            raise ValueError("max_new_tokens must be >= 1")

@@ -1,0 +1,132 @@
+"""ForwardBatch and the prefill / decode batch builders (sid/engine/batch.py).
+
+sample_pos is the absolute position of the token being generated, on every path:
+prefill of P tokens generates position P; a decode step feeding output_ids[N-1] (at
+position P+N-1) generates P+N; verify row j of a window starting at verified_len v
+generates P+v+j. (A mismatch here would make every verify window fail at index 0.)
+
+Host work per decode step is O(B) Python plus three host->device copies; the kv_indices
+of the whole batch are built on the device from the request->token table by one kernel.
+"""
+
+from __future__ import annotations
+
+import enum
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from sid.engine.request import Request
+from sid.kernels.jit import load_ext
+
+
+class ForwardMode(enum.Enum):
+    PREFILL = "prefill"
+    DECODE = "decode"
+    VERIFY = "verify"
+
+
+@dataclass
+class ForwardBatch:
+    mode: ForwardMode
+    input_ids: torch.Tensor       # int64 [T]
+    positions: torch.Tensor       # int64 [T]
+    out_slots: torch.Tensor       # int64 [T] (KV write targets; < 0 skips)
+    kv_indptr: Optional[torch.Tensor] = None   # int32 [B+1], full sequence (prefix + new)
+    kv_indices: Optional[torch.Tensor] = None  # int32
+    seq_lens: Optional[torch.Tensor] = None    # int32 [B] (decode)
+    max_seq_len: int = 0                        # host-side max(seq_lens)
+    qo_indptr: Optional[torch.Tensor] = None   # int32 [B+1] (extend paths)
+    max_extend_len: int = 0
+    sample_indices: Optional[torch.Tensor] = None    # int64 [R]; None = every row
+    sample_positions: Optional[torch.Tensor] = None  # int64 [R]
+    temperatures: Optional[torch.Tensor] = None      # fp32 [R]
+    top_ks: Optional[torch.Tensor] = None            # int64 [R]
+    top_ps: Optional[torch.Tensor] = None            # fp32 [R]
+    seeds: Optional[torch.Tensor] = None             # int64 [R]
+    invariant: bool = False
+    all_greedy: Optional[bool] = None  # host-known: every row has temperature 0
+
+
+def _sampling_host(reqs, repeat: int = 1):
+    temps = np.repeat(np.array([r.params.temperature for r in reqs], dtype=np.float32), repeat)
+    top_ps = np.repeat(np.array([r.params.top_p for r in reqs], dtype=np.float32), repeat)
+    top_ks = np.repeat(np.array([r.params.top_k if r.params.top_k > 0 else -1 for r in reqs],
+                                dtype=np.int64), repeat)
+    seeds = np.repeat(np.array([r.params.seed for r in reqs], dtype=np.int64), repeat)
+    return temps, top_ks, top_ps, seeds
+
+
+def _to_device(arrays: list, dtype, device) -> list:
+    """One host->device copy for several same-dtype 1-D arrays; returns device views."""
+    sizes = [int(a.size) for a in arrays]
+    host = torch.from_numpy(np.concatenate([np.asarray(a, dtype=dtype) for a in arrays]))
+    dev = host.to(device)
+    out, off = [], 0
+    for n in sizes:
+        out.append(dev[off:off + n])
+        off += n
+    return out
+
+
+def build_prefill_batch(reqs: list, kv, device: str, invariant: bool) -> ForwardBatch:
+    """Allocates prompt slots; extend attention with prefix 0."""
+    ids, pos, slots, qo = [], [], [], [0]
+    for r in reqs:
+        p = r.prompt_len
+        s = kv.alloc(p)
+        kv.write_row(r.req_row, 0, s)
+        ids.append(np.asarray(r.prompt_ids, dtype=np.int64))
+        pos.append(np.arange(p, dtype=np.int64))
+        slots.append(s.numpy())
+        qo.append(qo[-1] + p)
+    temps, top_ks, top_ps, seeds = _sampling_host(reqs)
+    qo_np = np.asarray(qo, dtype=np.int64)
+    i64 = _to_device([np.concatenate(ids), np.concatenate(pos), np.concatenate(slots),
+                      qo_np[1:] - 1, np.asarray([r.prompt_len for r in reqs]), top_ks, seeds],
+                     np.int64, device)
+    i32 = _to_device([qo_np, np.concatenate(slots)], np.int32, device)
+    f32 = _to_device([temps, top_ps], np.float32, device)
+    return ForwardBatch(
+        mode=ForwardMode.PREFILL, input_ids=i64[0], positions=i64[1], out_slots=i64[2],
+        qo_indptr=i32[0], kv_indptr=i32[0], kv_indices=i32[1],
+        max_extend_len=max(r.prompt_len for r in reqs),
+        sample_indices=i64[3], sample_positions=i64[4],
+        temperatures=f32[0], top_ks=i64[5], top_ps=f32[1], seeds=i64[6],
+        invariant=invariant, all_greedy=bool((temps == 0).all()),
+    )
+
+
+def build_decode_batch(reqs: list, kv, device: str, invariant: bool) -> ForwardBatch:
+    """One new token per request; attention covers the full sequence including the
+    position being written now."""
+    bs = len(reqs)
+    pos = np.fromiter((r.prompt_len + r.num_output - 1 for r in reqs), dtype=np.int64, count=bs)
+    for r, p in zip(reqs, pos.tolist()):
+        assert p == r.kv_len, f"req {r.rid}: decode position {p} != kv_len {r.kv_len}"
+    ids = np.fromiter((r.output_ids[-1] for r in reqs), dtype=np.int64, count=bs)
+    rows = np.fromiter((r.req_row for r in reqs), dtype=np.int64, count=bs)
+    new_slots = kv.alloc(bs).numpy()
+    kv.req_to_token[torch.from_numpy(rows), torch.from_numpy(pos)] = \
+        torch.from_numpy(new_slots.astype(np.int32))
+    seq_lens = pos + 1
+    indptr = np.zeros(bs + 1, dtype=np.int64)
+    np.cumsum(seq_lens, out=indptr[1:])
+    temps, top_ks, top_ps, seeds = _sampling_host(reqs)
+    d_ids, d_pos, d_rows, d_slots, d_spos, d_topk, d_seed = _to_device(
+        [ids, pos, rows, new_slots, pos + 1, top_ks, seeds], np.int64, device)
+    d_indptr, d_lens = _to_device([indptr, seq_lens], np.int32, device)
+    d_temps, d_topp = _to_device([temps, top_ps], np.float32, device)
+    kv_indices = torch.empty(int(indptr[-1]), dtype=torch.int32, device=device)
+    load_ext().build_decode_indices(kv.req_to_token_gpu, d_rows, d_slots, d_indptr, kv_indices)
+    return ForwardBatch(
+        mode=ForwardMode.DECODE, input_ids=d_ids, positions=d_pos, out_slots=d_slots,
+        kv_indptr=d_indptr, kv_indices=kv_indices, seq_lens=d_lens,
+        max_seq_len=int(seq_lens.max()) if bs else 0,
+        qo_indptr=None, max_extend_len=1,
+        sample_indices=None, sample_positions=d_spos,
+        temperatures=d_temps, top_ks=d_topk, top_ps=d_topp, seeds=d_seed,
+        invariant=invariant, all_greedy=bool((temps == 0).all()),
+    )

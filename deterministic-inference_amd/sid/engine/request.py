@@ -1,0 +1,81 @@
+"""Request state machine and the KV-length invariant (as sid/engine/request.py).
+
+  WAITING -> RUNNING -> DONE                                   (nondet / batch_invariant)
+  WAITING -> RUNNING <-> FINISHED_PENDING_VERIFY -> DONE        (dvr, is_deterministic)
+
+With P prompt tokens and N >= 1 outputs, the KV covers positions 0 .. P+N-2: the newest
+sampled token has no KV until it is fed back in the next decode step.
+"""
+
+from __future__ import annotations
+
+import enum
+from typing import Optional
+
+from sid.config import SamplingParams
+
+
+class RequestState(enum.Enum):
+    WAITING = "waiting"
+    RUNNING = "running"
+    FINISHED_PENDING_VERIFY = "finished_pending_verify"
+    DONE = "done"
+
+
+class Request:
+    def __init__(self, rid: int, prompt_ids: list, params: SamplingParams, eos_token_ids: tuple):
+        self.rid = rid
+        self.prompt_ids = list(prompt_ids)
+        self.params = params
+        self.eos_token_ids = set(eos_token_ids)
+        if params.stop_token_ids:
+            self.eos_token_ids.update(params.stop_token_ids)
+        self.output_ids: list = []
+        self.state = RequestState.WAITING
+        self.finished_reason: Optional[str] = None
+        self.req_row = -1
+        self.verified_len = 0
+        self.num_windows = 0
+        self.num_rollbacks = 0
+        self.tokens_rolled_back = 0
+        self.stream_offset = 0
+
+    @property
+    def prompt_len(self) -> int:
+        return len(self.prompt_ids)
+
+    @property
+    def num_output(self) -> int:
+        return len(self.output_ids)
+
+    @property
+    def kv_len(self) -> int:
+        return 0 if not self.output_ids else self.prompt_len + self.num_output - 1
+
+    def unverified(self) -> int:
+        return self.num_output - self.verified_len
+
+    def gate(self, dvr_mode: bool) -> int:
+        """How many output tokens the client may see."""
+        return self.verified_len if (dvr_mode and self.params.is_deterministic) else self.num_output
+
+    def check_finished(self) -> None:
+        """Derive finished_reason from the current outputs (re-derivable after a rollback)."""
+        if not self.output_ids:
+            self.finished_reason = None
+        elif not self.params.ignore_eos and self.output_ids[-1] in self.eos_token_ids:
+            self.finished_reason = "stop"
+        elif self.num_output >= self.params.max_new_tokens:
+            self.finished_reason = "length"
+        else:
+            self.finished_reason = None
+
+    def assert_invariants(self, dvr_mode: bool) -> None:
+        assert 0 <= self.verified_len <= self.num_output, \
+            f"req {self.rid}: verified_len {self.verified_len} vs outputs {self.num_output}"
+        assert self.stream_offset <= self.gate(dvr_mode), f"req {self.rid}: emitted beyond gate"
+
+    def __repr__(self) -> str:
+        return (f"Request(rid={self.rid}, state={self.state.value}, P={self.prompt_len}, "
+                f"N={self.num_output}, verified={self.verified_len}, "
+                f"finished={self.finished_reason})")

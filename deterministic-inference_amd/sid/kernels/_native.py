@@ -1,0 +1,232 @@
+"""ctypes binding of libsid_hip.so: torch tensors in, raw device pointers out.
+
+Each method checks its tensors the way the reference's TORCH_CHECKs do
+(sid/csrc/flash_decode.cu:325-345, 386-395) and raises RuntimeError on a violation or on
+a non-zero status from the library (message from `sid_last_error()`). Launches go on
+torch's current stream of the tensors' device, so they order with surrounding torch work
+and are captured by `torch.cuda.graph` like any torch op.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+_i32, _i64, _f32, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+# name -> argtypes (every entry point returns int status)
+_SIGNATURES = {
+    "sid_reshape_and_cache": [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp],
+    "sid_flash_decode_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i32,
+                             _i32, _f32, _vp, _vp, _i32, _i32, _vp, _vp],
+    "sid_extend_attention_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32,
+                                 _i64, _i32, _f32, _vp, _vp],
+    "sid_rmsnorm": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
+    "sid_fused_add_rmsnorm": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
+    "sid_rope_apply": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _vp],
+    "sid_linear": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    "sid_silu_mul": [_vp, _vp, _i64, _i64, _vp],
+    "sid_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
+    "sid_build_decode_indices": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
+}
+EXPORTED = ("sid_last_error", "sid_abi_version", *_SIGNATURES)
+ABI_VERSION = 1
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _gpu(t: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> None:
+    _check(isinstance(t, torch.Tensor) and t.is_cuda, f"{name} must be a GPU tensor")
+    _check(t.is_contiguous(), f"{name} must be contiguous")
+    if dtype is not None:
+        _check(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class NativeLib:
+    """The loaded library; method names and argument orders follow the reference ops."""
+
+    def __init__(self, path: Path):
+        self.path = Path(path)
+        self.lib = ctypes.CDLL(str(self.path))
+        self.lib.sid_last_error.restype = ctypes.c_char_p
+        self.lib.sid_last_error.argtypes = []
+        self.lib.sid_abi_version.restype = ctypes.c_int
+        self.lib.sid_abi_version.argtypes = []
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(self.lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        ver = self.lib.sid_abi_version()
+        _check(ver == ABI_VERSION, f"libsid_hip.so ABI {ver} != expected {ABI_VERSION}; rebuild")
+
+    def _call(self, name: str, *args) -> None:
+        rc = getattr(self.lib, name)(*args)
+        if rc != 0:
+            raise RuntimeError(f"{name}: {self.lib.sid_last_error().decode(errors='replace')}")
+
+    # ---- reference module `sid_flash_decode` (sid/csrc/flash_decode.cu:408-413) ----------
+
+    def flash_decode_fwd(self, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
+                         max_splits: int, fixed_split_size: int, sm_scale: float,
+                         part_o, part_lse, o) -> None:
+        _gpu(q, "q", torch.bfloat16)
+        _check(q.dim() == 3, "q must be [B, HQ, D]")
+        b, hq, d = q.shape
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+            _gpu(t, name, torch.bfloat16)
+            _check(t.dim() == 3 and t.shape[2] == d, f"{name} must be [slots, HKV, {d}]")
+        _check(k_cache.shape == v_cache.shape, "k_cache and v_cache shapes differ")
+        hkv = k_cache.shape[1]
+        _gpu(kv_indptr, "kv_indptr", torch.int32)
+        _check(kv_indptr.numel() == b + 1, "kv_indptr must have B+1 entries")
+        _gpu(kv_indices, "kv_indices", torch.int32)
+        _gpu(num_splits, "num_splits", torch.int32)
+        _check(num_splits.numel() == b, "num_splits must have B entries")
+        _gpu(part_o, "part_o", torch.float32)
+        _gpu(part_lse, "part_lse", torch.float32)
+        _check(part_o.dim() == 4 and part_o.shape[1] == hq and part_o.shape[3] == d,
+               "part_o workspace too small / wrong shape")
+        _check(part_lse.dim() == 3 and part_lse.shape[1] == hq
+               and part_lse.shape[2] == part_o.shape[2] and part_lse.shape[0] >= part_o.shape[0],
+               "part_lse workspace shape mismatch")
+        _gpu(o, "o", torch.bfloat16)
+        _check(o.shape == q.shape, "o must have q's shape")
+        self._call("sid_flash_decode_fwd", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                   kv_indptr.data_ptr(), kv_indices.data_ptr(), num_splits.data_ptr(), b, hq, hkv,
+                   d, k_cache.shape[0], int(max_splits), int(fixed_split_size), float(sm_scale),
+                   part_o.data_ptr(), part_lse.data_ptr(), part_o.shape[0], part_o.shape[2],
+                   o.data_ptr(), _stream(q))
+
+    def reshape_and_cache(self, k, v, k_cache, v_cache, slot_mapping) -> None:
+        _gpu(k, "k", torch.bfloat16)
+        _gpu(v, "v", torch.bfloat16)
+        _check(v.shape == k.shape, "v must have k's shape")
+        _gpu(k_cache, "k_cache", torch.bfloat16)
+        _gpu(v_cache, "v_cache", torch.bfloat16)
+        _check(k_cache.shape == v_cache.shape and k_cache.dim() == 3, "bad cache shapes")
+        _check(k.dim() == 3 and k.shape[1:] == k_cache.shape[1:],
+               "k must be [T, HKV, D] matching the cache")
+        _gpu(slot_mapping, "slot_mapping", torch.int64)
+        _check(slot_mapping.numel() == k.shape[0], "slot_mapping must have T entries")
+        if k.shape[0] == 0:
+            return
+        self._call("sid_reshape_and_cache", k.data_ptr(), v.data_ptr(), k_cache.data_ptr(),
+                   v_cache.data_ptr(), slot_mapping.data_ptr(), k.shape[0], k_cache.shape[1],
+                   k_cache.shape[2], k_cache.shape[0], _stream(k))
+
+    # ---- the rest of the decode path ----------------------------------------------------
+
+    def extend_attention_fwd(self, q, k_buffer, v_buffer, qo_indptr, kv_indptr, kv_indices,
+                             max_extend_len: int, sm_scale: float, o) -> None:
+        _gpu(q, "q_extend", torch.bfloat16)
+        _check(q.dim() == 3, "q_extend must be [Text, HQ, D]")
+        _gpu(k_buffer, "k_buffer", torch.bfloat16)
+        _gpu(v_buffer, "v_buffer", torch.bfloat16)
+        _check(k_buffer.shape == v_buffer.shape and k_buffer.dim() == 3
+               and k_buffer.shape[2] == q.shape[2], "bad KV buffer shapes")
+        _gpu(qo_indptr, "qo_indptr", torch.int32)
+        _gpu(kv_indptr, "kv_indptr", torch.int32)
+        _gpu(kv_indices, "kv_indices", torch.int32)
+        _check(qo_indptr.numel() == kv_indptr.numel(), "qo_indptr/kv_indptr length mismatch")
+        _gpu(o, "o", torch.bfloat16)
+        _check(o.shape == q.shape, "o must have q's shape")
+        self._call("sid_extend_attention_fwd", q.data_ptr(), k_buffer.data_ptr(),
+                   v_buffer.data_ptr(), qo_indptr.data_ptr(), kv_indptr.data_ptr(),
+                   kv_indices.data_ptr(), qo_indptr.numel() - 1, q.shape[0], q.shape[1],
+                   k_buffer.shape[1], q.shape[2], k_buffer.shape[0], int(max_extend_len),
+                   float(sm_scale), o.data_ptr(), _stream(q))
+
+    def rmsnorm(self, x, w, out, eps: float) -> None:
+        _gpu(x, "x", torch.bfloat16)
+        _gpu(w, "weight", torch.bfloat16)
+        _gpu(out, "out", torch.bfloat16)
+        hidden = x.shape[-1]
+        _check(w.numel() == hidden and out.shape == x.shape, "rmsnorm shape mismatch")
+        self._call("sid_rmsnorm", x.data_ptr(), w.data_ptr(), out.data_ptr(),
+                   x.numel() // max(hidden, 1), hidden, float(eps), _stream(x))
+
+    def fused_add_rmsnorm(self, x, residual, w, eps: float) -> None:
+        _gpu(x, "x", torch.bfloat16)
+        _gpu(residual, "residual", torch.bfloat16)
+        _gpu(w, "weight", torch.bfloat16)
+        hidden = x.shape[-1]
+        _check(residual.shape == x.shape and w.numel() == hidden, "fused_add_rmsnorm shape mismatch")
+        self._call("sid_fused_add_rmsnorm", x.data_ptr(), residual.data_ptr(), w.data_ptr(),
+                   x.numel() // max(hidden, 1), hidden, float(eps), _stream(x))
+
+    def rope_apply(self, q, k, positions, cos_sin) -> None:
+        _gpu(q, "q", torch.bfloat16)
+        _gpu(k, "k", torch.bfloat16)
+        _gpu(positions, "positions", torch.int64)
+        _gpu(cos_sin, "cos_sin", torch.float32)
+        t, hq, d = q.shape
+        _check(k.dim() == 3 and k.shape[0] == t and k.shape[2] == d, "k must be [T, HKV, D]")
+        _check(positions.numel() == t, "positions must have T entries")
+        _check(cos_sin.dim() == 2 and cos_sin.shape[1] == d, "cos_sin must be [max_pos, D]")
+        self._call("sid_rope_apply", q.data_ptr(), k.data_ptr(), positions.data_ptr(),
+                   cos_sin.data_ptr(), t, hq, k.shape[1], d, cos_sin.shape[0], _stream(q))
+
+    def linear(self, x, w, bias, y, out_fp32: bool) -> None:
+        _check(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1,
+               "x must be a 2-D bf16 GPU tensor with unit column stride")
+        _gpu(w, "weight", torch.bfloat16)
+        m, k = x.shape
+        n = w.shape[0]
+        _check(w.dim() == 2 and w.shape[1] == k, f"weight must be [N, {k}]")
+        if bias is not None:
+            _gpu(bias, "bias", torch.bfloat16)
+            _check(bias.numel() == n, "bias must have N entries")
+        _gpu(y, "out", torch.float32 if out_fp32 else torch.bfloat16)
+        _check(tuple(y.shape) == (m, n), "out must be [M, N]")
+        self._call("sid_linear", x.data_ptr(), x.stride(0) if m > 1 else k, w.data_ptr(),
+                   bias.data_ptr() if bias is not None else None, y.data_ptr(), m, n, k,
+                   1 if out_fp32 else 0, _stream(x))
+
+    def silu_mul(self, gate_up, out) -> None:
+        _gpu(gate_up, "gate_up", torch.bfloat16)
+        _gpu(out, "out", torch.bfloat16)
+        t, two_i = gate_up.shape
+        _check(two_i % 2 == 0 and tuple(out.shape) == (t, two_i // 2), "silu_mul shape mismatch")
+        self._call("sid_silu_mul", gate_up.data_ptr(), out.data_ptr(), t, two_i // 2, _stream(out))
+
+    def gather_rows(self, table, idx, out) -> None:
+        _gpu(table, "table", torch.bfloat16)
+        _gpu(idx, "indices", torch.int64)
+        _gpu(out, "out", torch.bfloat16)
+        _check(out.shape[0] == idx.numel() and out.shape[1:] == table.shape[1:],
+               "gather_rows shape mismatch")
+        row = table[0].numel() if table.shape[0] > 0 else out[0].numel()
+        self._call("sid_gather_rows", table.data_ptr(), idx.data_ptr(), out.data_ptr(),
+                   idx.numel(), row, table.shape[0], _stream(out))
+
+    def argmax_rows(self, logits, out) -> None:
+        _check(logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2
+               and logits.stride(1) == 1, "logits must be 2-D fp32 on the GPU, unit column stride")
+        _gpu(out, "out", torch.int64)
+        _check(out.numel() == logits.shape[0], "out must have one entry per row")
+        self._call("sid_argmax_rows", logits.data_ptr(), logits.stride(0), out.data_ptr(),
+                   logits.shape[0], logits.shape[1], _stream(out))
+
+    def build_decode_indices(self, req_to_token, rows, new_slots, kv_indptr, kv_indices) -> None:
+        _gpu(req_to_token, "req_to_token", torch.int32)
+        _gpu(rows, "rows", torch.int64)
+        if new_slots is not None:
+            _gpu(new_slots, "new_slots", torch.int64)
+            _check(new_slots.numel() == rows.numel(), "new_slots must have B entries")
+        _gpu(kv_indptr, "kv_indptr", torch.int32)
+        _gpu(kv_indices, "kv_indices", torch.int32)
+        _check(kv_indptr.numel() == rows.numel() + 1, "kv_indptr must have B+1 entries")
+        self._call("sid_build_decode_indices", req_to_token.data_ptr(), req_to_token.shape[1],
+                   req_to_token.shape[0], rows.data_ptr(),
+                   new_slots.data_ptr() if new_slots is not None else None,
+                   kv_indptr.data_ptr(), kv_indices.data_ptr(), rows.numel(), _stream(rows))

@@ -1,0 +1,118 @@
+"""Build and load the native HIP library (`libsid_hip.so`, the C-ABI in include/sid_hip.h).
+
+Mirrors the role of sid/kernels/jit.py:17-35 in the reference (`load_ext()` returns the
+module that carries `flash_decode_fwd` and `reshape_and_cache`), but the library is an
+ahead-of-time `hipcc --offload-arch=gfx950` build into the source tree, loaded with ctypes:
+no JIT cache, no pybind, no torch types across the boundary.
+
+`build_library()` always recompiles; `load_ext()` loads what is built and compiles only
+when no library exists yet. There is no fallback: without the library every op raises.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent.parent            # .../sid
+CSRC_DIR = PKG_DIR.parent / "csrc"                         # .../deterministic-inference_amd/csrc
+INCLUDE_DIR = PKG_DIR.parent.parent / "include"            # repo/include
+BUILD_DIR = PKG_DIR.parent / "_build"
+LIB_PATH = PKG_DIR / "libsid_hip.so"
+
+ARCH = "gfx950"
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-mcode-object-version=5",
+    # No packed-fp32 VALU instructions anywhere in this library.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+_ext = None
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: cannot build libsid_hip.so")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC_DIR.glob("*.hip"))
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libsid_hip.so (always rebuilds)."""
+    hipcc = _hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+
+    def compile_one(src: Path) -> Path:
+        obj = BUILD_DIR / (src.stem + ".o")
+        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr[-4000:]}")
+        if verbose:
+            print(f"[sid build] {src.name}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
+        objs = list(pool.map(compile_one, srcs))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link of libsid_hip.so failed:\n{res.stderr[-4000:]}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def load_ext():
+    """Return the native op module (a `sid.kernels._native.NativeLib`), building it if absent."""
+    global _ext
+    if _ext is not None:
+        return _ext
+    import torch  # noqa: F401  (torch's HIP runtime must be loaded before the library binds it)
+
+    from sid.kernels._native import NativeLib
+
+    if not LIB_PATH.exists():
+        build_library()
+    _ext = NativeLib(LIB_PATH)
+    return _ext
+
+
+def build_all() -> None:
+    """Build, load and run a one-request smoke decode on the GPU (sid/kernels/jit.py:38-63)."""
+    import torch
+
+    assert torch.cuda.is_available(), "a GPU is required to smoke-test the kernels"
+    ext = load_ext()
+    dev = "cuda"
+    num_kv, num_q, hd = 8, 16, 128
+    q = torch.randn(1, num_q, hd, device=dev, dtype=torch.bfloat16)
+    k_cache = torch.randn(8, num_kv, hd, device=dev, dtype=torch.bfloat16)
+    v_cache = torch.randn(8, num_kv, hd, device=dev, dtype=torch.bfloat16)
+    kv_indptr = torch.tensor([0, 4], device=dev, dtype=torch.int32)
+    kv_indices = torch.arange(1, 5, device=dev, dtype=torch.int32)
+    num_splits = torch.ones(1, device=dev, dtype=torch.int32)
+    part_o = torch.empty(1, num_q, 1, hd, device=dev, dtype=torch.float32)
+    part_lse = torch.empty(1, num_q, 1, device=dev, dtype=torch.float32)
+    o = torch.empty_like(q)
+    ext.flash_decode_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
+                         1, 0, hd ** -0.5, part_o, part_lse, o)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all(), "smoke decode produced non-finite output"
+
+
+if __name__ == "__main__":
+    build_library(verbose=True)
+    print(LIB_PATH)

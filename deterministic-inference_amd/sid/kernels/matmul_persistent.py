@@ -1,0 +1,50 @@
+"""Decode-step GEMMs on bf16 MFMA with a fixed, M-independent reduction order.
+
+`linear` replaces F.linear on the model path; `bi_linear` / `matmul_persistent` keep the
+names and signatures of sid/kernels/matmul_persistent.py:82-113. Every output element is
+reduced in the same order whatever M is (K in 256-wide chunks, chunk sums folded in
+increasing order), so `bi_linear` and `linear` are the same kernel: rows are bitwise
+batch-invariant in every mode, and the batch_invariant mode costs nothing extra here.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from sid.kernels.jit import load_ext
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+           out_fp32: bool = False) -> torch.Tensor:
+    """y = x @ weight^T (+ bias). x: [..., K] bf16, weight: [N, K] bf16 -> [..., N].
+
+    out_fp32=True returns fp32 holding the bf16-rounded result (F.linear(...).float())."""
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    n = weight.shape[0]
+    y = torch.empty(x2.shape[0], n, device=x.device,
+                    dtype=torch.float32 if out_fp32 else torch.bfloat16)
+    load_ext().linear(x2, weight, bias, y, out_fp32)
+    return y.view(*shape[:-1], n)
+
+
+def matmul_persistent(a: torch.Tensor, b: torch.Tensor,
+                      bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """C = A @ B (+ bias). A: [M, K], B: [K, N] (a transposed [N, K] view is used as is)."""
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    w = b.t()
+    if not w.is_contiguous():
+        w = w.contiguous()
+    return linear(a, w, bias)
+
+
+def bi_linear(x: torch.Tensor, weight: torch.Tensor,
+              bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Drop-in for F.linear(x, weight, bias) with batch-invariant reduction."""
+    return linear(x, weight, bias)

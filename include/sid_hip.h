@@ -1,0 +1,175 @@
+/*
+ * sid_hip.h — C-ABI of the MI355X (gfx950) decode hot path of sid.
+ *
+ * Every entry point takes raw device pointers, sizes and a hipStream_t passed
+ * as `void* stream` (NULL = the default stream), launches asynchronously on
+ * that stream, allocates nothing and returns SID_OK or an error code; the
+ * message for the last error on the calling thread is sid_last_error().
+ * bf16 tensors are passed as `void*` (raw 16-bit bf16 bits), row-major and
+ * contiguous. Shapes use the reference's names: B requests, T tokens,
+ * HQ = 16 query heads, HKV = 8 KV heads, D = 128 head dim, S pool slots.
+ *
+ * Reference interfaces replaced (paths relative to the sid repository):
+ *   sid/csrc/flash_decode.cu         pybind module `sid_flash_decode`
+ *   sid/kernels/extend_attention.py  Triton extend attention
+ *   sid/kernels/rmsnorm.py           Triton RMSNorm kernels
+ *   sid/kernels/rope.py              Triton RoPE kernel
+ *   sid/kernels/matmul_persistent.py Triton persistent GEMM / F.linear
+ *   sid/model/qwen3.py               torch glue (embedding, silu*up, row gather)
+ *   sid/engine/sampler.py            greedy argmax
+ */
+#ifndef SID_HIP_H_
+#define SID_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SID_OK 0
+#define SID_ERR_INVALID 1 /* bad argument: shape, size, null pointer */
+#define SID_ERR_LAUNCH 2  /* the HIP runtime rejected a launch */
+
+/* Message describing the last non-SID_OK return on this thread ("" if none). */
+const char* sid_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int sid_abi_version(void);
+
+/*
+ * Scatter new K/V rows into the paged KV pool: k_cache[slot[t]] = k[t],
+ * v_cache[slot[t]] = v[t]. k, v: bf16 [T, HKV, D]; k_cache, v_cache: bf16
+ * [S, HKV, D]; slot_mapping: int64 [T]. Slots < 0 are skipped (padding);
+ * slots >= S are skipped too, so a bad mapping cannot write out of bounds.
+ * Replaces reshape_and_cache, sid/csrc/flash_decode.cu:378-406 (kernel
+ * :275-296).
+ */
+int sid_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
+                          const int64_t* slot_mapping, int64_t num_tokens, int num_kv_heads,
+                          int head_dim, int64_t num_slots, void* stream);
+
+/*
+ * Split-KV paged decode attention (stage 1 partial softmax per KV split,
+ * stage 2 log-sum-exp merge in fixed split order). q, o: bf16 [B, HQ, D];
+ * k_cache, v_cache: bf16 [S, HKV, D]; kv_indptr int32 [B+1]; kv_indices int32
+ * [kv_indptr[B]] (pool slot of every position, in order); num_splits int32
+ * [B]; part_o fp32 [part_batch, HQ, part_stride, D]; part_lse fp32
+ * [part_batch, HQ, part_stride]. fixed_split_size > 0 gives fixed-size splits
+ * (batch-invariant mode), 0 the heuristic geometry
+ * ceil(ceil(len / n) / 32) * 32. Requires HQ == 2 * HKV, D == 128,
+ * part_batch >= B, part_stride >= max_splits >= 1. Slots outside [0, S) read
+ * slot 0. When max_splits == 1 the workspace is not touched.
+ * Replaces flash_decode_fwd, sid/csrc/flash_decode.cu:307-376.
+ */
+int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                         const int32_t* num_splits, int batch, int num_q_heads, int num_kv_heads,
+                         int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
+                         float sm_scale, float* part_o, float* part_lse, int part_batch,
+                         int part_stride, void* o, void* stream);
+
+/*
+ * Varlen causal attention over the paged pool (prefill, DVR verify). q, o:
+ * bf16 [Text, HQ, D]; qo_indptr, kv_indptr int32 [B+1] (kv = prefix +
+ * extend, all of it already in the pool); kv_indices int32. Query j of
+ * request b sits at absolute position prefix_b + j and sees keys
+ * 0 .. prefix_b + j. Key tiles are anchored at absolute position 0, so a
+ * query's result depends only on its absolute position and its sequence's
+ * keys (window-offset and batch-slot invariant, bit for bit).
+ * Replaces extend_attention_fwd, sid/kernels/extend_attention.py:115-144.
+ */
+int sid_extend_attention_fwd(const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* qo_indptr, const int32_t* kv_indptr,
+                             const int32_t* kv_indices, int batch, int64_t total_q,
+                             int num_q_heads, int num_kv_heads, int head_dim, int64_t num_slots,
+                             int max_extend_len, float sm_scale, void* o, void* stream);
+
+/*
+ * out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w, fp32 math, bf16 I/O.
+ * x, out: bf16 [rows, hidden]; w: bf16 [hidden]; hidden a multiple of 8,
+ * at most 8192. out may alias x.
+ * Replaces rmsnorm / qk_head_rmsnorm, sid/kernels/rmsnorm.py:45-55, 72-75.
+ */
+int sid_rmsnorm(const void* x, const void* w, void* out, int64_t rows, int hidden, float eps,
+                void* stream);
+
+/*
+ * In place: residual += x (stored as bf16); x = rmsnorm(residual) where the
+ * norm reads the fp32 sum before rounding. x, residual: bf16 [rows, hidden].
+ * Replaces fused_add_rmsnorm, sid/kernels/rmsnorm.py:58-69 (kernel :27-42).
+ */
+int sid_fused_add_rmsnorm(void* x, void* residual, const void* w, int64_t rows, int hidden,
+                          float eps, void* stream);
+
+/*
+ * NeoX rotate-half RoPE in place on q bf16 [T, HQ, D] and k bf16 [T, HKV, D]
+ * at positions int64 [T], using cos_sin fp32 [max_positions, D] =
+ * [cos(D/2) | sin(D/2)]. Tokens whose position is outside [0, max_positions)
+ * are left unchanged. Replaces RotaryEmbedding.apply, sid/kernels/rope.py:50-61
+ * (kernel :15-37).
+ */
+int sid_rope_apply(void* q, void* k, const int64_t* positions, const float* cos_sin,
+                   int64_t num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                   int64_t max_positions, void* stream);
+
+/*
+ * y = x @ w^T (+ bias). x: bf16 [M, K] with row stride ldx (elements);
+ * w: bf16 [N, K] contiguous (HF layout); bias: bf16 [N] or NULL; y: [M, N]
+ * contiguous, bf16 when out_fp32 == 0, else fp32 holding the bf16-rounded
+ * value (the reference's `linear(...).float()`). K must be a multiple of 256.
+ * The reduction order of every output element is fixed and independent of M
+ * (K in 256-wide chunks, each accumulated from zero in increasing k, chunk
+ * sums added in increasing chunk order), so each row is bitwise identical
+ * whatever batch it is computed in.
+ * Replaces F.linear / bi_linear / matmul_persistent at sid/model/qwen3.py:49,
+ * 80, 84, 86, 114 and sid/kernels/matmul_persistent.py:82-113.
+ */
+int sid_linear(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
+               int64_t n, int64_t k, int out_fp32, void* stream);
+
+/*
+ * out[t, i] = silu(gate[t, i]) * up[t, i] with gate = gate_up[t, :I] and
+ * up = gate_up[t, I:], each op rounded to bf16 like torch's
+ * `F.silu(gate) * up`. gate_up: bf16 [T, 2I]; out bf16 [T, I].
+ * Replaces sid/model/qwen3.py:84-85.
+ */
+int sid_silu_mul(const void* gate_up, void* out, int64_t num_tokens, int64_t inter, void* stream);
+
+/*
+ * out[i] = table[idx[i]] for bf16 rows of row_elems elements (row_elems a
+ * multiple of 8). Indices outside [0, table_rows) produce a zero row.
+ * Used for the embedding lookup (sid/model/qwen3.py:93) and the sampled-row
+ * gather (sid/model/qwen3.py:113).
+ */
+int sid_gather_rows(const void* table, const int64_t* idx, void* out, int64_t n,
+                    int64_t row_elems, int64_t table_rows, void* stream);
+
+/*
+ * out[r] = argmax(logits[r, :]) with first-index tie-break; fp32 logits
+ * [rows, cols] with row stride ld; out int64 [rows]. NaN compares greater
+ * than every number (torch.argmax semantics). Replaces the greedy branch of
+ * sample(), sid/engine/sampler.py:37.
+ */
+int sid_argmax_rows(const float* logits, int64_t ld, int64_t* out, int64_t rows, int64_t cols,
+                    void* stream);
+
+/*
+ * Device-side decode batch construction. For request b (row rows[b] of the
+ * int32 request->token table [num_rows, row_stride], L_b = kv_indptr[b+1] -
+ * kv_indptr[b] positions, the last one being decoded now): if new_slots
+ * (int64 [B]) is non-NULL, table[row][L_b - 1] = new_slots[b]; then
+ * kv_indices[kv_indptr[b] + i] = table[row][i] for i < L_b. Rows outside the
+ * table or L_b > row_stride are skipped. Replaces the per-request host loop of
+ * build_decode_batch, sid/engine/batch.py:120-133.
+ */
+int sid_build_decode_indices(int32_t* req_to_token, int64_t row_stride, int64_t num_rows,
+                             const int64_t* rows, const int64_t* new_slots,
+                             const int32_t* kv_indptr, int32_t* kv_indices, int batch,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SID_HIP_H_ */

@@ -1,0 +1,195 @@
+"""Split-KV decode attention (HIP) vs the fp32 CPU oracle, plus its bitwise invariants.
+
+Cases follow the reference's tests/test_02_flash_decode.py:61-118 (split boundaries
+31/32/33, 255/256/257, ragged batches, 5 split policies, shuffled slots), the BASELINE
+configs 1 and 2 (page_size-16 block tables over large pools), empty requests, and the
+determinism contract: fixed splits are run-to-run bitwise stable, fixed-256 results do
+not depend on the batch, and different split counts change low-order bits.
+Tolerance: max abs/rel error 2e-2 against fp32.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import HKV, HQ, D, SCALE, assert_close_bf16, decode_inputs
+from oracle.attention import decode_attention_ref, plan_fixed, plan_heuristic
+from oracle.cache import block_table_to_indices
+
+pytestmark = pytest.mark.gpu
+
+
+def _ext():
+    from sid.kernels.jit import load_ext
+    return load_ext()
+
+
+def _run(q, k, v, indptr, idx, num_splits, grid, fixed):
+    bs = q.shape[0]
+    ws = max(grid, 1)
+    part_o = torch.empty(bs, HQ, ws, D, device="cuda", dtype=torch.float32)
+    part_lse = torch.empty(bs, HQ, ws, device="cuda", dtype=torch.float32)
+    o = torch.empty_like(q)
+    ns = torch.tensor(num_splits, dtype=torch.int32, device="cuda")
+    _ext().flash_decode_fwd(q, k, v, indptr, idx, ns, grid, fixed, SCALE, part_o, part_lse, o)
+    return o
+
+
+def _policy(seq_lens, policy):
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    if policy == "heuristic":
+        ns, grid = plan_heuristic(seq_lens, cu, HKV, 32)
+        return ns, grid, 0
+    if policy == "fixed256":
+        ns, grid = plan_fixed(seq_lens)
+        return ns, grid, 256
+    s = int(policy.replace("splits", ""))
+    return [min(-(-x // 32), s) for x in seq_lens], s, 0
+
+
+CASES = [
+    [1], [31], [32], [33], [255], [256], [257], [300, 5], [1000, 32, 999], [100] * 8,
+    [17 * i + 1 for i in range(17)], [50] * 64, [5000],
+]
+
+
+@pytest.mark.parametrize("seq_lens", CASES, ids=lambda s: f"b{len(s)}_max{max(s)}")
+@pytest.mark.parametrize("policy", ["heuristic", "fixed256", "splits1", "splits8", "splits32"])
+def test_decode_vs_oracle(seq_lens, policy):
+    q, k, v, indptr, idx = decode_inputs(seq_lens)
+    ns, grid, fixed = _policy(seq_lens, policy)
+    out = _run(q, k, v, indptr, idx, ns, grid, fixed)
+    ref = decode_attention_ref(q, k, v, indptr, idx, SCALE)
+    assert_close_bf16(out, ref)
+
+
+def test_direct_single_split_equals_two_stage():
+    """Grid 1 writes o directly; a grid of 2 with every request on one split runs the
+    merge pass. Both must give the same bits (merge of one split is the identity)."""
+    lens = [37, 300, 1]
+    q, k, v, indptr, idx = decode_inputs(lens, seed=3)
+    a = _run(q, k, v, indptr, idx, [1, 1, 1], 1, 0)
+    b = _run(q, k, v, indptr, idx, [1, 1, 1], 2, 0)
+    assert torch.equal(a, b)
+
+
+def test_empty_request_gives_zeros():
+    q, k, v, indptr, idx = decode_inputs([5, 7], seed=4)
+    indptr = torch.tensor([0, 0, 7], dtype=torch.int32, device="cuda")
+    for grid in (1, 4):
+        out = _run(q, k, v, indptr, idx, [0, 1], grid, 0)
+        assert torch.count_nonzero(out[0]) == 0
+        ref = decode_attention_ref(q[1:], k, v, torch.tensor([0, 7]), idx.cpu(), SCALE)
+        assert_close_bf16(out[1:], ref)
+
+
+def test_fixed_splits_run_to_run_bitwise():
+    lens = [123, 456, 789, 7]
+    q, k, v, indptr, idx = decode_inputs(lens)
+    ns, grid = plan_fixed(lens)
+    a = _run(q, k, v, indptr, idx, ns, grid, 256)
+    for _ in range(3):
+        assert torch.equal(a, _run(q, k, v, indptr, idx, ns, grid, 256))
+
+
+def test_split_count_changes_bits():
+    q, k, v, indptr, idx = decode_inputs([4096])
+    outs = [_run(q, k, v, indptr, idx, [min(128, s)], s, 0) for s in (1, 3, 8, 32)]
+    for o in outs[1:]:
+        assert_close_bf16(o, outs[0].float(), atol=3e-2, rtol=3e-2)
+    assert any(not torch.equal(outs[0], o) for o in outs[1:])
+
+
+def test_fixed256_is_batch_invariant():
+    """A request's fixed-256 output is bitwise identical alone and inside other batches
+    (the grid size changes with the batch's max length; its result must not)."""
+    g = torch.Generator().manual_seed(9)
+    pool = 20000
+    k = torch.randn(pool, HKV, D, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(pool, HKV, D, generator=g).to(torch.bfloat16).cuda()
+    q0 = torch.randn(1, HQ, D, generator=g).to(torch.bfloat16).cuda()
+    idx0 = torch.randperm(pool - 1, generator=g)[:1500] + 1
+
+    def run(others):
+        qs, idxs, lens = [], [], []
+        for pos, L in enumerate(others):
+            if L is None:
+                qs.append(q0)
+                idxs.append(idx0)
+                lens.append(1500)
+            else:
+                qs.append(torch.randn(1, HQ, D, generator=g).to(torch.bfloat16).cuda())
+                idxs.append(torch.randint(1, pool, (L,), generator=g))
+                lens.append(L)
+        indptr = torch.zeros(len(lens) + 1, dtype=torch.int32)
+        indptr[1:] = torch.cumsum(torch.tensor(lens), 0)
+        ns, grid = plan_fixed(lens)
+        out = _run(torch.cat(qs), k, v, indptr.cuda(), torch.cat(idxs).to(torch.int32).cuda(),
+                   ns, grid, 256)
+        return out[others.index(None)]
+
+    base = run([None])
+    for comp in ([None, 100], [4000, None, 3], [7] * 15 + [None]):
+        assert torch.equal(base, run(comp))
+
+
+def _paged_case(num_pages, seq_lens, seed):
+    rng = np.random.default_rng(seed)
+    bs = len(seq_lens)
+    pages_needed = [-(-L // 16) for L in seq_lens]
+    perm = rng.permutation(num_pages)
+    tables, off = [], 0
+    for n in pages_needed:
+        tables.append(perm[off:off + n])
+        off += n
+    idx = np.concatenate([block_table_to_indices(t, L) for t, L in zip(tables, seq_lens)])
+    indptr = np.zeros(bs + 1, dtype=np.int64)
+    indptr[1:] = np.cumsum(seq_lens)
+    return torch.from_numpy(idx).cuda(), torch.from_numpy(indptr.astype(np.int32)).cuda()
+
+
+def test_config1_paged_single_request():
+    """q [1,16,128], ctx 1024, page 16, 256-page pool, randperm table."""
+    torch.manual_seed(1)
+    q = torch.randn(1, HQ, D, device="cuda").to(torch.bfloat16)
+    k = torch.randn(256 * 16, HKV, D, device="cuda").to(torch.bfloat16)
+    v = torch.randn(256 * 16, HKV, D, device="cuda").to(torch.bfloat16)
+    idx, indptr = _paged_case(256, [1024], seed=1)
+    ref = decode_attention_ref(q, k, v, indptr, idx, SCALE)
+    for policy in ("heuristic", "fixed256"):
+        ns, grid, fixed = _policy([1024], policy)
+        assert_close_bf16(_run(q, k, v, indptr, idx, ns, grid, fixed), ref)
+
+
+def test_config2_cache_write_then_decode():
+    """B=32, ctx ~ U[128, 4096], 32k-page x 16 pool, new K/V written by
+    reshape_and_cache (bit-exact) then attended with both split policies."""
+    rng = np.random.default_rng(2)
+    lens = rng.integers(128, 4097, size=32).tolist()
+    slots_total = 32768 * 16
+    torch.manual_seed(2)
+    k = torch.randn(slots_total, HKV, D, device="cuda").to(torch.bfloat16)
+    v = torch.randn(slots_total, HKV, D, device="cuda").to(torch.bfloat16)
+    q = torch.randn(32, HQ, D, device="cuda").to(torch.bfloat16)
+    idx, indptr = _paged_case(32768, lens, seed=2)
+    ends = indptr[1:].long() - 1
+    new_slots = idx[ends].long()
+    k_new = torch.randn(32, HKV, D, device="cuda").to(torch.bfloat16)
+    v_new = torch.randn(32, HKV, D, device="cuda").to(torch.bfloat16)
+    keep = torch.ones(idx.numel(), dtype=torch.bool, device="cuda")
+    keep[ends] = False
+    others = idx[keep].long()
+    before_k, before_v = k[others].clone(), v[others].clone()
+    _ext().reshape_and_cache(k_new, v_new, k, v, new_slots)
+    assert torch.equal(k[new_slots], k_new) and torch.equal(v[new_slots], v_new)
+    assert torch.equal(k[others], before_k) and torch.equal(v[others], before_v)
+    used = idx.long()
+    ref = decode_attention_ref(q.cpu(), k[used].cpu(), v[used].cpu(), indptr.cpu(),
+                               torch.arange(used.numel(), dtype=torch.int32), SCALE)
+    outs = {}
+    for policy in ("heuristic", "fixed256"):
+        ns, grid, fixed = _policy(lens, policy)
+        outs[policy] = _run(q, k, v, indptr, idx, ns, grid, fixed)
+        assert_close_bf16(outs[policy], ref)

@@ -1,0 +1,60 @@
+"""Decode-step GEMMs (HIP MFMA) vs fp32, and the M-invariance of every row (bitwise).
+Shapes: the reference's tests/test_10_batch_invariant.py:18-38 plus the Qwen3-0.6B decode
+(M=64) and verify (M=128) projections."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.gemm import linear_ref
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (1, 1024, 1024), (7, 3072, 1024), (128, 151936, 1024), (500, 1024, 3072),
+    (64, 4096, 1024), (64, 1024, 2048), (64, 6144, 1024), (64, 1024, 3072), (64, 151936, 1024),
+    (128, 6144, 1024), (33, 48, 256),
+])
+def test_linear_vs_fp32(m, n, k):
+    from sid.kernels.matmul_persistent import linear
+    torch.manual_seed(0)
+    x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(n, k, device="cuda") * 0.05).to(torch.bfloat16)
+    out = linear(x, w)
+    ref = linear_ref(x.cpu(), w.cpu())
+    torch.testing.assert_close(out.float().cpu(), ref, atol=3e-2, rtol=2e-2)
+
+
+def test_bias_and_fp32_output():
+    from sid.kernels.matmul_persistent import bi_linear, linear, matmul_persistent
+    torch.manual_seed(1)
+    x = torch.randn(9, 512, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(96, 512, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(96, device="cuda", dtype=torch.bfloat16)
+    y = bi_linear(x, w, b)
+    torch.testing.assert_close(y.float().cpu(), linear_ref(x.cpu(), w.cpu(), b.cpu()), atol=2e-1, rtol=2e-2)
+    y32 = linear(x, w, b, out_fp32=True)
+    assert y32.dtype == torch.float32 and torch.equal(y32.to(torch.bfloat16), y)
+    assert torch.equal(matmul_persistent(x, w.t(), b), y)
+
+
+def test_row_invariance():
+    from sid.kernels.matmul_persistent import bi_linear
+    torch.manual_seed(2)
+    x0 = torch.randn(1, 1024, device="cuda", dtype=torch.bfloat16)
+    for n in (3072, 151936):
+        w = (torch.randn(n, 1024, device="cuda") * 0.05).to(torch.bfloat16)
+        alone = bi_linear(x0, w)
+        for m in (2, 64, 65, 333):
+            x = torch.cat([torch.randn(m - 1, 1024, device="cuda", dtype=torch.bfloat16), x0])
+            assert torch.equal(alone[0], bi_linear(x, w)[-1]), (n, m)
+
+
+def test_strided_input_rows():
+    from sid.kernels.matmul_persistent import linear
+    torch.manual_seed(3)
+    big = torch.randn(16, 2048, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(64, 1024, device="cuda", dtype=torch.bfloat16)
+    assert torch.equal(linear(big[:, :1024], w), linear(big[:, :1024].contiguous(), w))
