@@ -26,14 +26,14 @@ _SIGNATURES = {
     "sid_rmsnorm": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
     "sid_fused_add_rmsnorm": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
     "sid_rope_apply": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _vp],
-    "sid_linear": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    "sid_linear": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
     "sid_silu_mul": [_vp, _vp, _i64, _i64, _vp],
     "sid_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
     "sid_build_decode_indices": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
 }
-EXPORTED = ("sid_last_error", "sid_abi_version", *_SIGNATURES)
-ABI_VERSION = 1
+EXPORTED = ("sid_last_error", "sid_abi_version", "sid_linear_workspace_bytes", *_SIGNATURES)
+ABI_VERSION = 2
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -62,6 +62,8 @@ class NativeLib:
         self.lib.sid_last_error.argtypes = []
         self.lib.sid_abi_version.restype = ctypes.c_int
         self.lib.sid_abi_version.argtypes = []
+        self.lib.sid_linear_workspace_bytes.restype = ctypes.c_int64
+        self.lib.sid_linear_workspace_bytes.argtypes = [_i64, _i64, _i64]
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.argtypes = argtypes
@@ -176,7 +178,10 @@ class NativeLib:
         self._call("sid_rope_apply", q.data_ptr(), k.data_ptr(), positions.data_ptr(),
                    cos_sin.data_ptr(), t, hq, k.shape[1], d, cos_sin.shape[0], _stream(q))
 
-    def linear(self, x, w, bias, y, out_fp32: bool) -> None:
+    def linear_workspace_bytes(self, m: int, n: int, k: int) -> int:
+        return int(self.lib.sid_linear_workspace_bytes(m, n, k))
+
+    def linear(self, x, w, bias, y, out_fp32: bool, workspace=None) -> None:
         _check(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1,
                "x must be a 2-D bf16 GPU tensor with unit column stride")
         _gpu(w, "weight", torch.bfloat16)
@@ -188,9 +193,13 @@ class NativeLib:
             _check(bias.numel() == n, "bias must have N entries")
         _gpu(y, "out", torch.float32 if out_fp32 else torch.bfloat16)
         _check(tuple(y.shape) == (m, n), "out must be [M, N]")
+        ws_ptr, ws_bytes = None, 0
+        if workspace is not None:
+            _gpu(workspace, "workspace", torch.uint8)
+            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel()
         self._call("sid_linear", x.data_ptr(), x.stride(0) if m > 1 else k, w.data_ptr(),
                    bias.data_ptr() if bias is not None else None, y.data_ptr(), m, n, k,
-                   1 if out_fp32 else 0, _stream(x))
+                   1 if out_fp32 else 0, ws_ptr, ws_bytes, _stream(x))
 
     def silu_mul(self, gate_up, out) -> None:
         _gpu(gate_up, "gate_up", torch.bfloat16)

@@ -117,16 +117,25 @@ int sid_rope_apply(void* q, void* k, const int64_t* positions, const float* cos_
  * y = x @ w^T (+ bias). x: bf16 [M, K] with row stride ldx (elements);
  * w: bf16 [N, K] contiguous (HF layout); bias: bf16 [N] or NULL; y: [M, N]
  * contiguous, bf16 when out_fp32 == 0, else fp32 holding the bf16-rounded
- * value (the reference's `linear(...).float()`). K must be a multiple of 256.
+ * value (the reference's `linear(...).float()`). K must be a multiple of 256,
+ * N a multiple of 64.
  * The reduction order of every output element is fixed and independent of M
  * (K in 256-wide chunks, each accumulated from zero in increasing k, chunk
  * sums added in increasing chunk order), so each row is bitwise identical
- * whatever batch it is computed in.
+ * whatever batch it is computed in, with or without a workspace.
+ * workspace: optional device buffer of workspace_bytes (256-byte aligned,
+ * zero-filled once before first use; the kernels leave it zeroed) that lets
+ * small-M GEMMs split K over more workgroups; see sid_linear_workspace_bytes.
+ * Calls sharing a workspace must be ordered on one stream.
  * Replaces F.linear / bi_linear / matmul_persistent at sid/model/qwen3.py:49,
  * 80, 84, 86, 114 and sid/kernels/matmul_persistent.py:82-113.
  */
 int sid_linear(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
-               int64_t n, int64_t k, int out_fp32, void* stream);
+               int64_t n, int64_t k, int out_fp32, void* workspace, int64_t workspace_bytes,
+               void* stream);
+
+/* Workspace bytes sid_linear uses for an (m, n, k) problem; 0 = it does not split. */
+int64_t sid_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
 /*
  * out[t, i] = silu(gate[t, i]) * up[t, i] with gate = gate_up[t, :I] and

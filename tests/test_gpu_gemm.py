@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("m,n,k", [
     (1, 1024, 1024), (7, 3072, 1024), (128, 151936, 1024), (500, 1024, 3072),
     (64, 4096, 1024), (64, 1024, 2048), (64, 6144, 1024), (64, 1024, 3072), (64, 151936, 1024),
-    (128, 6144, 1024), (33, 48, 256),
+    (128, 6144, 1024), (33, 64, 256), (200, 128, 512), (64, 2048, 1024),
 ])
 def test_linear_vs_fp32(m, n, k):
     from sid.kernels.matmul_persistent import linear
@@ -31,8 +31,8 @@ def test_bias_and_fp32_output():
     from sid.kernels.matmul_persistent import bi_linear, linear, matmul_persistent
     torch.manual_seed(1)
     x = torch.randn(9, 512, device="cuda", dtype=torch.bfloat16)
-    w = torch.randn(96, 512, device="cuda", dtype=torch.bfloat16)
-    b = torch.randn(96, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(128, 512, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(128, device="cuda", dtype=torch.bfloat16)
     y = bi_linear(x, w, b)
     torch.testing.assert_close(y.float().cpu(), linear_ref(x.cpu(), w.cpu(), b.cpu()), atol=2e-1, rtol=2e-2)
     y32 = linear(x, w, b, out_fp32=True)
@@ -58,3 +58,27 @@ def test_strided_input_rows():
     big = torch.randn(16, 2048, device="cuda", dtype=torch.bfloat16)
     w = torch.randn(64, 1024, device="cuda", dtype=torch.bfloat16)
     assert torch.equal(linear(big[:, :1024], w), linear(big[:, :1024].contiguous(), w))
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 4096, 1024), (64, 1024, 2048), (64, 6144, 1024),
+                                   (64, 1024, 3072), (5, 1024, 3072), (1, 4096, 1024)])
+def test_split_k_bitwise_equals_single_pass(m, n, k):
+    """Split mode (one K chunk per workgroup, last arrival folds) and the single-pass mode
+    produce identical bits; repeated calls reuse the self-resetting counters."""
+    from sid.kernels.jit import load_ext
+    ext = load_ext()
+    torch.manual_seed(4)
+    x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(n, k, device="cuda") * 0.05).to(torch.bfloat16)
+    b = torch.randn(n, device="cuda", dtype=torch.bfloat16)
+    need = ext.linear_workspace_bytes(m, n, k)
+    assert need > 0
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    ref = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ext.linear(x, w, b, ref, False, None)
+    for _ in range(3):
+        out = torch.empty_like(ref)
+        ext.linear(x, w, b, out, False, ws)
+        assert torch.equal(out, ref)
+    counters = ws[: ((n // 64) * 4 + 255) // 256 * 256]
+    assert torch.count_nonzero(counters) == 0
