@@ -41,6 +41,7 @@ def parse():
     ap.add_argument("--mode", default="nondet", choices=["nondet", "dvr", "batch_invariant"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--attn-reps", type=int, default=4)
+    ap.add_argument("--eager", action="store_true", help="no HIP graphs (launch every kernel)")
     return ap.parse_args()
 
 
@@ -48,7 +49,7 @@ class DecodeWorkload:
     """64 running requests with 2048-token prefixes whose KV is synthetic (N(0,1) bf16 in
     page-shuffled slots); each decode step feeds one token per request at position 2048."""
 
-    def __init__(self, batch, context, mode, seed=0):
+    def __init__(self, batch, context, mode, seed=0, graphs=True):
         import torch
         from sid.config import EngineConfig, Mode, SamplingParams
         from sid.engine.model_runner import ModelRunner
@@ -57,7 +58,8 @@ class DecodeWorkload:
         self.torch = torch
         pool = batch * (context + 16) + 4096
         self.cfg = EngineConfig(mode=Mode(mode), kv_pool_tokens=pool, max_reqs=batch + 2,
-                                max_seq_len=context + 64, max_decode_batch=batch, seed=seed)
+                                max_seq_len=context + 64, max_decode_batch=batch, seed=seed,
+                                use_graphs=graphs)
         self.runner = ModelRunner(self.cfg, "cuda")
         kv = self.kv = self.runner.kv_cache
         g = torch.Generator(device="cuda").manual_seed(seed + 1)
@@ -82,8 +84,7 @@ class DecodeWorkload:
         self.invariant = self.cfg.mode == Mode.BATCH_INVARIANT
 
     def build(self):
-        from sid.engine.batch import build_decode_batch
-        return build_decode_batch(self.reqs, self.kv, "cuda", self.invariant)
+        return self.runner.prepare_decode(self.reqs, self.invariant)
 
     def step(self):
         fb = self.build()
@@ -200,7 +201,7 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    wl = DecodeWorkload(args.batch, args.context, args.mode)
+    wl = DecodeWorkload(args.batch, args.context, args.mode, graphs=not args.eager)
     sec = time_steps(wl, args.steps, args.warmup)
     roof = attention_roofline(wl, args.attn_reps)
     base = None if args.no_cpu_baseline else cpu_baseline(wl)
@@ -212,7 +213,8 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: random-init weights ~N(0,0.02), random token ids, N(0,1) KV prefixes",
         "config": {"workload": f"Qwen3-0.6B-shape decode step, batch {b}, context "
-                               f"{args.context}+1, greedy, {args.mode} split policy",
+                               f"{args.context}+1, greedy, {args.mode} split policy, "
+                               f"{'eager launches' if args.eager else 'HIP graph replay'}",
                    "batch": b, "context": args.context, "layers": wl.runner.mcfg.num_layers,
                    "mode": args.mode},
         "roofline": roof,

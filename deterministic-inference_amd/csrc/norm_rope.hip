@@ -1,23 +1,23 @@
-// Row-wise elementwise kernels of the decode step: RMSNorm (plain and fused
-// with the residual add), NeoX RoPE and the SwiGLU gate. All are tiny and
-// bandwidth/launch bound; what matters is a fixed in-row reduction order
-// (every row is reduced by the same lane pattern, so results are independent
-// of the row's index and of how many rows are processed together).
+// Row-wise kernels of the decode step: RMSNorm (plain and fused with the
+// residual add), NeoX RoPE, SwiGLU, and the fused QKV epilogue (q/k-norm +
+// RoPE + KV-cache write). They are launch/bandwidth bound; what matters is a
+// fixed in-row reduction order (every row is reduced by the same lane
+// pattern, so results do not depend on the row's index or on how many rows
+// are processed together).
+//
+// Inputs that come straight out of a projection can be given either as the
+// bf16 matrix or as the GEMM's fp32 chunk partials (sid_linear_partials); in
+// the latter case the chunks are folded here in increasing chunk order and
+// rounded to bf16, which is exactly sid_linear's result, so the fused kernels
+// are bit-identical to "sid_linear, then the op". All arithmetic that two
+// kernels share goes through the same helpers with explicit fmaf, so the
+// fused and unfused paths also agree bit for bit after the first rounding.
 #include "common.h"
 
 #include <cmath>
 
 namespace sid {
 namespace {
-
-// A row is processed by LPR consecutive lanes (LPR a power of two <= 64);
-// lane j of the row owns 16-byte vectors j, j + LPR, j + 2*LPR, ...
-// Sum of squares: lane-local sequential sum, then an xor butterfly across
-// the LPR lanes; every lane of the row ends with identical bits.
-__device__ __forceinline__ float row_sum(float v, int lpr) {
-  for (int mask = 1; mask < lpr; mask <<= 1) v += lane_xor(v, mask);
-  return v;
-}
 
 __device__ __forceinline__ void load8(const uint4& u, float (&f)[8]) {
   f[0] = bf16_lo(u.x); f[1] = bf16_hi(u.x);
@@ -31,23 +31,88 @@ __device__ __forceinline__ uint4 store8(const float (&f)[8]) {
                     pack_bf16x2(f[6], f[7]));
 }
 
-// Up to MAXV vectors per lane are kept in registers between the two passes.
-constexpr int MAXV = 16;
+// An activation row: a bf16 matrix [rows, ld], or GEMM chunk partials
+// fp32 [nchunks][rows][ld] folded in chunk order and rounded to bf16.
+struct RowSrc {
+  const bf16_t* bf;
+  const float* part;
+  int64_t ld;
+  int64_t chunk_stride;
+  int nchunks;
+};
+
+__device__ __forceinline__ void load8_src(const RowSrc& s, int64_t row, int64_t col, float (&f)[8]) {
+  if (s.part == nullptr) {
+    load8(*reinterpret_cast<const uint4*>(s.bf + row * s.ld + col), f);
+    return;
+  }
+  const float* p = s.part + row * s.ld + col;
+  float4 a = *reinterpret_cast<const float4*>(p);
+  float4 b = *reinterpret_cast<const float4*>(p + 4);
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  for (int c = 1; c < s.nchunks; ++c) {
+    p += s.chunk_stride;
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+    f[0] += a.x; f[1] += a.y; f[2] += a.z; f[3] += a.w;
+    f[4] += b.x; f[5] += b.y; f[6] += b.z; f[7] += b.w;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = round_bf16(f[e]);
+}
+
+// ---- shared arithmetic --------------------------------------------------------------
+
+__device__ __forceinline__ float sumsq8(const float (&v)[8], float acc) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = fmaf(v[e], v[e], acc);
+  return acc;
+}
+
+// Xor butterfly over an aligned group of `lpr` lanes (identical bits in every lane).
+__device__ __forceinline__ float group_sum(float v, int lpr) {
+  for (int mask = 1; mask < lpr; mask <<= 1) v += lane_xor(v, mask);
+  return v;
+}
+
+__device__ __forceinline__ float rms_rstd(float sumsq, int hidden, float eps) {
+  return 1.0f / sqrtf(sumsq / static_cast<float>(hidden) + eps);
+}
+
+__device__ __forceinline__ void rms_apply8(const float (&v)[8], float rstd, const float (&w)[8],
+                                           float (&y)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = (v[e] * rstd) * w[e];
+}
+
+// NeoX rotate-half on one (x1, x2) = (x[i], x[i + D/2]) pair.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float& o1, float& o2) {
+  o1 = fmaf(x1, c, -(x2 * s));
+  o2 = fmaf(x2, c, x1 * s);
+}
+
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+  const float s = round_bf16(g / (1.0f + __expf(-g)));
+  return s * u;
+}
+
+// ---- RMSNorm ----------------------------------------------------------------------------
+
+constexpr int MAXV = 16;  // vectors per lane kept in registers between the two passes
 
 // FUSED = false: out = rmsnorm(x) * w.
-// FUSED = true:  r = x + residual (fp32); residual = bf16(r); x = rmsnorm(r) * w.
+// FUSED = true:  r = residual + x (fp32); residual = bf16(r); out = rmsnorm(r) * w.
 template <bool FUSED>
-__global__ void __launch_bounds__(256) rmsnorm_kernel(uint4* __restrict__ x,
-                                                      uint4* __restrict__ residual,
+__global__ void __launch_bounds__(256) rmsnorm_kernel(RowSrc xs, uint4* __restrict__ residual,
                                                       const uint4* __restrict__ w,
                                                       uint4* __restrict__ out, int64_t rows,
                                                       int hidden, int lpr, float eps) {
   const int tid = threadIdx.x;
-  const int rows_per_block = 256 / lpr;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_block + tid / lpr;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / lpr) + tid / lpr;
   const int j = tid % lpr;
   const int nvec = hidden / 8;
-  const int per_lane = nvec / lpr;  // host guarantees nvec % lpr == 0 and per_lane <= MAXV
+  const int per_lane = nvec / lpr;  // the host guarantees nvec % lpr == 0, per_lane <= MAXV
   const bool active = row < rows;
   const int64_t base = row * nvec;
 
@@ -57,7 +122,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(uint4* __restrict__ x,
   for (int i = 0; i < MAXV; ++i) {
     if (i < per_lane && active) {
       const int c = j + i * lpr;
-      load8(x[base + c], v[i]);
+      load8_src(xs, row, static_cast<int64_t>(c) * 8, v[i]);
       if constexpr (FUSED) {
         float r[8];
         load8(residual[base + c], r);
@@ -65,26 +130,21 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(uint4* __restrict__ x,
         for (int e = 0; e < 8; ++e) v[i][e] = r[e] + v[i][e];
         residual[base + c] = store8(v[i]);
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+      ss = sumsq8(v[i], ss);
     }
   }
-  // Rows of a block are whole lane groups, so the butterfly never mixes rows;
-  // inactive lanes contribute zeros to their own (discarded) row.
-  ss = row_sum(ss, lpr);
-  const float rstd = 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
+  // Rows of a block are whole lane groups: the butterfly never mixes rows.
+  ss = group_sum(ss, lpr);
+  const float rstd = rms_rstd(ss, hidden, eps);
   if (!active) return;
-  uint4* dst = FUSED ? x : out;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     if (i < per_lane) {
       const int c = j + i * lpr;
-      float wf[8];
+      float wf[8], y[8];
       load8(w[c], wf);
-      float y[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = v[i][e] * rstd * wf[e];
-      dst[base + c] = store8(y);
+      rms_apply8(v[i], rstd, wf, y);
+      out[base + c] = store8(y);
     }
   }
 }
@@ -96,6 +156,8 @@ int pick_lpr(int hidden) {
   while (lpr > nvec) lpr >>= 1;
   return lpr;
 }
+
+// ---- RoPE -----------------------------------------------------------------------------
 
 // One block per token; thread -> (head, pair of rotary indices).
 __global__ void __launch_bounds__(256) rope_kernel(uint32_t* __restrict__ q, uint32_t* __restrict__ k,
@@ -118,32 +180,102 @@ __global__ void __launch_bounds__(256) rope_kernel(uint32_t* __restrict__ q, uin
                          : k + (t * num_kv_heads + (head - num_q_heads)) * (head_dim / 2);
     const uint32_t a = base[i];
     const uint32_t b = base[pairs + i];
-    const float c0 = cs[2 * i], c1 = cs[2 * i + 1];
-    const float s0 = cs[half + 2 * i], s1 = cs[half + 2 * i + 1];
-    const float x1a = bf16_lo(a), x1b = bf16_hi(a);
-    const float x2a = bf16_lo(b), x2b = bf16_hi(b);
-    base[i] = pack_bf16x2(x1a * c0 - x2a * s0, x1b * c1 - x2b * s1);
-    base[pairs + i] = pack_bf16x2(x2a * c0 + x1a * s0, x2b * c1 + x1b * s1);
+    float o1a, o2a, o1b, o2b;
+    rope_pair(bf16_lo(a), bf16_lo(b), cs[2 * i], cs[half + 2 * i], o1a, o2a);
+    rope_pair(bf16_hi(a), bf16_hi(b), cs[2 * i + 1], cs[half + 2 * i + 1], o1b, o2b);
+    base[i] = pack_bf16x2(o1a, o1b);
+    base[pairs + i] = pack_bf16x2(o2a, o2b);
   }
 }
 
+// ---- SwiGLU -------------------------------------------------------------------------------
+
 // out = bf16(bf16(silu(gate)) * up), 8 elements per thread.
-__global__ void __launch_bounds__(256) silu_mul_kernel(const uint4* __restrict__ gate_up,
-                                                       uint4* __restrict__ out, int64_t rows,
-                                                       int64_t inter_vec) {
+__global__ void __launch_bounds__(256) silu_mul_kernel(RowSrc gu, uint4* __restrict__ out,
+                                                       int64_t rows, int64_t inter_vec) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= rows * inter_vec) return;
   const int64_t r = i / inter_vec;
   const int64_t c = i % inter_vec;
   float g[8], u[8], y[8];
-  load8(gate_up[r * 2 * inter_vec + c], g);
-  load8(gate_up[r * 2 * inter_vec + inter_vec + c], u);
+  load8_src(gu, r, c * 8, g);
+  load8_src(gu, r, (inter_vec + c) * 8, u);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float s = round_bf16(g[e] / (1.0f + __expf(-g[e])));
-    y[e] = s * u[e];
-  }
+  for (int e = 0; e < 8; ++e) y[e] = silu_mul1(g[e], u[e]);
   out[i] = store8(y);
+}
+
+// ---- fused QKV epilogue -------------------------------------------------------------------
+
+// Row t of the projection is [q (HQ*128) | k (HKV*128) | v (HKV*128)]. A head is
+// handled by 16 lanes (lane j: dims 8j..8j+7, which is rmsnorm_kernel's layout for
+// hidden 128), 16 heads per block. q/k heads: per-head RMSNorm, round, RoPE (the
+// rotate-half partner of lane j is lane j ^ 8, one DPP row_ror:8 away), round;
+// v heads: copied. q goes to q_out [T, HQ, 128]; k and v to the pools at slots[t].
+constexpr int QD = 128;
+
+__global__ void __launch_bounds__(256) qkv_post_kernel(
+    RowSrc src, int num_q_heads, int num_kv_heads, const uint4* __restrict__ q_norm,
+    const uint4* __restrict__ k_norm, float eps, const int64_t* __restrict__ positions,
+    const float* __restrict__ cos_sin, int64_t max_positions, const int64_t* __restrict__ slots,
+    uint4* __restrict__ q_out, uint4* __restrict__ k_cache, uint4* __restrict__ v_cache,
+    int64_t num_slots) {
+  const int64_t t = blockIdx.x;
+  const int head = blockIdx.y * 16 + (threadIdx.x >> 4);
+  const int j = threadIdx.x & 15;
+  const int heads = num_q_heads + 2 * num_kv_heads;
+  // Whole 16-lane groups are uniform; the DPP/bpermute below needs every lane of a
+  // row active, so out-of-range heads compute on clamped data and skip the stores.
+  const bool valid = head < heads;
+  const int hh = valid ? head : heads - 1;
+  float v[8];
+  load8_src(src, t, static_cast<int64_t>(hh) * QD + 8 * j, v);
+
+  const bool is_v = hh >= num_q_heads + num_kv_heads;
+  const int64_t slot = slots[t];
+  const bool slot_ok = slot >= 0 && slot < num_slots;
+  const int kv_row = 16 * num_kv_heads;  // uint4 per pool row
+  if (is_v) {
+    if (valid && slot_ok)
+      v_cache[slot * kv_row + (hh - num_q_heads - num_kv_heads) * 16 + j] = store8(v);
+    return;  // v heads occupy whole blocks' tail groups; no cross-lane op follows for them
+  }
+  const bool is_q = hh < num_q_heads;
+  float wf[8], y[8];
+  load8((is_q ? q_norm : k_norm)[j], wf);
+  const float ss = group_sum(sumsq8(v, 0.0f), 16);
+  rms_apply8(v, rms_rstd(ss, QD, eps), wf, y);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = round_bf16(y[e]);
+
+  const int64_t pos = positions[t];
+  float o[8];
+  if (pos >= 0 && pos < max_positions) {
+    const float* cs = cos_sin + pos * QD;
+    const int ri = 8 * (j & 7);  // rotary index of this lane's first element
+    const bool first_half = j < 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float partner = dpp<DPP_ROW_ROR8>(y[e]);
+      float o1, o2;
+      if (first_half) {
+        rope_pair(y[e], partner, cs[ri + e], cs[QD / 2 + ri + e], o1, o2);
+        o[e] = o1;
+      } else {
+        rope_pair(partner, y[e], cs[ri + e], cs[QD / 2 + ri + e], o1, o2);
+        o[e] = o2;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = y[e];
+  }
+  if (!valid) return;
+  if (is_q) {
+    q_out[(t * num_q_heads + hh) * 16 + j] = store8(o);
+  } else if (slot_ok) {
+    k_cache[slot * kv_row + (hh - num_q_heads) * 16 + j] = store8(o);
+  }
 }
 
 }  // namespace
@@ -151,11 +283,11 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const uint4* __restrict__
 
 using namespace sid;
 
-static int launch_rmsnorm(bool fused, void* x, void* residual, const void* w, void* out,
+static int launch_rmsnorm(bool fused, RowSrc xs, void* residual, const void* w, void* out,
                           int64_t rows, int hidden, float eps, void* stream, const char* name) {
   SID_REQUIRE(rows >= 0, "%s: negative rows", name);
   if (rows == 0) return SID_OK;
-  SID_REQUIRE(x && w && (fused ? residual != nullptr : out != nullptr), "%s: null pointer", name);
+  SID_REQUIRE((xs.bf || xs.part) && w && out && (!fused || residual), "%s: null pointer", name);
   SID_REQUIRE(hidden >= 8 && hidden % 8 == 0, "%s: hidden %d must be a positive multiple of 8",
               name, hidden);
   const int lpr = pick_lpr(hidden);
@@ -166,25 +298,39 @@ static int launch_rmsnorm(bool fused, void* x, void* residual, const void* w, vo
   SID_REQUIRE(blocks < (1ll << 31), "%s: too many rows", name);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (fused) {
-    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, (uint4*)x,
-                       (uint4*)residual, (const uint4*)w, nullptr, rows, hidden, lpr, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, xs,
+                       (uint4*)residual, (const uint4*)w, (uint4*)out, rows, hidden, lpr, eps);
   } else {
-    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, (uint4*)x,
+    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, xs,
                        nullptr, (const uint4*)w, (uint4*)out, rows, hidden, lpr, eps);
   }
   return check_launch(name);
 }
 
+static RowSrc bf_src(const void* x, int64_t ld) { return RowSrc{(const bf16_t*)x, nullptr, ld, 0, 0}; }
+
+static RowSrc part_src(const float* p, int nchunks, int64_t rows, int64_t ld) {
+  return RowSrc{nullptr, p, ld, rows * ld, nchunks};
+}
+
 extern "C" int sid_rmsnorm(const void* x, const void* w, void* out, int64_t rows, int hidden,
                            float eps, void* stream) {
-  return launch_rmsnorm(false, const_cast<void*>(x), nullptr, w, out, rows, hidden, eps, stream,
+  return launch_rmsnorm(false, bf_src(x, hidden), nullptr, w, out, rows, hidden, eps, stream,
                         "rmsnorm");
 }
 
 extern "C" int sid_fused_add_rmsnorm(void* x, void* residual, const void* w, int64_t rows,
                                      int hidden, float eps, void* stream) {
-  return launch_rmsnorm(true, x, residual, w, nullptr, rows, hidden, eps, stream,
+  return launch_rmsnorm(true, bf_src(x, hidden), residual, w, x, rows, hidden, eps, stream,
                         "fused_add_rmsnorm");
+}
+
+extern "C" int sid_fused_add_rmsnorm_partials(const float* partials, int nchunks, void* residual,
+                                              const void* w, void* out, int64_t rows, int hidden,
+                                              float eps, void* stream) {
+  SID_REQUIRE(nchunks >= 1, "fused_add_rmsnorm_partials: nchunks must be >= 1");
+  return launch_rmsnorm(true, part_src(partials, nchunks, rows, hidden), residual, w, out, rows,
+                        hidden, eps, stream, "fused_add_rmsnorm_partials");
 }
 
 extern "C" int sid_rope_apply(void* q, void* k, const int64_t* positions, const float* cos_sin,
@@ -203,17 +349,56 @@ extern "C" int sid_rope_apply(void* q, void* k, const int64_t* positions, const 
   return check_launch("rope");
 }
 
-extern "C" int sid_silu_mul(const void* gate_up, void* out, int64_t num_tokens, int64_t inter,
-                            void* stream) {
-  SID_REQUIRE(num_tokens >= 0, "silu_mul: negative token count");
+static int launch_silu(RowSrc gu, void* out, int64_t num_tokens, int64_t inter, void* stream,
+                       const char* name) {
+  SID_REQUIRE(num_tokens >= 0, "%s: negative token count", name);
   if (num_tokens == 0) return SID_OK;
-  SID_REQUIRE(gate_up && out, "silu_mul: null pointer");
-  SID_REQUIRE(inter > 0 && inter % 8 == 0, "silu_mul: intermediate size must be a multiple of 8");
+  SID_REQUIRE((gu.bf || gu.part) && out, "%s: null pointer", name);
+  SID_REQUIRE(inter > 0 && inter % 8 == 0, "%s: intermediate size must be a multiple of 8", name);
   const int64_t total = num_tokens * (inter / 8);
   const int64_t blocks = (total + 255) / 256;
-  SID_REQUIRE(blocks < (1ll << 31), "silu_mul: too many elements");
+  SID_REQUIRE(blocks < (1ll << 31), "%s: too many elements", name);
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), (const uint4*)gate_up, (uint4*)out,
-                     num_tokens, inter / 8);
-  return check_launch("silu_mul");
+                     static_cast<hipStream_t>(stream), gu, (uint4*)out, num_tokens, inter / 8);
+  return check_launch(name);
+}
+
+extern "C" int sid_silu_mul(const void* gate_up, void* out, int64_t num_tokens, int64_t inter,
+                            void* stream) {
+  return launch_silu(bf_src(gate_up, 2 * inter), out, num_tokens, inter, stream, "silu_mul");
+}
+
+extern "C" int sid_silu_mul_partials(const float* partials, int nchunks, void* out,
+                                     int64_t num_tokens, int64_t inter, void* stream) {
+  SID_REQUIRE(nchunks >= 1, "silu_mul_partials: nchunks must be >= 1");
+  return launch_silu(part_src(partials, nchunks, num_tokens, 2 * inter), out, num_tokens, inter,
+                     stream, "silu_mul_partials");
+}
+
+extern "C" int sid_qkv_post(const void* qkv, const float* partials, int nchunks,
+                            int64_t num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                            const void* q_norm, const void* k_norm, float eps,
+                            const int64_t* positions, const float* cos_sin,
+                            int64_t max_positions, const int64_t* slots, void* q_out,
+                            void* k_cache, void* v_cache, int64_t num_slots, void* stream) {
+  SID_REQUIRE(num_tokens >= 0, "qkv_post: negative token count");
+  if (num_tokens == 0) return SID_OK;
+  SID_REQUIRE((qkv != nullptr) != (partials != nullptr),
+              "qkv_post: exactly one of qkv and partials must be given");
+  SID_REQUIRE(partials == nullptr || nchunks >= 1, "qkv_post: nchunks must be >= 1");
+  SID_REQUIRE(head_dim == QD, "qkv_post: head_dim must be %d, got %d", QD, head_dim);
+  SID_REQUIRE(num_q_heads > 0 && num_kv_heads > 0, "qkv_post: bad head counts");
+  SID_REQUIRE(q_norm && k_norm && positions && cos_sin && slots && q_out && k_cache && v_cache,
+              "qkv_post: null pointer");
+  SID_REQUIRE(num_slots > 0, "qkv_post: empty KV pool");
+  SID_REQUIRE(num_tokens < (1ll << 31), "qkv_post: too many tokens");
+  const int64_t ld = static_cast<int64_t>(num_q_heads + 2 * num_kv_heads) * QD;
+  const RowSrc src = partials ? part_src(partials, nchunks, num_tokens, ld) : bf_src(qkv, ld);
+  const int heads = num_q_heads + 2 * num_kv_heads;
+  const dim3 grid((unsigned)num_tokens, (unsigned)ceil_div(heads, 16));
+  hipLaunchKernelGGL(qkv_post_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), src,
+                     num_q_heads, num_kv_heads, (const uint4*)q_norm, (const uint4*)k_norm, eps,
+                     positions, cos_sin, max_positions, slots, (uint4*)q_out, (uint4*)k_cache,
+                     (uint4*)v_cache, num_slots);
+  return check_launch("qkv_post");
 }

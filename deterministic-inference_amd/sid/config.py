@@ -73,6 +73,7 @@ class EngineConfig:
     invariant_split_size: int = 256
 
     decode_backend: str = "hip"  # "hip" split-KV kernel | "extend" (extend kernel, debugging)
+    use_graphs: bool = True  # replay decode / verify forwards as HIP graphs
 
     device: str = "cuda"
     seed: int = 0  # random-init weight seed

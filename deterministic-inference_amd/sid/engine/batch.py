@@ -48,6 +48,26 @@ class ForwardBatch:
     seeds: Optional[torch.Tensor] = None             # int64 [R]
     invariant: bool = False
     all_greedy: Optional[bool] = None  # host-known: every row has temperature 0
+    graph_key: Optional[tuple] = None  # set when the inputs live in graph-static buffers
+
+
+class DecodeStatic:
+    """Fixed-address device buffers for decode batches of up to max_bs requests, shared by
+    every captured decode graph (replays are ordered on one stream). Host staging is pinned
+    so the three per-step host->device copies are asynchronous; a staging buffer is reused
+    only after the event of its previous copy has completed."""
+
+    def __init__(self, max_bs: int, kv_capacity: int, device):
+        self.max_bs = max_bs
+        self.i64 = torch.zeros(7, max_bs, dtype=torch.int64, device=device)
+        self.i32 = torch.zeros(2 * max_bs + 1, dtype=torch.int32, device=device)
+        self.f32 = torch.zeros(2, max_bs, dtype=torch.float32, device=device)
+        self.kv_indices = torch.zeros(kv_capacity, dtype=torch.int32, device=device)
+        self.h64 = torch.zeros(7, max_bs, dtype=torch.int64, pin_memory=True)
+        self.h32 = torch.zeros(2 * max_bs + 1, dtype=torch.int32, pin_memory=True)
+        self.hf32 = torch.zeros(2, max_bs, dtype=torch.float32, pin_memory=True)
+        self.copied = torch.cuda.Event()
+        self.copied.record()
 
 
 def _sampling_host(reqs, repeat: int = 1):
@@ -99,9 +119,10 @@ def build_prefill_batch(reqs: list, kv, device: str, invariant: bool) -> Forward
     )
 
 
-def build_decode_batch(reqs: list, kv, device: str, invariant: bool) -> ForwardBatch:
+def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
+                       static: Optional[DecodeStatic] = None) -> ForwardBatch:
     """One new token per request; attention covers the full sequence including the
-    position being written now."""
+    position being written now. With `static`, the batch lives in its fixed buffers."""
     bs = len(reqs)
     pos = np.fromiter((r.prompt_len + r.num_output - 1 for r in reqs), dtype=np.int64, count=bs)
     for r, p in zip(reqs, pos.tolist()):
@@ -115,11 +136,34 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool) -> ForwardB
     indptr = np.zeros(bs + 1, dtype=np.int64)
     np.cumsum(seq_lens, out=indptr[1:])
     temps, top_ks, top_ps, seeds = _sampling_host(reqs)
-    d_ids, d_pos, d_rows, d_slots, d_spos, d_topk, d_seed = _to_device(
-        [ids, pos, rows, new_slots, pos + 1, top_ks, seeds], np.int64, device)
-    d_indptr, d_lens = _to_device([indptr, seq_lens], np.int32, device)
-    d_temps, d_topp = _to_device([temps, top_ps], np.float32, device)
-    kv_indices = torch.empty(int(indptr[-1]), dtype=torch.int32, device=device)
+    total = int(indptr[-1])
+    if static is None:
+        d_ids, d_pos, d_rows, d_slots, d_spos, d_topk, d_seed = _to_device(
+            [ids, pos, rows, new_slots, pos + 1, top_ks, seeds], np.int64, device)
+        d_indptr, d_lens = _to_device([indptr, seq_lens], np.int32, device)
+        d_temps, d_topp = _to_device([temps, top_ps], np.float32, device)
+        kv_indices = torch.empty(total, dtype=torch.int32, device=device)
+    else:
+        assert bs <= static.max_bs and total <= static.kv_indices.numel()
+        mb = static.max_bs
+        static.copied.synchronize()
+        h64 = static.h64.numpy()
+        for i, a in enumerate((ids, pos, rows, new_slots, pos + 1, top_ks, seeds)):
+            h64[i, :bs] = a
+        h32 = static.h32.numpy()
+        h32[:bs + 1] = indptr
+        h32[mb + 1:mb + 1 + bs] = seq_lens
+        hf = static.hf32.numpy()
+        hf[0, :bs] = temps
+        hf[1, :bs] = top_ps
+        static.i64.copy_(static.h64, non_blocking=True)
+        static.i32.copy_(static.h32, non_blocking=True)
+        static.f32.copy_(static.hf32, non_blocking=True)
+        static.copied.record()
+        d_ids, d_pos, d_rows, d_slots, d_spos, d_topk, d_seed = (static.i64[i, :bs] for i in range(7))
+        d_indptr, d_lens = static.i32[:bs + 1], static.i32[mb + 1:mb + 1 + bs]
+        d_temps, d_topp = static.f32[0, :bs], static.f32[1, :bs]
+        kv_indices = static.kv_indices[:total]
     load_ext().build_decode_indices(kv.req_to_token_gpu, d_rows, d_slots, d_indptr, kv_indices)
     return ForwardBatch(
         mode=ForwardMode.DECODE, input_ids=d_ids, positions=d_pos, out_slots=d_slots,

@@ -8,11 +8,12 @@ change bits between runs of the same shape.
 from __future__ import annotations
 
 import logging
+from collections import OrderedDict
 
 import torch
 
 from sid.config import EngineConfig, Mode, ModelConfig
-from sid.engine.batch import ForwardBatch
+from sid.engine.batch import DecodeStatic, ForwardBatch, ForwardMode, build_decode_batch
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
 from sid.kernels.decode_attention import DecodeAttention
@@ -55,6 +56,7 @@ class ModelRunner:
             max_seq_len=cfg.max_seq_len, device=device)
         self.verify_buffers = self._alloc_verify_buffers(cfg, device) \
             if cfg.mode == Mode.DVR else None
+        self.graphs = GraphCache(self) if cfg.use_graphs else None
 
     @staticmethod
     def _alloc_verify_buffers(cfg: EngineConfig, device: str) -> dict:
@@ -75,9 +77,77 @@ class ModelRunner:
         }
 
     def forward(self, fb: ForwardBatch) -> torch.Tensor:
+        if self.graphs is not None and fb.graph_key is not None:
+            return self.graphs.run(fb)
+        return self._forward_eager(fb)
+
+    def _forward_eager(self, fb: ForwardBatch) -> torch.Tensor:
         return self.model.forward(fb, self.kv_cache, self.decode_attn,
                                   decode_backend=self.cfg.decode_backend)
+
+    def prepare_decode(self, reqs: list, invariant: bool) -> ForwardBatch:
+        """build_decode_batch, into the graph-static buffers when graphs are enabled."""
+        if self.graphs is None:
+            return build_decode_batch(reqs, self.kv_cache, self.device, invariant)
+        fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant,
+                                static=self.graphs.decode_static)
+        bucket = 0
+        if invariant:  # the fixed-256 grid depends on the longest request; bucket it
+            bucket = 256
+            while bucket < fb.max_seq_len:
+                bucket *= 2
+            fb.max_seq_len = bucket
+        fb.graph_key = ("decode", len(reqs), invariant, bucket)
+        return fb
+
+    def tag_verify(self, fb: ForwardBatch) -> ForwardBatch:
+        """Verify batches always live in the persistent verify buffers: graph them."""
+        if self.graphs is not None:
+            fb.graph_key = ("verify",)
+        return fb
 
     def sample(self, fb: ForwardBatch, logits: torch.Tensor) -> torch.Tensor:
         return _sample(logits, fb.temperatures, fb.top_ks, fb.top_ps, fb.seeds,
                        fb.sample_positions, all_greedy=fb.all_greedy)
+
+
+class GraphCache:
+    """HIP graphs of the decode forward (one per batch size and split policy) and of the
+    fixed-shape verify forward. Every captured graph reads its inputs from fixed buffers
+    (DecodeStatic / the verify buffers), so a step is: host builds the batch into those
+    buffers, then one graph replay. Kernels of this library take every size they need from
+    device memory or from launch arguments that are fixed per key; nothing in the captured
+    region allocates host-side or issues memsets."""
+
+    def __init__(self, runner: "ModelRunner", max_graphs: int = 64):
+        cfg = runner.cfg
+        self.runner = runner
+        self.max_graphs = max_graphs
+        self.graphs: OrderedDict = OrderedDict()
+        self.pool = torch.cuda.graph_pool_handle()
+        self.decode_static = DecodeStatic(cfg.max_decode_batch,
+                                          cfg.max_decode_batch * cfg.max_seq_len, runner.device)
+
+    def run(self, fb: ForwardBatch) -> torch.Tensor:
+        entry = self.graphs.get(fb.graph_key)
+        if entry is None:
+            entry = self._capture(fb)
+            self.graphs[fb.graph_key] = entry
+            while len(self.graphs) > self.max_graphs:
+                self.graphs.popitem(last=False)
+        else:
+            self.graphs.move_to_end(fb.graph_key)
+        graph, logits = entry
+        graph.replay()
+        return logits
+
+    def _capture(self, fb: ForwardBatch):
+        runner = self.runner
+        # One eager pass first (lazy initialisation inside torch ops happens outside the
+        # capture); it computes exactly what the replay will recompute.
+        runner._forward_eager(fb)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=self.pool):
+            logits = runner._forward_eager(fb)
+        return graph, logits

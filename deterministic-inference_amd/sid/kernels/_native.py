@@ -26,14 +26,19 @@ _SIGNATURES = {
     "sid_rmsnorm": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
     "sid_fused_add_rmsnorm": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
     "sid_rope_apply": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _vp],
-    "sid_linear": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
+    "sid_linear": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    "sid_linear_partials": [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp],
+    "sid_fused_add_rmsnorm_partials": [_vp, _i32, _vp, _vp, _vp, _i64, _i32, _f32, _vp],
+    "sid_silu_mul_partials": [_vp, _i32, _vp, _i64, _i64, _vp],
+    "sid_qkv_post": [_vp, _vp, _i32, _i64, _i32, _i32, _i32, _vp, _vp, _f32, _vp, _vp, _i64, _vp,
+                     _vp, _vp, _vp, _i64, _vp],
     "sid_silu_mul": [_vp, _vp, _i64, _i64, _vp],
     "sid_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
     "sid_build_decode_indices": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
 }
-EXPORTED = ("sid_last_error", "sid_abi_version", "sid_linear_workspace_bytes", *_SIGNATURES)
-ABI_VERSION = 2
+EXPORTED = ("sid_last_error", "sid_abi_version", *_SIGNATURES)
+ABI_VERSION = 3
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -62,8 +67,6 @@ class NativeLib:
         self.lib.sid_last_error.argtypes = []
         self.lib.sid_abi_version.restype = ctypes.c_int
         self.lib.sid_abi_version.argtypes = []
-        self.lib.sid_linear_workspace_bytes.restype = ctypes.c_int64
-        self.lib.sid_linear_workspace_bytes.argtypes = [_i64, _i64, _i64]
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.argtypes = argtypes
@@ -178,28 +181,80 @@ class NativeLib:
         self._call("sid_rope_apply", q.data_ptr(), k.data_ptr(), positions.data_ptr(),
                    cos_sin.data_ptr(), t, hq, k.shape[1], d, cos_sin.shape[0], _stream(q))
 
-    def linear_workspace_bytes(self, m: int, n: int, k: int) -> int:
-        return int(self.lib.sid_linear_workspace_bytes(m, n, k))
-
-    def linear(self, x, w, bias, y, out_fp32: bool, workspace=None) -> None:
-        _check(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1,
-               "x must be a 2-D bf16 GPU tensor with unit column stride")
-        _gpu(w, "weight", torch.bfloat16)
-        m, k = x.shape
-        n = w.shape[0]
-        _check(w.dim() == 2 and w.shape[1] == k, f"weight must be [N, {k}]")
+    def linear(self, x, w, bias, y, out_fp32: bool) -> None:
+        m, k, n = self._linear_check(x, w)
         if bias is not None:
             _gpu(bias, "bias", torch.bfloat16)
             _check(bias.numel() == n, "bias must have N entries")
         _gpu(y, "out", torch.float32 if out_fp32 else torch.bfloat16)
         _check(tuple(y.shape) == (m, n), "out must be [M, N]")
-        ws_ptr, ws_bytes = None, 0
-        if workspace is not None:
-            _gpu(workspace, "workspace", torch.uint8)
-            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel()
         self._call("sid_linear", x.data_ptr(), x.stride(0) if m > 1 else k, w.data_ptr(),
                    bias.data_ptr() if bias is not None else None, y.data_ptr(), m, n, k,
-                   1 if out_fp32 else 0, ws_ptr, ws_bytes, _stream(x))
+                   1 if out_fp32 else 0, _stream(x))
+
+    def linear_partials(self, x, w, partials) -> None:
+        m, k, n = self._linear_check(x, w)
+        _gpu(partials, "partials", torch.float32)
+        _check(tuple(partials.shape) == (k // 256, m, n), "partials must be [K/256, M, N]")
+        self._call("sid_linear_partials", x.data_ptr(), x.stride(0) if m > 1 else k,
+                   w.data_ptr(), partials.data_ptr(), m, n, k, _stream(x))
+
+    @staticmethod
+    def _linear_check(x, w):
+        _check(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1,
+               "x must be a 2-D bf16 GPU tensor with unit column stride")
+        _gpu(w, "weight", torch.bfloat16)
+        m, k = x.shape
+        _check(w.dim() == 2 and w.shape[1] == k, f"weight must be [N, {k}]")
+        return m, k, w.shape[0]
+
+    def fused_add_rmsnorm_partials(self, partials, residual, w, out, eps: float) -> None:
+        _gpu(partials, "partials", torch.float32)
+        _gpu(residual, "residual", torch.bfloat16)
+        _gpu(out, "out", torch.bfloat16)
+        _gpu(w, "weight", torch.bfloat16)
+        nch, rows, hidden = partials.shape
+        _check(tuple(residual.shape) == (rows, hidden) and out.shape == residual.shape
+               and w.numel() == hidden, "fused_add_rmsnorm_partials shape mismatch")
+        self._call("sid_fused_add_rmsnorm_partials", partials.data_ptr(), nch, residual.data_ptr(),
+                   w.data_ptr(), out.data_ptr(), rows, hidden, float(eps), _stream(out))
+
+    def silu_mul_partials(self, partials, out) -> None:
+        _gpu(partials, "partials", torch.float32)
+        _gpu(out, "out", torch.bfloat16)
+        nch, t, two_i = partials.shape
+        _check(two_i % 2 == 0 and tuple(out.shape) == (t, two_i // 2), "silu_mul_partials shape")
+        self._call("sid_silu_mul_partials", partials.data_ptr(), nch, out.data_ptr(), t,
+                   two_i // 2, _stream(out))
+
+    def qkv_post(self, qkv, partials, q_norm, k_norm, eps: float, positions, cos_sin, slots,
+                 q_out, k_cache, v_cache) -> None:
+        _check((qkv is None) != (partials is None), "give exactly one of qkv and partials")
+        if qkv is not None:
+            _gpu(qkv, "qkv", torch.bfloat16)
+            t, width, nch = qkv.shape[0], qkv.shape[1], 0
+        else:
+            _gpu(partials, "partials", torch.float32)
+            nch, t, width = partials.shape
+        _gpu(q_out, "q_out", torch.bfloat16)
+        _check(q_out.dim() == 3 and q_out.shape[0] == t, "q_out must be [T, HQ, D]")
+        hq, d = q_out.shape[1], q_out.shape[2]
+        for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+            _gpu(c, name, torch.bfloat16)
+            _check(c.dim() == 3 and c.shape[2] == d, f"{name} must be [S, HKV, D]")
+        hkv = k_cache.shape[1]
+        _check(width == (hq + 2 * hkv) * d, "projection width != (HQ + 2*HKV) * D")
+        _gpu(q_norm, "q_norm", torch.bfloat16)
+        _gpu(k_norm, "k_norm", torch.bfloat16)
+        _gpu(positions, "positions", torch.int64)
+        _gpu(slots, "slots", torch.int64)
+        _gpu(cos_sin, "cos_sin", torch.float32)
+        _check(positions.numel() == t and slots.numel() == t, "positions/slots must have T entries")
+        self._call("sid_qkv_post", qkv.data_ptr() if qkv is not None else None,
+                   partials.data_ptr() if partials is not None else None, nch, t, hq, hkv, d,
+                   q_norm.data_ptr(), k_norm.data_ptr(), float(eps), positions.data_ptr(),
+                   cos_sin.data_ptr(), cos_sin.shape[0], slots.data_ptr(), q_out.data_ptr(),
+                   k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0], _stream(q_out))
 
     def silu_mul(self, gate_up, out) -> None:
         _gpu(gate_up, "gate_up", torch.bfloat16)

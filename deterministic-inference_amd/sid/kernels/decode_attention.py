@@ -55,6 +55,11 @@ class DecodeAttention:
         self._plan_src = None
         self._plan = None
 
+    def reset_plan(self) -> None:
+        """Forget the cached split plan (called at the start of every forward)."""
+        self._plan_src = None
+        self._plan = None
+
     def cu_count(self) -> int:
         idx = self.device.index if self.device.index is not None else torch.cuda.current_device()
         return _cu_count(idx)

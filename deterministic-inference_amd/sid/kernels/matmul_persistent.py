@@ -15,23 +15,6 @@ import torch
 
 from sid.kernels.jit import load_ext
 
-# Per-device split-K workspace (zero-filled once; the kernels leave it zeroed). Grown on
-# demand; all users are ordered on torch's current stream.
-_workspaces: dict = {}
-
-
-def workspace_for(m: int, n: int, k: int, device) -> Optional[torch.Tensor]:
-    need = load_ext().linear_workspace_bytes(m, n, k)
-    if need == 0:
-        return None
-    key = torch.device(device)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(max(need, 8 << 20), dtype=torch.uint8, device=key)
-        _workspaces[key] = ws
-    return ws
-
-
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
            out_fp32: bool = False) -> torch.Tensor:
     """y = x @ weight^T (+ bias). x: [..., K] bf16, weight: [N, K] bf16 -> [..., N].
@@ -44,8 +27,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     n = weight.shape[0]
     y = torch.empty(x2.shape[0], n, device=x.device,
                     dtype=torch.float32 if out_fp32 else torch.bfloat16)
-    ws = workspace_for(x2.shape[0], n, x2.shape[1], x.device)
-    load_ext().linear(x2, weight, bias, y, out_fp32, ws)
+    load_ext().linear(x2, weight, bias, y, out_fp32)
     return y.view(*shape[:-1], n)
 
 
@@ -65,3 +47,15 @@ def bi_linear(x: torch.Tensor, weight: torch.Tensor,
               bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Drop-in for F.linear(x, weight, bias) with batch-invariant reduction."""
     return linear(x, weight, bias)
+
+
+def linear_partials(x: torch.Tensor, weight: torch.Tensor,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Split-K chunk sums fp32 [K/256, M, N] of x @ weight^T (fold in order + round to bf16
+    = linear(x, weight) bit for bit); consumed by the *_partials fused ops."""
+    m, k = x.shape
+    n = weight.shape[0]
+    if out is None:
+        out = torch.empty(k // 256, m, n, dtype=torch.float32, device=x.device)
+    load_ext().linear_partials(x, weight, out)
+    return out

@@ -34,3 +34,33 @@ def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     out = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
     load_ext().argmax_rows(logits, out)
     return out
+
+
+def silu_mul_partials(partials: torch.Tensor) -> torch.Tensor:
+    """SwiGLU straight from the gate_up projection's chunk partials [C, T, 2I] -> [T, I]."""
+    _, t, two_i = partials.shape
+    out = torch.empty(t, two_i // 2, dtype=torch.bfloat16, device=partials.device)
+    load_ext().silu_mul_partials(partials, out)
+    return out
+
+
+def fused_add_rmsnorm_partials(partials: torch.Tensor, residual: torch.Tensor,
+                               weight: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """residual += bf16(fold(partials)); returns (rmsnorm(residual), residual)."""
+    out = torch.empty_like(residual)
+    load_ext().fused_add_rmsnorm_partials(partials, residual, weight, out, eps)
+    return out, residual
+
+
+def qkv_post(qkv_or_partials: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor, eps: float,
+             positions: torch.Tensor, cos_sin: torch.Tensor, slots: torch.Tensor,
+             k_cache: torch.Tensor, v_cache: torch.Tensor, num_q_heads: int) -> torch.Tensor:
+    """Fused q/k-norm + RoPE + KV-cache write of a QKV projection (bf16 [T, W] or chunk
+    partials [C, T, W]); returns q [T, HQ, D]."""
+    partial = qkv_or_partials.dtype == torch.float32
+    t = qkv_or_partials.shape[1] if partial else qkv_or_partials.shape[0]
+    d = k_cache.shape[2]
+    q = torch.empty(t, num_q_heads, d, dtype=torch.bfloat16, device=k_cache.device)
+    load_ext().qkv_post(None if partial else qkv_or_partials, qkv_or_partials if partial else None,
+                        q_norm, k_norm, eps, positions, cos_sin, slots, q, k_cache, v_cache)
+    return q

@@ -15,10 +15,16 @@ import torch
 from sid.config import ModelConfig
 from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.kernels.extend_attention import extend_attention_fwd
-from sid.kernels.matmul_persistent import linear
-from sid.kernels.ops import embedding, gather_rows, silu_mul
-from sid.kernels.rmsnorm import fused_add_rmsnorm, qk_head_rmsnorm, rmsnorm
+from sid.kernels.matmul_persistent import linear, linear_partials
+from sid.kernels.ops import (embedding, fused_add_rmsnorm_partials, gather_rows, qkv_post,
+                             silu_mul, silu_mul_partials)
+from sid.kernels.rmsnorm import fused_add_rmsnorm, rmsnorm
 from sid.kernels.rope import RotaryEmbedding
+
+
+# Token counts up to this use split-K projections whose chunk partials are folded by the
+# consuming fused kernel (decode batches); larger ones (prefill) use direct GEMMs.
+SPLIT_K_MAX_TOKENS = 64
 
 
 class Qwen3Model:
@@ -33,57 +39,61 @@ class Qwen3Model:
 
     def set_batch_invariant(self, enabled: bool) -> None:
         # Every GEMM here already reduces in an M-independent order (see
-        # sid.kernels.matmul_persistent), so both settings run the same kernel.
+        # sid.kernels.matmul_persistent), so both settings run the same kernels.
         self.invariant_gemm = enabled
 
-    def _attention(self, layer_idx: int, hidden: torch.Tensor, fb: ForwardBatch, kv_cache,
-                   decode_attn, decode_backend: str) -> torch.Tensor:
+    def _attention(self, layer_idx: int, x: torch.Tensor, fb: ForwardBatch, kv_cache,
+                   decode_attn, decode_backend: str, split: bool) -> torch.Tensor:
+        """qkv projection -> (q/k-norm, RoPE, cache write) -> attention. Returns o [T, HQ*D]."""
         cfg = self.cfg
         lw = self.w["layers"][layer_idx]
-        t = hidden.shape[0]
-        qkv = linear(hidden, lw["qkv"])
-        q, k, v = qkv.split([cfg.q_size, cfg.kv_size, cfg.kv_size], dim=-1)
-        q = q.contiguous().view(t, cfg.num_q_heads, cfg.head_dim)
-        k = k.contiguous().view(t, cfg.num_kv_heads, cfg.head_dim)
-        v = v.contiguous().view(t, cfg.num_kv_heads, cfg.head_dim)
-        q = qk_head_rmsnorm(q, lw["q_norm"], cfg.rms_norm_eps)
-        k = qk_head_rmsnorm(k, lw["k_norm"], cfg.rms_norm_eps)
-        self.rope.apply(q, k, fb.positions)
+        t = x.shape[0]
         k_pool, v_pool = kv_cache.layer(layer_idx)
-        kv_cache.ext.reshape_and_cache(k, v, k_pool, v_pool, fb.out_slots)
+        proj = linear_partials(x, lw["qkv"]) if split else linear(x, lw["qkv"])
+        q = qkv_post(proj, lw["q_norm"], lw["k_norm"], cfg.rms_norm_eps, fb.positions,
+                     self.rope.cos_sin, fb.out_slots, k_pool, v_pool, cfg.num_q_heads)
         if fb.mode == ForwardMode.DECODE and decode_backend == "hip":
             o = decode_attn.forward(q, k_pool, v_pool, fb.kv_indptr, fb.kv_indices, fb.seq_lens,
                                     fb.max_seq_len, self.sm_scale, invariant=fb.invariant)
         else:
             qo = fb.qo_indptr
             if qo is None:  # decode through the extend kernel: one query per request
-                qo = torch.arange(t + 1, dtype=torch.int32, device=hidden.device)
+                qo = torch.arange(t + 1, dtype=torch.int32, device=x.device)
             o = extend_attention_fwd(q, k_pool, v_pool, qo, fb.kv_indptr, fb.kv_indices,
                                      max(fb.max_extend_len, 1), self.sm_scale)
-        return linear(o.view(t, cfg.q_size), lw["o"])
-
-    def _mlp(self, layer_idx: int, hidden: torch.Tensor) -> torch.Tensor:
-        lw = self.w["layers"][layer_idx]
-        return linear(silu_mul(linear(hidden, lw["gate_up"])), lw["down"])
+        return o.view(t, cfg.q_size)
 
     @torch.inference_mode()
     def forward(self, fb: ForwardBatch, kv_cache, decode_attn,
                 decode_backend: str = "hip") -> torch.Tensor:
-        """fp32 logits [R, vocab] for the sampled rows (bf16-rounded values)."""
+        """fp32 logits [R, vocab] for the sampled rows (bf16-rounded values).
+
+        Same op order as sid/model/qwen3.py:88-115; the residual add + RMSNorm that follows
+        each o / down projection consumes the projection directly (fused), and the down
+        projection of layer i feeds layer i+1's input norm (or the final norm)."""
         cfg = self.cfg
-        hidden = embedding(fb.input_ids, self.w["embed"])
-        residual = None
+        eps = cfg.rms_norm_eps
+        layers = self.w["layers"]
+        t = fb.input_ids.shape[0]
+        split = t <= SPLIT_K_MAX_TOKENS
+        decode_attn.reset_plan()
+        residual = embedding(fb.input_ids, self.w["embed"])
+        x = rmsnorm(residual, layers[0]["input_ln"], eps)
         for i in range(cfg.num_layers):
-            lw = self.w["layers"][i]
-            if residual is None:
-                residual = hidden
-                hidden = rmsnorm(hidden, lw["input_ln"], cfg.rms_norm_eps)
+            lw = layers[i]
+            o = self._attention(i, x, fb, kv_cache, decode_attn, decode_backend, split)
+            if split:
+                x, residual = fused_add_rmsnorm_partials(linear_partials(o, lw["o"]), residual,
+                                                         lw["post_ln"], eps)
+                act = silu_mul_partials(linear_partials(x, lw["gate_up"]))
             else:
-                hidden, residual = fused_add_rmsnorm(hidden, residual, lw["input_ln"],
-                                                     cfg.rms_norm_eps)
-            hidden = self._attention(i, hidden, fb, kv_cache, decode_attn, decode_backend)
-            hidden, residual = fused_add_rmsnorm(hidden, residual, lw["post_ln"], cfg.rms_norm_eps)
-            hidden = self._mlp(i, hidden)
-        hidden, _ = fused_add_rmsnorm(hidden, residual, self.w["norm"], cfg.rms_norm_eps)
-        rows = hidden if fb.sample_indices is None else gather_rows(hidden, fb.sample_indices)
+                x, residual = fused_add_rmsnorm(linear(o, lw["o"]), residual, lw["post_ln"], eps)
+                act = silu_mul(linear(x, lw["gate_up"]))
+            next_w = layers[i + 1]["input_ln"] if i + 1 < cfg.num_layers else self.w["norm"]
+            if split:
+                x, residual = fused_add_rmsnorm_partials(linear_partials(act, lw["down"]),
+                                                         residual, next_w, eps)
+            else:
+                x, residual = fused_add_rmsnorm(linear(act, lw["down"]), residual, next_w, eps)
+        rows = x if fb.sample_indices is None else gather_rows(x, fb.sample_indices)
         return linear(rows, self.w["lm_head"], out_fp32=True)

@@ -103,6 +103,17 @@ int sid_fused_add_rmsnorm(void* x, void* residual, const void* w, int64_t rows, 
                           float eps, void* stream);
 
 /*
+ * sid_fused_add_rmsnorm with the x operand given as sid_linear_partials
+ * output (nchunks chunk tiles of [rows, hidden]): x = bf16(fold(partials));
+ * residual += x (stored as bf16); out = rmsnorm(residual). Bit-identical to
+ * sid_linear followed by sid_fused_add_rmsnorm. Replaces the o/down
+ * projection + fused_add_rmsnorm pair, sid/model/qwen3.py:80, 86, 104-108.
+ */
+int sid_fused_add_rmsnorm_partials(const float* partials, int nchunks, void* residual,
+                                   const void* w, void* out, int64_t rows, int hidden, float eps,
+                                   void* stream);
+
+/*
  * NeoX rotate-half RoPE in place on q bf16 [T, HQ, D] and k bf16 [T, HKV, D]
  * at positions int64 [T], using cos_sin fp32 [max_positions, D] =
  * [cos(D/2) | sin(D/2)]. Tokens whose position is outside [0, max_positions)
@@ -121,21 +132,24 @@ int sid_rope_apply(void* q, void* k, const int64_t* positions, const float* cos_
  * N a multiple of 64.
  * The reduction order of every output element is fixed and independent of M
  * (K in 256-wide chunks, each accumulated from zero in increasing k, chunk
- * sums added in increasing chunk order), so each row is bitwise identical
- * whatever batch it is computed in, with or without a workspace.
- * workspace: optional device buffer of workspace_bytes (256-byte aligned,
- * zero-filled once before first use; the kernels leave it zeroed) that lets
- * small-M GEMMs split K over more workgroups; see sid_linear_workspace_bytes.
- * Calls sharing a workspace must be ordered on one stream.
+ * sums added in increasing chunk order, then the bias, then one rounding),
+ * so each row is bitwise identical whatever batch it is computed in.
  * Replaces F.linear / bi_linear / matmul_persistent at sid/model/qwen3.py:49,
  * 80, 84, 86, 114 and sid/kernels/matmul_persistent.py:82-113.
  */
 int sid_linear(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
-               int64_t n, int64_t k, int out_fp32, void* workspace, int64_t workspace_bytes,
-               void* stream);
+               int64_t n, int64_t k, int out_fp32, void* stream);
 
-/* Workspace bytes sid_linear uses for an (m, n, k) problem; 0 = it does not split. */
-int64_t sid_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
+/*
+ * Split-K form of sid_linear without bias: partials fp32 [K/256][M][N] gets
+ * the sum of each 256-wide K chunk (accumulated exactly as in sid_linear).
+ * Folding the chunks in increasing order and rounding to bf16 gives
+ * sid_linear's result bit for bit; the *_partials consumers below do that.
+ * Used for the small-M decode projections, whose N alone is too small to
+ * fill the GPU. Same shape rules as sid_linear.
+ */
+int sid_linear_partials(const void* x, int64_t ldx, const void* w, float* partials, int64_t m,
+                        int64_t n, int64_t k, void* stream);
 
 /*
  * out[t, i] = silu(gate[t, i]) * up[t, i] with gate = gate_up[t, :I] and
@@ -144,6 +158,27 @@ int64_t sid_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
  * Replaces sid/model/qwen3.py:84-85.
  */
 int sid_silu_mul(const void* gate_up, void* out, int64_t num_tokens, int64_t inter, void* stream);
+
+/* sid_silu_mul with gate_up given as sid_linear_partials output [nchunks][T][2I]. */
+int sid_silu_mul_partials(const float* partials, int nchunks, void* out, int64_t num_tokens,
+                          int64_t inter, void* stream);
+
+/*
+ * Fused QKV epilogue of Qwen3 attention (sid/model/qwen3.py:49-61): row t of
+ * the projection is [q (HQ*D) | k (HKV*D) | v (HKV*D)], given either as bf16
+ * qkv [T, (HQ+2*HKV)*D] or as sid_linear_partials output (exactly one of qkv
+ * and partials non-NULL). q and k get the per-head RMSNorm (weights q_norm,
+ * k_norm bf16 [D]) then NeoX RoPE at positions[t] (cos_sin as in
+ * sid_rope_apply); q goes to q_out bf16 [T, HQ, D]; k and v are written to
+ * k_cache / v_cache [S, HKV, D] at slots[t] (slots outside [0, S) skipped).
+ * Bit-identical to split + qk_head_rmsnorm + rope + reshape_and_cache.
+ * D must be 128.
+ */
+int sid_qkv_post(const void* qkv, const float* partials, int nchunks, int64_t num_tokens,
+                 int num_q_heads, int num_kv_heads, int head_dim, const void* q_norm,
+                 const void* k_norm, float eps, const int64_t* positions, const float* cos_sin,
+                 int64_t max_positions, const int64_t* slots, void* q_out, void* k_cache,
+                 void* v_cache, int64_t num_slots, void* stream);
 
 /*
  * out[i] = table[idx[i]] for bf16 rows of row_elems elements (row_elems a

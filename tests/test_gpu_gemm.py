@@ -61,24 +61,18 @@ def test_strided_input_rows():
 
 
 @pytest.mark.parametrize("m,n,k", [(64, 4096, 1024), (64, 1024, 2048), (64, 6144, 1024),
-                                   (64, 1024, 3072), (5, 1024, 3072), (1, 4096, 1024)])
-def test_split_k_bitwise_equals_single_pass(m, n, k):
-    """Split mode (one K chunk per workgroup, last arrival folds) and the single-pass mode
-    produce identical bits; repeated calls reuse the self-resetting counters."""
-    from sid.kernels.jit import load_ext
-    ext = load_ext()
+                                   (64, 1024, 3072), (5, 1024, 3072), (1, 4096, 1024),
+                                   (100, 1024, 2048)])
+def test_partials_fold_equals_linear(m, n, k):
+    """Chunk partials folded in increasing chunk order and rounded to bf16 equal sid_linear
+    bit for bit (the contract the *_partials consumers rely on)."""
+    from sid.kernels.matmul_persistent import linear, linear_partials
     torch.manual_seed(4)
     x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
     w = (torch.randn(n, k, device="cuda") * 0.05).to(torch.bfloat16)
-    b = torch.randn(n, device="cuda", dtype=torch.bfloat16)
-    need = ext.linear_workspace_bytes(m, n, k)
-    assert need > 0
-    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
-    ref = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
-    ext.linear(x, w, b, ref, False, None)
-    for _ in range(3):
-        out = torch.empty_like(ref)
-        ext.linear(x, w, b, out, False, ws)
-        assert torch.equal(out, ref)
-    counters = ws[: ((n // 64) * 4 + 255) // 256 * 256]
-    assert torch.count_nonzero(counters) == 0
+    p = linear_partials(x, w)
+    assert p.shape == (k // 256, m, n)
+    fold = p[0].clone()
+    for c in range(1, p.shape[0]):
+        fold += p[c]
+    assert torch.equal(fold.to(torch.bfloat16), linear(x, w))

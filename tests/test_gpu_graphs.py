@@ -1,0 +1,88 @@
+"""HIP-graph replays of the decode and verify forwards are bit-identical to eager forwards
+(same weights, same requests), across steps, batch sizes (one graph each) and modes."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from sid.config import EngineConfig, Mode, SamplingParams
+from sid.engine.batch import build_prefill_batch
+from sid.engine.model_runner import ModelRunner
+from sid.engine.request import Request
+
+pytestmark = pytest.mark.gpu
+
+
+def _runner(graphs, mode=Mode.NONDET):
+    cfg = EngineConfig(mode=mode, kv_pool_tokens=8192, max_reqs=16, max_seq_len=1024,
+                       max_decode_batch=16, num_layers=2, seed=11, use_graphs=graphs)
+    return ModelRunner(cfg, "cuda")
+
+
+def _requests(runner, lens, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    reqs = []
+    for rid, p in enumerate(lens):
+        r = Request(rid, torch.randint(0, 151936, (p,), generator=g).tolist(),
+                    SamplingParams(max_new_tokens=64), runner.mcfg.eos_token_ids)
+        r.req_row = runner.kv_cache.alloc_row()
+        reqs.append(r)
+    return reqs
+
+
+@pytest.mark.parametrize("invariant", [False, True])
+def test_decode_graph_equals_eager(invariant):
+    lens = [30, 300, 7, 64, 129]
+    outs = {}
+    for graphs in (False, True):
+        runner = _runner(graphs)
+        reqs = _requests(runner, lens)
+        fb = build_prefill_batch(reqs, runner.kv_cache, "cuda", invariant=False)
+        for r, t in zip(reqs, runner.sample(fb, runner.forward(fb)).tolist()):
+            r.output_ids.append(t)
+        logs = []
+        for step in range(6):
+            active = reqs if step < 3 else reqs[:3]  # batch 5, then batch 3 (second graph)
+            fb = runner.prepare_decode(active, invariant)
+            assert (fb.graph_key is not None) == graphs
+            lg = runner.forward(fb)
+            logs.append(lg.clone())
+            for r, t in zip(active, runner.sample(fb, lg).tolist()):
+                r.output_ids.append(t)
+        outs[graphs] = (logs, [r.output_ids for r in reqs])
+    assert outs[True][1] == outs[False][1]
+    for a, b in zip(outs[True][0], outs[False][0]):
+        assert torch.equal(a, b)
+
+
+def test_verify_graph_equals_eager():
+    from sid.engine.dvr import Verifier
+    results = {}
+    for graphs in (False, True):
+        runner = _runner(graphs, Mode.DVR)
+        reqs = _requests(runner, [40, 90], seed=3)
+        for r in reqs:
+            r.params.is_deterministic = True
+        ver = Verifier(runner.cfg, runner, runner.kv_cache)
+        fb = build_prefill_batch(reqs[:1], runner.kv_cache, "cuda", invariant=False)
+        reqs[0].output_ids.append(runner.sample(fb, runner.forward(fb)).item())
+        fb = build_prefill_batch(reqs[1:], runner.kv_cache, "cuda", invariant=False)
+        reqs[1].output_ids.append(runner.sample(fb, runner.forward(fb)).item())
+        for r in reqs:
+            r.verified_len = 1
+        for _ in range(40):
+            fb = runner.prepare_decode(reqs, False)
+            for r, t in zip(reqs, runner.sample(fb, runner.forward(fb)).tolist()):
+                r.output_ids.append(t)
+        logs = []
+        for _ in range(2):  # two verify passes over the same group: graph replayed twice
+            fb, meta = ver.build_verify_batch(reqs)
+            runner.tag_verify(fb)
+            lg = runner.forward(fb)
+            logs.append(lg.clone())
+            ver.compare_and_rollback(meta, runner.sample(fb, lg))
+        results[graphs] = (logs, [r.output_ids for r in reqs])
+    assert results[True][1] == results[False][1]
+    for a, b in zip(results[True][0], results[False][0]):
+        assert torch.equal(a, b)

@@ -40,7 +40,7 @@ def test_python_binding_matches_header(ext):
 
 
 def test_abi_version(ext):
-    assert ext.lib.sid_abi_version() == 2
+    assert ext.lib.sid_abi_version() == 3
 
 
 def test_validation_errors_without_device_work(ext):
@@ -56,9 +56,9 @@ def test_validation_errors_without_device_work(ext):
     rc = lib.sid_flash_decode_fwd(1, 1, 1, 1, 1, 1, 2, 16, 8, 128, 10, 4, 0, f, 1, 1, 1, 2, 1,
                                   None)
     assert rc == 1 and b"workspace" in lib.sid_last_error()
-    rc = lib.sid_linear(16, 1000, 16, None, 16, 4, 64, 1000, 0, None, 0, None)
+    rc = lib.sid_linear(16, 1000, 16, None, 16, 4, 64, 1000, 0, None)
     assert rc == 1 and b"multiple of 256" in lib.sid_last_error()
-    rc = lib.sid_linear(16, 1024, 16, None, 16, 4, 60, 1024, 0, None, 0, None)
+    rc = lib.sid_linear(16, 1024, 16, None, 16, 4, 60, 1024, 0, None)
     assert rc == 1 and b"multiple of 64" in lib.sid_last_error()
     rc = lib.sid_reshape_and_cache(1, 1, 1, 1, 1, 4, 1, 3, 10, None)
     assert rc == 1 and b"16-byte" in lib.sid_last_error()
