@@ -40,32 +40,36 @@ __device__ __forceinline__ bf16x8_v ld_frag(const bf16_t* p) {
   return *reinterpret_cast<const bf16x8_v*>(p);
 }
 
-// x chunk in registers: thread t holds 16-byte vector t%32 of rows t/32 + 8*i.
-struct XRegs {
-  uint4 v[8];
-};
-
-__device__ __forceinline__ void load_x(XRegs& xr, const bf16_t* __restrict__ x, int64_t ldx,
+// x chunk in registers: thread t holds 16-byte vector t%32 of rows t/32 + 8*i. The
+// row-count test is written per pass (i < rows16 / 8, uniform over the workgroup because
+// rows16 is a multiple of 16), which keeps the 8 vectors in registers: a per-lane test
+// here, or HIP's struct-wrapped uint4 as the element type, made the compiler demote them
+// to scratch and serialise every load (native vector types stay in registers).
+__device__ __forceinline__ void load_x(bf16x8_v (&xv)[8], const bf16_t* __restrict__ x, int64_t ldx,
                                        int64_t m0, int64_t M, int rows16, int64_t k0) {
   const int tid = threadIdx.x;
   const int vec = tid & 31;
+  const int passes = rows16 >> 3;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int row = (tid >> 5) + 8 * i;
-    if (row < rows16) {
+    if (i < passes) {
+      const int row = (tid >> 5) + 8 * i;
       const int64_t gr = min<int64_t>(m0 + row, M - 1);  // rows >= M are clamped and discarded
-      xr.v[i] = *reinterpret_cast<const uint4*>(x + gr * ldx + k0 + vec * 8);
+      xv[i] = ld_frag(x + gr * ldx + k0 + vec * 8);
     }
   }
 }
 
-__device__ __forceinline__ void store_x(bf16_t* sx, const XRegs& xr, int rows16) {
+__device__ __forceinline__ void store_x(bf16_t* sx, const bf16x8_v (&xv)[8], int rows16) {
   const int tid = threadIdx.x;
   const int vec = tid & 31;
+  const int passes = rows16 >> 3;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int row = (tid >> 5) + 8 * i;
-    if (row < rows16) *reinterpret_cast<uint4*>(&sx[row * XS + vec * 8]) = xr.v[i];
+    if (i < passes) {
+      const int row = (tid >> 5) + 8 * i;
+      *reinterpret_cast<bf16x8_v*>(&sx[row * XS + vec * 8]) = xv[i];
+    }
   }
 }
 
@@ -118,7 +122,7 @@ __global__ void __launch_bounds__(256) linear_kernel(
   const int c_end = partial ? c_begin + 1 : nchunks;
 
   bf16x8_v wf[NSTEP];
-  XRegs xr;
+  bf16x8_v xr[8];
   load_w(wf, wrow, static_cast<int64_t>(c_begin) * KC);
   load_x(xr, x, ldx, m0, M, rows16, static_cast<int64_t>(c_begin) * KC);
 

@@ -71,12 +71,12 @@ def test_verify_graph_equals_eager():
         reqs[1].output_ids.append(runner.sample(fb, runner.forward(fb)).item())
         for r in reqs:
             r.verified_len = 1
-        for _ in range(40):
-            fb = runner.prepare_decode(reqs, False)
-            for r, t in zip(reqs, runner.sample(fb, runner.forward(fb)).tolist()):
-                r.output_ids.append(t)
         logs = []
-        for _ in range(2):  # two verify passes over the same group: graph replayed twice
+        for _ in range(2):  # two verify passes: the graph is captured, then replayed
+            while any(r.unverified() < 20 for r in reqs):
+                fb = runner.prepare_decode(reqs, False)
+                for r, t in zip(reqs, runner.sample(fb, runner.forward(fb)).tolist()):
+                    r.output_ids.append(t)
             fb, meta = ver.build_verify_batch(reqs)
             runner.tag_verify(fb)
             lg = runner.forward(fb)

@@ -74,7 +74,8 @@ def test_prefill_then_decode_vs_oracle(layers):
     used = fb.out_slots.cpu()
     torch.testing.assert_close(kv.k_pools[0][used.cuda()].float().cpu(), kp[0][used].float(),
                                atol=2e-2, rtol=2e-2)
-    assert torch.equal(kv.v_pools[0][used.cuda()].cpu(), vp[0][used])  # v: projection only
+    torch.testing.assert_close(kv.v_pools[0][used.cuda()].float().cpu(), vp[0][used].float(),
+                               atol=1e-2, rtol=1e-2)
 
     toks = runner.sample(fb, logits).tolist()
     for r, t in zip(reqs, toks):
