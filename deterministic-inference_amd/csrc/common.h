@@ -21,6 +21,8 @@ typedef uint16_t bf16_t;  // raw bf16 bits; the C-ABI passes bf16 tensors as voi
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_v;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_v;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_v;
+// Native 16-byte vector (HIP's uint4 is a struct; arrays of it can defeat SROA).
+typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_lo(uint32_t packed) {
   return __uint_as_float(packed << 16);

@@ -45,7 +45,7 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 
 // 16-dim partial dot product of one query head with one token row (the two
 // 16-byte halves a lane owns), fixed order.
-__device__ __forceinline__ float dot16(const uint4 (&qa)[2], const uint4 (&ka)[2]) {
+__device__ __forceinline__ float dot16(const u32x4_v (&qa)[2], const u32x4_v (&ka)[2]) {
   float s = dot2(qa[0].x, ka[0].x, 0.0f);
   s = dot2(qa[0].y, ka[0].y, s);
   s = dot2(qa[0].z, ka[0].z, s);
@@ -65,7 +65,7 @@ __device__ __forceinline__ float group8_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ void unpack16(const uint4 (&va)[2], float (&out)[16]) {
+__device__ __forceinline__ void unpack16(const u32x4_v (&va)[2], float (&out)[16]) {
   const uint32_t w[8] = {va[0].x, va[0].y, va[0].z, va[0].w, va[1].x, va[1].y, va[1].z, va[1].w};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -104,9 +104,32 @@ __device__ __forceinline__ void merge_with_partner(float (&m)[QPK], float (&l)[Q
   }
 }
 
+// Per-iteration register state of one lane: the pool slots of its TPL tokens
+// and their K and V halves.
+template <int TPL>
+struct TileRegs {
+  u32x4_v k[TPL][2];
+  u32x4_v v[TPL][2];
+};
+
+template <bool NT>
+__device__ __forceinline__ u32x4_v ld16(const u32x4_v* p) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+
 // NW waves per workgroup; TPL tokens per lane group per iteration, so one
 // wave iteration covers IT = 8 * TPL consecutive tokens of the split.
-template <int NW, int TPL>
+// PF: software pipeline inside each wave (slot indices fetched two iterations
+// ahead, K/V rows one iteration ahead) so the index -> row dependent loads
+// are off the critical path. NT: non-temporal K/V loads (streamed once).
+// RF: request-fastest grid (blockIdx.x = request, blockIdx.y = kv head), so the
+// round-robin workgroup->XCD assignment keeps all heads of a request on one XCD;
+// otherwise the kv head is fastest (every workgroup of head h on the same XCD).
+template <int NW, int TPL, bool PF, bool NT, bool RF = false>
 __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ kv_indptr,
@@ -114,8 +137,8 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
     int fixed_split, float sm_scale, int num_kv_heads, int64_t num_slots, int part_stride,
     float* __restrict__ part_o, float* __restrict__ part_lse, bf16_t* __restrict__ o_direct) {
   constexpr int IT = 8 * TPL;
-  const int h_kv = blockIdx.x;
-  const int b = blockIdx.y;
+  const int h_kv = RF ? blockIdx.y : blockIdx.x;
+  const int b = RF ? blockIdx.x : blockIdx.y;
   const int split = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -147,9 +170,9 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   const int end = min(start + chunk, seq_len);
 
   // Query pair, packed bf16: lane `sub` holds the dims it owns for both heads.
-  uint4 qv[QPK][2];
+  u32x4_v qv[QPK][2];
   {
-    const uint4* qb = reinterpret_cast<const uint4*>(q + out_row * HEAD_DIM);
+    const u32x4_v* qb = reinterpret_cast<const u32x4_v*>(q + out_row * HEAD_DIM);
 #pragma unroll
     for (int h = 0; h < QPK; ++h) {
       qv[h][0] = qb[h * (HEAD_DIM / 8) + sub];
@@ -169,57 +192,99 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   const int n_it = ceil_div(end - start, IT);
   const int32_t* idx = kv_indices + kv_base;
   const int64_t row_stride = static_cast<int64_t>(num_kv_heads) * HEAD_DIM;
+  const bf16_t* kbase = k_cache + h_kv * HEAD_DIM;
+  const bf16_t* vbase = v_cache + h_kv * HEAD_DIM;
 
-  for (int it = wave; it < n_it; it += NW) {
-    const int tok0 = start + it * IT + grp;
-    bool valid[TPL];
-    uint4 kr[TPL][2], vr[TPL][2];
+  // Slot of token t of iteration `it` for this lane (-1 = past the split's end).
+  auto load_slots = [&](int it, int64_t (&sl)[TPL]) {
 #pragma unroll
     for (int t = 0; t < TPL; ++t) {
-      const int pos = tok0 + 8 * t;
-      valid[t] = pos < end;
-      int64_t slot = valid[t] ? static_cast<int64_t>(idx[pos]) : 0;
-      if (slot < 0 || slot >= num_slots) slot = 0;
-      const uint4* kp = reinterpret_cast<const uint4*>(k_cache + slot * row_stride + h_kv * HEAD_DIM);
-      const uint4* vp = reinterpret_cast<const uint4*>(v_cache + slot * row_stride + h_kv * HEAD_DIM);
-      if (valid[t]) {
-        kr[t][0] = kp[sub];
-        kr[t][1] = kp[8 + sub];
-        vr[t][0] = vp[sub];
-        vr[t][1] = vp[8 + sub];
+      const int pos = start + it * IT + grp + 8 * t;
+      int64_t s = -1;
+      if (it < n_it && pos < end) {
+        s = static_cast<int64_t>(idx[pos]);
+        if (s < 0 || s >= num_slots) s = 0;
+      }
+      sl[t] = s;
+    }
+  };
+  auto load_rows = [&](const int64_t (&sl)[TPL], TileRegs<TPL>& r) {
+#pragma unroll
+    for (int t = 0; t < TPL; ++t) {
+      if (sl[t] >= 0) {
+        const u32x4_v* kp = reinterpret_cast<const u32x4_v*>(kbase + sl[t] * row_stride);
+        const u32x4_v* vp = reinterpret_cast<const u32x4_v*>(vbase + sl[t] * row_stride);
+        r.k[t][0] = ld16<NT>(kp + sub);
+        r.k[t][1] = ld16<NT>(kp + 8 + sub);
+        r.v[t][0] = ld16<NT>(vp + sub);
+        r.v[t][1] = ld16<NT>(vp + 8 + sub);
       } else {
-        kr[t][0] = kr[t][1] = vr[t][0] = vr[t][1] = make_uint4(0, 0, 0, 0);
+        r.k[t][0] = r.k[t][1] = r.v[t][0] = r.v[t][1] = u32x4_v{0u, 0u, 0u, 0u};
       }
     }
-
+  };
+  auto compute = [&](const int64_t (&sl)[TPL], const TileRegs<TPL>& r) {
 #pragma unroll
     for (int h = 0; h < QPK; ++h) {
       float s[TPL];
       float tmax = NEG_BIG;
 #pragma unroll
       for (int t = 0; t < TPL; ++t) {
-        s[t] = group8_sum(dot16(qv[h], kr[t])) * sm_scale;
-        if (valid[t]) tmax = fmaxf(tmax, s[t]);
+        s[t] = group8_sum(dot16(qv[h], r.k[t])) * sm_scale;
+        if (sl[t] >= 0) tmax = fmaxf(tmax, s[t]);
       }
       const float mn = fmaxf(m[h], tmax);
-      const float r = __expf(m[h] - mn);
+      const float rs = __expf(m[h] - mn);
       float psum = 0.0f;
 #pragma unroll
       for (int t = 0; t < TPL; ++t) {
-        s[t] = valid[t] ? __expf(s[t] - mn) : 0.0f;
+        s[t] = sl[t] >= 0 ? __expf(s[t] - mn) : 0.0f;
         psum += s[t];
       }
-      l[h] = l[h] * r + psum;
+      l[h] = l[h] * rs + psum;
       m[h] = mn;
 #pragma unroll
-      for (int d = 0; d < 16; ++d) acc[h][d] *= r;
+      for (int d = 0; d < 16; ++d) acc[h][d] *= rs;
 #pragma unroll
       for (int t = 0; t < TPL; ++t) {
         float vf[16];
-        unpack16(vr[t], vf);
+        unpack16(r.v[t], vf);
 #pragma unroll
         for (int d = 0; d < 16; ++d) acc[h][d] += s[t] * vf[d];
       }
+    }
+  };
+
+  if constexpr (!PF) {
+    for (int it = wave; it < n_it; it += NW) {
+      int64_t sl[TPL];
+      TileRegs<TPL> r;
+      load_slots(it, sl);
+      load_rows(sl, r);
+      compute(sl, r);
+    }
+  } else {
+    // Two register sets A/B alternate; slots run two iterations ahead of compute.
+    int64_t sa[TPL], sb[TPL], sn[TPL];
+    TileRegs<TPL> ra, rb;
+    int it = wave;
+    load_slots(it, sa);
+    load_slots(it + NW, sb);
+    load_rows(sa, ra);
+    while (it < n_it) {
+      load_rows(sb, rb);                // rows of it + NW
+      load_slots(it + 2 * NW, sn);      // slots of it + 2*NW
+      compute(sa, ra);                  // it
+      it += NW;
+      if (it >= n_it) break;
+#pragma unroll
+      for (int t = 0; t < TPL; ++t) sa[t] = sn[t];
+      load_rows(sa, ra);                // rows of it + NW
+      load_slots(it + 2 * NW, sn);      // slots of it + 2*NW
+      compute(sb, rb);                  // it
+      it += NW;
+#pragma unroll
+      for (int t = 0; t < TPL; ++t) sb[t] = sn[t];
     }
   }
 
@@ -299,8 +364,34 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_kernel(
   o[row * HEAD_DIM + d] = f32_to_bf16(num / den);
 }
 
+// Production configuration (the bits of a result depend on NW and TPL, which fix the
+// in-split reduction order; they are constants, independent of batch and policy).
 constexpr int kWaves = 4;
 constexpr int kTokPerLane = 4;
+constexpr bool kPipelined = false;   // measured: no gain over 2 workgroups per CU
+constexpr bool kNonTemporal = true;  // K/V rows are streamed once: +9% HBM throughput
+constexpr bool kRequestFastest = true;
+
+template <int NW, int TPL, bool PF, bool NT, bool RF = false>
+int launch_decode(const void* q, const void* k_cache, const void* v_cache,
+                  const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
+                  int batch, int num_q_heads, int num_kv_heads, int64_t num_slots, int max_splits,
+                  int fixed_split_size, float sm_scale, float* part_o, float* part_lse,
+                  int part_stride, void* o, hipStream_t s) {
+  const bool direct = (max_splits == 1);
+  const dim3 grid1 = RF ? dim3(batch, num_kv_heads, max_splits) : dim3(num_kv_heads, batch, max_splits);
+  hipLaunchKernelGGL((decode_stage1_kernel<NW, TPL, PF, NT, RF>), grid1, dim3(NW * 64), 0, s,
+                     (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr,
+                     kv_indices, num_splits, fixed_split_size, sm_scale, num_kv_heads, num_slots,
+                     part_stride, part_o, part_lse, direct ? (bf16_t*)o : nullptr);
+  int rc = check_launch("flash_decode_fwd stage1");
+  if (rc != SID_OK || direct) return rc;
+  const dim3 grid2(num_q_heads, batch);
+  hipLaunchKernelGGL(decode_stage2_kernel, grid2, dim3(HEAD_DIM), 0, s, part_o, part_lse,
+                     kv_indptr, num_splits, fixed_split_size, max_splits, num_q_heads,
+                     part_stride, (bf16_t*)o);
+  return check_launch("flash_decode_fwd stage2");
+}
 
 }  // namespace
 }  // namespace sid
@@ -336,17 +427,8 @@ extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const vo
                 "(part_batch %d, part_stride %d, batch %d, max_splits %d)",
                 part_batch, part_stride, batch, max_splits);
   }
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid1(num_kv_heads, batch, max_splits);
-  hipLaunchKernelGGL((decode_stage1_kernel<kWaves, kTokPerLane>), grid1, dim3(kWaves * 64), 0, s,
-                     (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr,
-                     kv_indices, num_splits, fixed_split_size, sm_scale, num_kv_heads, num_slots,
-                     part_stride, part_o, part_lse, direct ? (bf16_t*)o : nullptr);
-  int rc = check_launch("flash_decode_fwd stage1");
-  if (rc != SID_OK || direct) return rc;
-  const dim3 grid2(num_q_heads, batch);
-  hipLaunchKernelGGL(decode_stage2_kernel, grid2, dim3(HEAD_DIM), 0, s, part_o, part_lse,
-                     kv_indptr, num_splits, fixed_split_size, max_splits, num_q_heads,
-                     part_stride, (bf16_t*)o);
-  return check_launch("flash_decode_fwd stage2");
+  return launch_decode<kWaves, kTokPerLane, kPipelined, kNonTemporal, kRequestFastest>(
+      q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, batch, num_q_heads, num_kv_heads,
+      num_slots, max_splits, fixed_split_size, sm_scale, part_o, part_lse, part_stride, o,
+      static_cast<hipStream_t>(stream));
 }

@@ -41,25 +41,62 @@ struct RowSrc {
   int nchunks;
 };
 
+// NCH > 0: exactly NCH chunks, all loads issued before the fold (fully unrolled);
+// NCH == 0: s.bf; NCH < 0: s.nchunks chunks, generic loop.
+template <int NCH>
 __device__ __forceinline__ void load8_src(const RowSrc& s, int64_t row, int64_t col, float (&f)[8]) {
-  if (s.part == nullptr) {
+  if constexpr (NCH == 0) {
     load8(*reinterpret_cast<const uint4*>(s.bf + row * s.ld + col), f);
     return;
-  }
-  const float* p = s.part + row * s.ld + col;
-  float4 a = *reinterpret_cast<const float4*>(p);
-  float4 b = *reinterpret_cast<const float4*>(p + 4);
-  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-  for (int c = 1; c < s.nchunks; ++c) {
-    p += s.chunk_stride;
-    a = *reinterpret_cast<const float4*>(p);
-    b = *reinterpret_cast<const float4*>(p + 4);
-    f[0] += a.x; f[1] += a.y; f[2] += a.z; f[3] += a.w;
-    f[4] += b.x; f[5] += b.y; f[6] += b.z; f[7] += b.w;
-  }
+  } else {
+    const float* p = s.part + row * s.ld + col;
+    if constexpr (NCH > 0) {
+      float4 a[NCH], b[NCH];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) f[e] = round_bf16(f[e]);
+      for (int c = 0; c < NCH; ++c) {
+        a[c] = *reinterpret_cast<const float4*>(p + c * s.chunk_stride);
+        b[c] = *reinterpret_cast<const float4*>(p + c * s.chunk_stride + 4);
+      }
+      f[0] = a[0].x; f[1] = a[0].y; f[2] = a[0].z; f[3] = a[0].w;
+      f[4] = b[0].x; f[5] = b[0].y; f[6] = b[0].z; f[7] = b[0].w;
+#pragma unroll
+      for (int c = 1; c < NCH; ++c) {
+        f[0] += a[c].x; f[1] += a[c].y; f[2] += a[c].z; f[3] += a[c].w;
+        f[4] += b[c].x; f[5] += b[c].y; f[6] += b[c].z; f[7] += b[c].w;
+      }
+    } else {
+      float4 a = *reinterpret_cast<const float4*>(p);
+      float4 b = *reinterpret_cast<const float4*>(p + 4);
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+      f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+      for (int c = 1; c < s.nchunks; ++c) {
+        p += s.chunk_stride;
+        a = *reinterpret_cast<const float4*>(p);
+        b = *reinterpret_cast<const float4*>(p + 4);
+        f[0] += a.x; f[1] += a.y; f[2] += a.z; f[3] += a.w;
+        f[4] += b.x; f[5] += b.y; f[6] += b.z; f[7] += b.w;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = round_bf16(f[e]);
+  }
+}
+
+// Calls fn.template operator()<NCH>() with NCH the compile-time chunk count of src
+// (0 for a bf16 source; -1 for a count without a specialised instance).
+template <typename F>
+__host__ void dispatch_nch(const RowSrc& src, F&& fn) {
+  if (src.part == nullptr) return fn.template operator()<0>();
+  switch (src.nchunks) {
+    case 1: return fn.template operator()<1>();
+    case 2: return fn.template operator()<2>();
+    case 3: return fn.template operator()<3>();
+    case 4: return fn.template operator()<4>();
+    case 8: return fn.template operator()<8>();
+    case 12: return fn.template operator()<12>();
+    case 16: return fn.template operator()<16>();
+    default: return fn.template operator()<-1>();
+  }
 }
 
 // ---- shared arithmetic --------------------------------------------------------------
@@ -103,7 +140,7 @@ constexpr int MAXV = 16;  // vectors per lane kept in registers between the two 
 
 // FUSED = false: out = rmsnorm(x) * w.
 // FUSED = true:  r = residual + x (fp32); residual = bf16(r); out = rmsnorm(r) * w.
-template <bool FUSED>
+template <bool FUSED, int NCH>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(RowSrc xs, uint4* __restrict__ residual,
                                                       const uint4* __restrict__ w,
                                                       uint4* __restrict__ out, int64_t rows,
@@ -122,7 +159,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(RowSrc xs, uint4* __restri
   for (int i = 0; i < MAXV; ++i) {
     if (i < per_lane && active) {
       const int c = j + i * lpr;
-      load8_src(xs, row, static_cast<int64_t>(c) * 8, v[i]);
+      load8_src<NCH>(xs, row, static_cast<int64_t>(c) * 8, v[i]);
       if constexpr (FUSED) {
         float r[8];
         load8(residual[base + c], r);
@@ -191,6 +228,7 @@ __global__ void __launch_bounds__(256) rope_kernel(uint32_t* __restrict__ q, uin
 // ---- SwiGLU -------------------------------------------------------------------------------
 
 // out = bf16(bf16(silu(gate)) * up), 8 elements per thread.
+template <int NCH>
 __global__ void __launch_bounds__(256) silu_mul_kernel(RowSrc gu, uint4* __restrict__ out,
                                                        int64_t rows, int64_t inter_vec) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -198,8 +236,8 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(RowSrc gu, uint4* __restr
   const int64_t r = i / inter_vec;
   const int64_t c = i % inter_vec;
   float g[8], u[8], y[8];
-  load8_src(gu, r, c * 8, g);
-  load8_src(gu, r, (inter_vec + c) * 8, u);
+  load8_src<NCH>(gu, r, c * 8, g);
+  load8_src<NCH>(gu, r, (inter_vec + c) * 8, u);
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = silu_mul1(g[e], u[e]);
   out[i] = store8(y);
@@ -214,6 +252,7 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(RowSrc gu, uint4* __restr
 // v heads: copied. q goes to q_out [T, HQ, 128]; k and v to the pools at slots[t].
 constexpr int QD = 128;
 
+template <int NCH>
 __global__ void __launch_bounds__(256) qkv_post_kernel(
     RowSrc src, int num_q_heads, int num_kv_heads, const uint4* __restrict__ q_norm,
     const uint4* __restrict__ k_norm, float eps, const int64_t* __restrict__ positions,
@@ -229,7 +268,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
   const bool valid = head < heads;
   const int hh = valid ? head : heads - 1;
   float v[8];
-  load8_src(src, t, static_cast<int64_t>(hh) * QD + 8 * j, v);
+  load8_src<NCH>(src, t, static_cast<int64_t>(hh) * QD + 8 * j, v);
 
   const bool is_v = hh >= num_q_heads + num_kv_heads;
   const int64_t slot = slots[t];
@@ -297,13 +336,15 @@ static int launch_rmsnorm(bool fused, RowSrc xs, void* residual, const void* w, 
   const int64_t blocks = (rows + rpb - 1) / rpb;
   SID_REQUIRE(blocks < (1ll << 31), "%s: too many rows", name);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (fused) {
-    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, xs,
-                       (uint4*)residual, (const uint4*)w, (uint4*)out, rows, hidden, lpr, eps);
-  } else {
-    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, xs,
-                       nullptr, (const uint4*)w, (uint4*)out, rows, hidden, lpr, eps);
-  }
+  dispatch_nch(xs, [&]<int NCH>() {
+    if (fused) {
+      hipLaunchKernelGGL((rmsnorm_kernel<true, NCH>), dim3((unsigned)blocks), dim3(256), 0, s, xs,
+                         (uint4*)residual, (const uint4*)w, (uint4*)out, rows, hidden, lpr, eps);
+    } else {
+      hipLaunchKernelGGL((rmsnorm_kernel<false, NCH>), dim3((unsigned)blocks), dim3(256), 0, s,
+                         xs, nullptr, (const uint4*)w, (uint4*)out, rows, hidden, lpr, eps);
+    }
+  });
   return check_launch(name);
 }
 
@@ -358,8 +399,10 @@ static int launch_silu(RowSrc gu, void* out, int64_t num_tokens, int64_t inter, 
   const int64_t total = num_tokens * (inter / 8);
   const int64_t blocks = (total + 255) / 256;
   SID_REQUIRE(blocks < (1ll << 31), "%s: too many elements", name);
-  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), gu, (uint4*)out, num_tokens, inter / 8);
+  dispatch_nch(gu, [&]<int NCH>() {
+    hipLaunchKernelGGL(silu_mul_kernel<NCH>, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), gu, (uint4*)out, num_tokens, inter / 8);
+  });
   return check_launch(name);
 }
 
@@ -396,9 +439,11 @@ extern "C" int sid_qkv_post(const void* qkv, const float* partials, int nchunks,
   const RowSrc src = partials ? part_src(partials, nchunks, num_tokens, ld) : bf_src(qkv, ld);
   const int heads = num_q_heads + 2 * num_kv_heads;
   const dim3 grid((unsigned)num_tokens, (unsigned)ceil_div(heads, 16));
-  hipLaunchKernelGGL(qkv_post_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), src,
-                     num_q_heads, num_kv_heads, (const uint4*)q_norm, (const uint4*)k_norm, eps,
-                     positions, cos_sin, max_positions, slots, (uint4*)q_out, (uint4*)k_cache,
-                     (uint4*)v_cache, num_slots);
+  dispatch_nch(src, [&]<int NCH>() {
+    hipLaunchKernelGGL(qkv_post_kernel<NCH>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       src, num_q_heads, num_kv_heads, (const uint4*)q_norm, (const uint4*)k_norm,
+                       eps, positions, cos_sin, max_positions, slots, (uint4*)q_out,
+                       (uint4*)k_cache, (uint4*)v_cache, num_slots);
+  });
   return check_launch("qkv_post");
 }

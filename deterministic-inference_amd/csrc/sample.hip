@@ -26,13 +26,37 @@ __global__ void __launch_bounds__(kThreads) argmax_kernel(const float* __restric
   const float* row = logits + r * ld;
   float bv = -INFINITY;
   int64_t bi = cols;  // sentinel larger than any index
-  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
-    const float v = row[c];
+  auto take = [&](float v, int64_t c) {
     if (better(v, c, bv, bi)) {
       bv = v;
       bi = c;
     }
+  };
+  // Vector body: 16-byte loads, UNROLL of them in flight per thread (the row start must
+  // be 16-byte aligned for this; otherwise everything goes through the scalar tail).
+  constexpr int UNROLL = 8;
+  int64_t vec_cols = 0;
+  if ((reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+    const float4* row4 = reinterpret_cast<const float4*>(row);
+    const int64_t n4 = cols / 4;
+    const int64_t step = static_cast<int64_t>(kThreads) * UNROLL;
+    int64_t base = 0;
+    for (; base + step <= n4; base += step) {
+      float4 v[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) v[u] = row4[base + u * kThreads + threadIdx.x];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int64_t c = 4 * (base + u * kThreads + threadIdx.x);
+        take(v[u].x, c);
+        take(v[u].y, c + 1);
+        take(v[u].z, c + 2);
+        take(v[u].w, c + 3);
+      }
+    }
+    vec_cols = 4 * base;
   }
+  for (int64_t c = vec_cols + threadIdx.x; c < cols; c += kThreads) take(row[c], c);
   // Wave reduction, then across waves through LDS.
   for (int mask = 1; mask < 64; mask <<= 1) {
     const float ov = lane_xor(bv, mask);

@@ -76,3 +76,18 @@ def test_partials_fold_equals_linear(m, n, k):
     for c in range(1, p.shape[0]):
         fold += p[c]
     assert torch.equal(fold.to(torch.bfloat16), linear(x, w))
+
+
+@pytest.mark.parametrize("m", [1, 16, 33, 64])
+def test_wide_lm_head_path_bitwise_matches_tiled(m):
+    """lm_head-shaped GEMMs (K=1024, huge N, M<=64) take the wide kernel; its bits equal the
+    tiled kernel's (checked on the first 128 columns computed through the tiled path)."""
+    from sid.kernels.matmul_persistent import linear
+    torch.manual_seed(6)
+    x = torch.randn(m, 1024, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(151936, 1024, device="cuda") * 0.05).to(torch.bfloat16)
+    full = linear(x, w, out_fp32=True)              # wide kernel (N/128 >= 512)
+    part = linear(x, w[:4096].contiguous(), out_fp32=True)  # tiled kernel (N/128 < 512)
+    assert torch.equal(full[:, :4096], part)
+    ref = x.float().cpu() @ w[:2048].float().cpu().t()
+    torch.testing.assert_close(full[:, :2048].cpu(), ref, atol=3e-2, rtol=2e-2)
