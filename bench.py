@@ -42,6 +42,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--attn-reps", type=int, default=4)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (launch every kernel)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run one 256 MiB device-to-device copy (known bytes) so that "
+                         "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE readings can be scaled")
     return ap.parse_args()
 
 
@@ -124,18 +127,20 @@ def attention_roofline(wl, reps):
         attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len, scale,
                      wl.invariant)
     torch.cuda.synchronize()
-    pairs = []
+    # One event pair around reps x 28 back-to-back launches on the launch stream: the
+    # average is the kernel's steady-state duration (launch overhead overlaps execution).
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    launches = 0
     for _ in range(reps):
         for layer in range(mcfg.num_layers):
             kp, vp = wl.kv.layer(layer)
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
             attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len,
                          scale, wl.invariant)
-            e.record()
-            pairs.append((s, e))
+            launches += 1
+    end.record()
     torch.cuda.synchronize()
-    avg_ms = sum(s.elapsed_time(e) for s, e in pairs) / len(pairs)
+    avg_ms = start.elapsed_time(end) / launches
     rows = int(fb.kv_indptr[-1].item())
     b = len(wl.reqs)
     bytes_launch = (rows * mcfg.num_kv_heads * mcfg.head_dim * 2 * 2   # K + V rows
@@ -144,10 +149,22 @@ def attention_roofline(wl, reps):
     wl.kv.free(wl.kv.req_to_token[[r.req_row for r in wl.reqs], [r.kv_len for r in wl.reqs]])
     achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "kernel": "decode_stage1_kernel (split-KV flash decode, 1 split at B=64)",
             "avg_launch_us": round(avg_ms * 1e3, 2), "bytes_per_launch": bytes_launch,
-            "launches_timed": len(pairs)}
+            "launches_timed": launches}
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "decode_stage1_b64_ctx2048_traffic.json"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode-attention kernel from the committed rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE runs (scaled by the copy calibration), or None."""
+    try:
+        return json.loads(TRAFFIC_FILE.read_text())["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(wl):
@@ -202,6 +219,12 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
     wl = DecodeWorkload(args.batch, args.context, args.mode, graphs=not args.eager)
+    if args.copy_calib:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     sec = time_steps(wl, args.steps, args.warmup)
     roof = attention_roofline(wl, args.attn_reps)
     base = None if args.no_cpu_baseline else cpu_baseline(wl)

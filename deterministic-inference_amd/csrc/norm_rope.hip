@@ -146,13 +146,19 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(RowSrc xs, uint4* __restri
                                                       uint4* __restrict__ out, int64_t rows,
                                                       int hidden, int lpr, float eps) {
   const int tid = threadIdx.x;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / lpr) + tid / lpr;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / lpr) + tid / lpr;
   const int j = tid % lpr;
   const int nvec = hidden / 8;
   const int per_lane = nvec / lpr;  // the host guarantees nvec % lpr == 0, per_lane <= MAXV
   const bool active = row < rows;
   const int64_t base = row * nvec;
 
+  // Weights first: independent of the row, so their latency overlaps the row loads.
+  uint4 wv[MAXV];
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    if (i < per_lane) wv[i] = w[j + i * lpr];
+  }
   float v[MAXV][8];
   float ss = 0.0f;
 #pragma unroll
@@ -179,7 +185,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(RowSrc xs, uint4* __restri
     if (i < per_lane) {
       const int c = j + i * lpr;
       float wf[8], y[8];
-      load8(w[c], wf);
+      load8(wv[i], wf);
       rms_apply8(v[i], rstd, wf, y);
       out[base + c] = store8(y);
     }
@@ -332,16 +338,20 @@ static int launch_rmsnorm(bool fused, RowSrc xs, void* residual, const void* w, 
   const int lpr = pick_lpr(hidden);
   SID_REQUIRE(hidden / 8 / lpr <= MAXV, "%s: hidden %d too large (max %d)", name, hidden,
               MAXV * 64 * 8);
-  const int rpb = 256 / lpr;
+  // Rows per block: few rows (decode) -> one 64-lane group per block, so every row gets
+  // its own workgroup and the memory requests spread over as many CUs as possible.
+  int rpb = 256 / lpr;
+  while (rpb > 1 && rows < 1024 && rpb * lpr > 64) rpb >>= 1;
+  const int threads = rpb * lpr;
   const int64_t blocks = (rows + rpb - 1) / rpb;
   SID_REQUIRE(blocks < (1ll << 31), "%s: too many rows", name);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   dispatch_nch(xs, [&]<int NCH>() {
     if (fused) {
-      hipLaunchKernelGGL((rmsnorm_kernel<true, NCH>), dim3((unsigned)blocks), dim3(256), 0, s, xs,
+      hipLaunchKernelGGL((rmsnorm_kernel<true, NCH>), dim3((unsigned)blocks), dim3(threads), 0, s, xs,
                          (uint4*)residual, (const uint4*)w, (uint4*)out, rows, hidden, lpr, eps);
     } else {
-      hipLaunchKernelGGL((rmsnorm_kernel<false, NCH>), dim3((unsigned)blocks), dim3(256), 0, s,
+      hipLaunchKernelGGL((rmsnorm_kernel<false, NCH>), dim3((unsigned)blocks), dim3(threads), 0, s,
                          xs, nullptr, (const uint4*)w, (uint4*)out, rows, hidden, lpr, eps);
     }
   });
