@@ -42,6 +42,11 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--attn-reps", type=int, default=4)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (launch every kernel)")
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5],
+                    help="BASELINE config: 3 (default) = full decode step; 1 = decode attention op; "
+                         "2 = cache write + decode attention at B=32; 4 = DVR verify pass; "
+                         "5 = continuous-batching stress")
+    ap.add_argument("--stress-requests", type=int, default=512)
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one 256 MiB device-to-device copy (known bytes) so that "
                          "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE readings can be scaled")
@@ -218,6 +223,10 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.config != 3:
+        import bench_configs
+        print(json.dumps(bench_configs.run(args)), flush=True)
+        return
     wl = DecodeWorkload(args.batch, args.context, args.mode, graphs=not args.eager)
     if args.copy_calib:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)

@@ -1,0 +1,213 @@
+"""The other BASELINE configs, run by `python bench.py --config N` (config 3, the headline
+decode step, lives in bench.py). Each returns one JSON-able dict.
+
+1  split-KV decode attention, one op: q [1,16,128], ctx 1024, page 16, 256-page pool,
+   seeded randperm block table, both split policies; vs the CPU oracle op.
+2  reshape_and_cache + decode attention at B=32, ctx ~ U[128, 4096], 32k-page x 16 pool,
+   nondet heuristic vs fixed-256; cache writes checked bit-exact.
+4  DVR verify pass on the Qwen3-0.6B shape: G=4 x W=32 over 2048-token prefixes (time per
+   pass, graph replay), plus the watched request's SHA-256 across decode batch widths 1/4/8/16.
+5  continuous batching: synthetic requests (prompt lognormal median 512 capped at 8192,
+   max_new ~ U[64, 512], seeded Gumbel-max at T=0.7, half of them is_deterministic);
+   tokens/s in dvr, nondet and batch_invariant modes.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import os
+import time
+
+import numpy as np
+import torch
+
+HQ, HKV, D = 16, 8, 128
+HBM_PEAK_GBS = 8000.0
+
+
+def _time_us(fn, reps=50, warm=5):
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps * 1e3
+
+
+def _paged(num_pages, lens, rng):
+    perm = rng.permutation(num_pages)
+    idx, off = [], 0
+    for L in lens:
+        n = -(-L // 16)
+        pages = perm[off:off + n]
+        off += n
+        pos = np.arange(L)
+        idx.append(pages[pos // 16] * 16 + pos % 16)
+    indptr = np.zeros(len(lens) + 1, dtype=np.int64)
+    indptr[1:] = np.cumsum(lens)
+    return (torch.from_numpy(np.concatenate(idx).astype(np.int32)).cuda(),
+            torch.from_numpy(indptr.astype(np.int32)).cuda())
+
+
+def _attn_case(q, k, v, indptr, idx, lens):
+    from sid.kernels.decode_attention import DecodeAttention
+    attn = DecodeAttention(len(lens), HQ, HKV, D, 32, 256, 32768, "cuda")
+    seq = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    bytes_ = sum(lens) * (HKV * D * 2 * 2 + 4) + 2 * len(lens) * HQ * D * 2
+    out = {}
+    for name, inv in (("nondet", False), ("fixed256", True)):
+        us = _time_us(lambda: attn.forward(q, k, v, indptr, idx, seq, max(lens), D ** -0.5, inv))
+        ns, grid, _ = attn.plan(seq, max(lens), inv)
+        out[name] = {"us_per_call": round(us, 2), "GB_s": round(bytes_ / us / 1e3, 1),
+                     "frac_of_hbm_peak": round(bytes_ / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "grid_splits": grid}
+    return out, attn, seq
+
+
+def config1(args):
+    from oracle.attention import decode_attention_ref
+    g = torch.Generator(device="cuda").manual_seed(1)
+    q = torch.randn(1, HQ, D, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(4096, HKV, D, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(4096, HKV, D, device="cuda", generator=g).to(torch.bfloat16)
+    idx, indptr = _paged(256, [1024], np.random.default_rng(1))
+    res, attn, seq = _attn_case(q, k, v, indptr, idx, [1024])
+    qc, kc, vc, ic, pc = q.cpu(), k.cpu(), v.cpu(), idx.cpu(), indptr.cpu()
+    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < 2.0:
+        ref = decode_attention_ref(qc, kc, vc, pc, ic, D ** -0.5)
+        n += 1
+    cpu_us = (time.perf_counter() - t0) / n * 1e6
+    o = attn.forward(q, k, v, indptr, idx, seq, 1024, D ** -0.5, False)
+    err = (o.float().cpu() - ref).abs().max().item()
+    return {"metric": "decode attention op latency, B=1 ctx 1024 page 16 (config 1)",
+            "value": res["nondet"]["us_per_call"], "unit": "us", "higher_is_better": False,
+            "policies": res, "max_abs_err_vs_oracle": err,
+            "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us", "kind": "port",
+                             "cores": torch.get_num_threads(),
+                             "sample": "oracle.attention.decode_attention_ref, same inputs"},
+            "note": "one request of 1024 tokens is launch/latency bound (4 MiB of K/V)"}
+
+
+def config2(args):
+    rng = np.random.default_rng(2)
+    lens = rng.integers(128, 4097, size=32).tolist()
+    g = torch.Generator(device="cuda").manual_seed(2)
+    slots = 32768 * 16
+    k = torch.randn(slots, HKV, D, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(slots, HKV, D, device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn(32, HQ, D, device="cuda", generator=g).to(torch.bfloat16)
+    idx, indptr = _paged(32768, lens, rng)
+    new_slots = idx[indptr[1:].long() - 1].long()
+    kn = torch.randn(32, HKV, D, device="cuda", generator=g).to(torch.bfloat16)
+    vn = torch.randn(32, HKV, D, device="cuda", generator=g).to(torch.bfloat16)
+    from sid.kernels.jit import load_ext
+    ext = load_ext()
+    us_cache = _time_us(lambda: ext.reshape_and_cache(kn, vn, k, v, new_slots))
+    exact = bool(torch.equal(k[new_slots], kn) and torch.equal(v[new_slots], vn))
+    res, _, _ = _attn_case(q, k, v, indptr, idx, lens)
+    return {"metric": "cache write + decode attention, B=32 ctx U[128,4096] (config 2)",
+            "value": res["nondet"]["GB_s"], "unit": "GB/s", "higher_is_better": True,
+            "policies": res, "sum_ctx": int(sum(lens)),
+            "reshape_and_cache": {"us_per_call": round(us_cache, 2), "bit_exact": exact,
+                                  "bytes": 32 * HKV * D * 2 * 2 * 2}}
+
+
+def _engine(mode, layers=None, pool=None, max_reqs=64, seq=4096, batch=64):
+    from sid.config import EngineConfig, Mode
+    from sid.engine.engine import Engine
+    cfg = EngineConfig(mode=Mode(mode), kv_pool_tokens=pool or 400_000, max_reqs=max_reqs,
+                       max_seq_len=seq, max_decode_batch=batch, num_layers=layers, seed=0)
+    return Engine(cfg)
+
+
+def config4(args):
+    from sid.config import SamplingParams
+    eng = _engine("dvr", pool=200_000, max_reqs=40, seq=4096, batch=32)
+    vocab = eng.runner.mcfg.vocab_size
+    g = torch.Generator().manual_seed(4)
+    prompt = lambda n: torch.randint(0, vocab, (n,), generator=g).tolist()
+    watched = prompt(2048)
+    fillers = [prompt(int(x)) for x in torch.randint(64, 2048, (15,), generator=g)]
+    hashes, stats, t_gen = {}, {}, 0.0
+    for width in (1, 4, 8, 16):
+        comp = [watched] + fillers[:width - 1]
+        params = [SamplingParams(max_new_tokens=96, temperature=0.0, is_deterministic=True,
+                                 ignore_eos=True) for _ in comp]
+        t0 = time.perf_counter()
+        out = eng.generate(comp, params)
+        t_gen += time.perf_counter() - t0
+        w = out[0]
+        hashes[width] = hashlib.sha256(str(w.token_ids).encode()).hexdigest()[:16]
+        stats[width] = {"windows": w.num_windows, "rollbacks": w.num_rollbacks}
+    # time one verify pass in isolation: G=4 requests with 2048-token prefixes
+    from sid.engine.request import RequestState
+    runner, ver = eng.runner, eng.verifier
+    reqs = []
+    for i in range(4):
+        rid = eng.add_request(prompt_ids=prompt(2048),
+                              params=SamplingParams(max_new_tokens=200, is_deterministic=True,
+                                                    ignore_eos=True))
+        reqs.append(rid)
+    # admit + prefill, then decode 40 tokens without verifying
+    new = eng.scheduler.admit()
+    for grp in eng.scheduler.prefill_groups(new):
+        eng._run_prefill(grp)
+    for _ in range(40):
+        eng._run_decode(eng.scheduler.decode_reqs())
+    group = eng.scheduler.decode_reqs()[:4]
+    fb, meta = ver.build_verify_batch(group)
+    runner.tag_verify(fb)
+
+    def one():
+        runner.sample(fb, runner.forward(fb))
+    us = _time_us(one, reps=20, warm=3)
+    return {"metric": "DVR verify pass (G=4 x W=32 over 2048-token prefixes) (config 4)",
+            "value": round(us / 1e3, 3), "unit": "ms/pass", "higher_is_better": False,
+            "verify_tokens_per_s": round(128 / (us * 1e-6), 1),
+            "sha256_watched_by_decode_width": hashes,
+            "sha256_identical": len(set(hashes.values())) == 1,
+            "watched_windows_rollbacks": stats,
+            "generate_wall_s": round(t_gen, 2)}
+
+
+def config5(args):
+    from sid.config import SamplingParams
+    n = args.stress_requests
+    rng = np.random.default_rng(5)
+    plen = np.minimum(np.maximum(rng.lognormal(np.log(512), 0.8, n).astype(int), 1), 8192)
+    max_new = rng.integers(64, 513, n)
+    det = rng.random(n) < 0.5
+    prompts = [rng.integers(0, 151936, int(p)).tolist() for p in plen]
+    results = {}
+    for mode in ("nondet", "dvr", "batch_invariant"):
+        eng = _engine(mode, pool=1_200_000, max_reqs=260, seq=9000, batch=256)
+        params = [SamplingParams(max_new_tokens=int(m), temperature=0.7, top_p=1.0, seed=i,
+                                 is_deterministic=bool(d), ignore_eos=True)
+                  for i, (m, d) in enumerate(zip(max_new, det))]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        outs = eng.generate(prompts, params)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        toks = sum(len(o.token_ids) for o in outs)
+        results[mode] = {"tokens_per_s": round(toks / dt, 1), "wall_s": round(dt, 2),
+                         "generated_tokens": toks,
+                         "rollbacks": sum(o.num_rollbacks for o in outs)}
+        del eng
+        torch.cuda.empty_cache()
+    return {"metric": f"continuous batching, {n} requests, T=0.7 (config 5)",
+            "value": results["dvr"]["tokens_per_s"], "unit": "tokens/s", "higher_is_better": True,
+            "modes": results,
+            "workload": {"prompt_median": int(np.median(plen)), "prompt_max": int(plen.max()),
+                         "max_new_mean": float(max_new.mean()), "deterministic_frac": float(det.mean())}}
+
+
+def run(args):
+    return {1: config1, 2: config2, 4: config4, 5: config5}[args.config](args)

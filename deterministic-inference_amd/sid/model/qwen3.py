@@ -22,9 +22,10 @@ from sid.kernels.rmsnorm import fused_add_rmsnorm, rmsnorm
 from sid.kernels.rope import RotaryEmbedding
 
 
-# Token counts up to this use split-K projections whose chunk partials are folded by the
-# consuming fused kernel (decode batches); larger ones (prefill) use direct GEMMs.
-SPLIT_K_MAX_TOKENS = 64
+# Token counts up to this (decode batches, the 4 x 32 DVR verify pass) use split-K
+# projections whose chunk partials are folded by the consuming fused kernel; larger ones
+# (prefill) use direct GEMMs.
+SPLIT_K_MAX_TOKENS = 128
 
 
 class Qwen3Model:
