@@ -40,6 +40,7 @@ class ForwardBatch:
     max_seq_len: int = 0                        # host-side max(seq_lens)
     qo_indptr: Optional[torch.Tensor] = None   # int32 [B+1] (extend paths)
     max_extend_len: int = 0
+    max_kv_len: int = 0                         # host-side bound of every kv length (extend)
     sample_indices: Optional[torch.Tensor] = None    # int64 [R]; None = every row
     sample_positions: Optional[torch.Tensor] = None  # int64 [R]
     temperatures: Optional[torch.Tensor] = None      # fp32 [R]
@@ -113,6 +114,7 @@ def build_prefill_batch(reqs: list, kv, device: str, invariant: bool) -> Forward
         mode=ForwardMode.PREFILL, input_ids=i64[0], positions=i64[1], out_slots=i64[2],
         qo_indptr=i32[0], kv_indptr=i32[0], kv_indices=i32[1],
         max_extend_len=max(r.prompt_len for r in reqs),
+        max_kv_len=max(r.prompt_len for r in reqs),
         sample_indices=i64[3], sample_positions=i64[4],
         temperatures=f32[0], top_ks=i64[5], top_ps=f32[1], seeds=i64[6],
         invariant=invariant, all_greedy=bool((temps == 0).all()),

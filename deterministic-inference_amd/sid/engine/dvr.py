@@ -28,6 +28,15 @@ from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.engine.request import Request
 
 
+def _bucket(n: int) -> int:
+    """Power-of-two bound (>= 512) of the longest verify sequence: the verify pass is
+    replayed as a graph per bucket, whose attention grid covers every sequence up to it."""
+    b = 512
+    while b < n:
+        b *= 2
+    return b
+
+
 class DummyPool:
     """Scratch KV slots: G*W for dummy sequences, G*(W-1) for window padding."""
 
@@ -144,6 +153,7 @@ class Verifier:
             input_ids=buf["input_ids"], positions=buf["positions"], out_slots=buf["out_slots"],
             qo_indptr=buf["qo_indptr"], kv_indptr=buf["kv_indptr"],
             kv_indices=buf["kv_indices"][:total_kv], max_extend_len=W,
+            max_kv_len=_bucket(max(kv_lens)),
             sample_indices=self._sample_indices, sample_positions=buf["sample_positions"],
             temperatures=buf["temperatures"], top_ks=buf["top_ks"], top_ps=buf["top_ps"],
             seeds=buf["seeds"], invariant=True, all_greedy=all(t == 0 for t in temps),

@@ -22,7 +22,7 @@ _SIGNATURES = {
     "sid_flash_decode_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _i32,
                              _i32, _f32, _vp, _vp, _i32, _i32, _vp, _vp],
     "sid_extend_attention_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32,
-                                 _i64, _i32, _f32, _vp, _vp],
+                                 _i64, _i32, _i32, _f32, _vp, _i64, _vp, _vp],
     "sid_rmsnorm": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
     "sid_fused_add_rmsnorm": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
     "sid_rope_apply": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _vp],
@@ -37,8 +37,9 @@ _SIGNATURES = {
     "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
     "sid_build_decode_indices": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
 }
-EXPORTED = ("sid_last_error", "sid_abi_version", *_SIGNATURES)
-ABI_VERSION = 3
+EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
+            *_SIGNATURES)
+ABI_VERSION = 4
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -67,6 +68,8 @@ class NativeLib:
         self.lib.sid_last_error.argtypes = []
         self.lib.sid_abi_version.restype = ctypes.c_int
         self.lib.sid_abi_version.argtypes = []
+        self.lib.sid_extend_attention_workspace_bytes.restype = ctypes.c_int64
+        self.lib.sid_extend_attention_workspace_bytes.argtypes = [_i32, _i64, _i32, _i32, _i32, _i32]
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.argtypes = argtypes
@@ -131,8 +134,14 @@ class NativeLib:
 
     # ---- the rest of the decode path ----------------------------------------------------
 
+    def extend_attention_workspace_bytes(self, batch, total_q, hq, hkv, max_extend_len,
+                                         max_kv_len) -> int:
+        return int(self.lib.sid_extend_attention_workspace_bytes(
+            batch, total_q, hq, hkv, max_extend_len, max_kv_len))
+
     def extend_attention_fwd(self, q, k_buffer, v_buffer, qo_indptr, kv_indptr, kv_indices,
-                             max_extend_len: int, sm_scale: float, o) -> None:
+                             max_extend_len: int, sm_scale: float, o, max_kv_len: int,
+                             workspace=None) -> None:
         _gpu(q, "q_extend", torch.bfloat16)
         _check(q.dim() == 3, "q_extend must be [Text, HQ, D]")
         _gpu(k_buffer, "k_buffer", torch.bfloat16)
@@ -145,11 +154,15 @@ class NativeLib:
         _check(qo_indptr.numel() == kv_indptr.numel(), "qo_indptr/kv_indptr length mismatch")
         _gpu(o, "o", torch.bfloat16)
         _check(o.shape == q.shape, "o must have q's shape")
+        ws_ptr, ws_bytes = None, 0
+        if workspace is not None:
+            _gpu(workspace, "workspace", torch.uint8)
+            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel()
         self._call("sid_extend_attention_fwd", q.data_ptr(), k_buffer.data_ptr(),
                    v_buffer.data_ptr(), qo_indptr.data_ptr(), kv_indptr.data_ptr(),
                    kv_indices.data_ptr(), qo_indptr.numel() - 1, q.shape[0], q.shape[1],
                    k_buffer.shape[1], q.shape[2], k_buffer.shape[0], int(max_extend_len),
-                   float(sm_scale), o.data_ptr(), _stream(q))
+                   int(max_kv_len), float(sm_scale), ws_ptr, ws_bytes, o.data_ptr(), _stream(q))
 
     def rmsnorm(self, x, w, out, eps: float) -> None:
         _gpu(x, "x", torch.bfloat16)

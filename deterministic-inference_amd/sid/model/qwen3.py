@@ -61,7 +61,8 @@ class Qwen3Model:
             if qo is None:  # decode through the extend kernel: one query per request
                 qo = torch.arange(t + 1, dtype=torch.int32, device=x.device)
             o = extend_attention_fwd(q, k_pool, v_pool, qo, fb.kv_indptr, fb.kv_indices,
-                                     max(fb.max_extend_len, 1), self.sm_scale)
+                                     max(fb.max_extend_len, 1), self.sm_scale,
+                                     max_kv_len=fb.max_kv_len or fb.max_seq_len or None)
         return o.view(t, cfg.q_size)
 
     @torch.inference_mode()

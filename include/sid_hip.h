@@ -74,16 +74,27 @@ int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache
  * bf16 [Text, HQ, D]; qo_indptr, kv_indptr int32 [B+1] (kv = prefix +
  * extend, all of it already in the pool); kv_indices int32. Query j of
  * request b sits at absolute position prefix_b + j and sees keys
- * 0 .. prefix_b + j. Key tiles are anchored at absolute position 0, so a
- * query's result depends only on its absolute position and its sequence's
- * keys (window-offset and batch-slot invariant, bit for bit).
+ * 0 .. prefix_b + j. max_kv_len: an upper bound of every request's kv length
+ * (sizes the split grid). Keys are reduced in 256-position splits anchored at
+ * absolute position 0 and folded in split order, so a query's result depends
+ * only on its absolute position and its sequence's keys (window-offset and
+ * batch-slot invariant, bit for bit). workspace (optional, any alignment of
+ * 16 bytes, sid_extend_attention_workspace_bytes(...) bytes) lets small
+ * grids give each split its own workgroup; the result is bitwise the same
+ * with or without it.
  * Replaces extend_attention_fwd, sid/kernels/extend_attention.py:115-144.
  */
 int sid_extend_attention_fwd(const void* q, const void* k_cache, const void* v_cache,
                              const int32_t* qo_indptr, const int32_t* kv_indptr,
                              const int32_t* kv_indices, int batch, int64_t total_q,
                              int num_q_heads, int num_kv_heads, int head_dim, int64_t num_slots,
-                             int max_extend_len, float sm_scale, void* o, void* stream);
+                             int max_extend_len, int max_kv_len, float sm_scale, void* workspace,
+                             int64_t workspace_bytes, void* o, void* stream);
+
+/* Workspace bytes sid_extend_attention_fwd uses for split fan-out; 0 = it does not fan out. */
+int64_t sid_extend_attention_workspace_bytes(int batch, int64_t total_q, int num_q_heads,
+                                             int num_kv_heads, int max_extend_len,
+                                             int max_kv_len);
 
 /*
  * out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w, fp32 math, bf16 I/O.

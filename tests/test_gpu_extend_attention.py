@@ -111,3 +111,32 @@ def test_decode_shape_matches_decode_kernel_numerically():
     q, kb, vb, qo, kvp, idx = _make(specs, seed=5)
     out = _fwd(q, kb, vb, qo, kvp, idx, 1, SCALE)
     assert_close_bf16(out, decode_attention_ref(q, kb, vb, kvp, idx, SCALE))
+
+
+@pytest.mark.parametrize("specs", [
+    [(2048, 32), (2049, 32), (2070, 32), (0, 32)],   # the verify shape with 2k prefixes
+    [(100, 32), (0, 17), (999, 1), (5, 64)],
+    [(0, 300)],
+], ids=str)
+def test_split_fanout_bitwise_equals_sequential_fold(specs):
+    """With a workspace the kernel gives every 256-key split its own workgroup and folds the
+    split states afterwards; without one a workgroup folds them itself: same bits."""
+    from sid.kernels.jit import load_ext
+    ext = load_ext()
+    q, kb, vb, qo, kvp, idx = _make(specs, seed=9)
+    max_e = max(e for _, e in specs)
+    max_kv = max(p + e for p, e in specs)
+    need = ext.extend_attention_workspace_bytes(len(specs), q.shape[0], HQ, HKV, max_e, max_kv)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    a = torch.empty_like(q)
+    b = torch.empty_like(q)
+    ext.extend_attention_fwd(q, kb, vb, qo, kvp, idx, max_e, SCALE, a, max_kv, ws)
+    ext.extend_attention_fwd(q, kb, vb, qo, kvp, idx, max_e, SCALE, b, max_kv, None)
+    assert torch.equal(a, b)
+    # a looser bound (more, empty splits in the grid) changes nothing either
+    ws2 = torch.empty(ext.extend_attention_workspace_bytes(len(specs), q.shape[0], HQ, HKV, max_e,
+                                                           4 * max_kv), dtype=torch.uint8, device="cuda")
+    c = torch.empty_like(q)
+    ext.extend_attention_fwd(q, kb, vb, qo, kvp, idx, max_e, SCALE, c, 4 * max_kv, ws2)
+    assert torch.equal(a, c)
