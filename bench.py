@@ -96,8 +96,7 @@ class DecodeWorkload:
 
     def step(self):
         fb = self.build()
-        logits = self.runner.forward(fb)
-        toks = self.runner.sample(fb, logits).tolist()
+        toks = self.runner.step(fb).tolist()
         # roll the state back: release this step's slots (LIFO: the next step reuses them)
         rows = [r.req_row for r in self.reqs]
         pos = [r.kv_len for r in self.reqs]

@@ -166,7 +166,7 @@ def config4(args):
     runner.tag_verify(fb)
 
     def one():
-        runner.sample(fb, runner.forward(fb))
+        runner.step(fb)
     us = _time_us(one, reps=20, warm=3)
     return {"metric": "DVR verify pass (G=4 x W=32 over 2048-token prefixes) (config 4)",
             "value": round(us / 1e3, 3), "unit": "ms/pass", "higher_is_better": False,

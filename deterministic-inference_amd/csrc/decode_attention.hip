@@ -84,11 +84,11 @@ __device__ __forceinline__ float xchg(float v) {
   }
 }
 
-template <int MASK>
-__device__ __forceinline__ void merge_with_partner(float (&m)[QPK], float (&l)[QPK],
-                                                   float (&acc)[QPK][16]) {
+template <int MASK, int NH>
+__device__ __forceinline__ void merge_with_partner(float (&m)[NH], float (&l)[NH],
+                                                   float (&acc)[NH][16]) {
 #pragma unroll
-  for (int h = 0; h < QPK; ++h) {
+  for (int h = 0; h < NH; ++h) {
     const float mo = xchg<MASK>(m[h]);
     const float lo = xchg<MASK>(l[h]);
     const float mn = fmaxf(m[h], mo);
@@ -106,10 +106,10 @@ __device__ __forceinline__ void merge_with_partner(float (&m)[QPK], float (&l)[Q
 
 // Per-iteration register state of one lane: the pool slots of its TPL tokens
 // and their K and V halves.
-template <int TPL>
+template <int TPL, int HPW>
 struct TileRegs {
-  u32x4_v k[TPL][2];
-  u32x4_v v[TPL][2];
+  u32x4_v k[TPL][HPW][2];
+  u32x4_v v[TPL][HPW][2];
 };
 
 template <bool NT>
@@ -126,10 +126,13 @@ __device__ __forceinline__ u32x4_v ld16(const u32x4_v* p) {
 // PF: software pipeline inside each wave (slot indices fetched two iterations
 // ahead, K/V rows one iteration ahead) so the index -> row dependent loads
 // are off the critical path. NT: non-temporal K/V loads (streamed once).
-// RF: request-fastest grid (blockIdx.x = request, blockIdx.y = kv head), so the
+// RF: request-fastest grid (blockIdx.x = request, blockIdx.y = kv head group), so the
 // round-robin workgroup->XCD assignment keeps all heads of a request on one XCD;
 // otherwise the kv head is fastest (every workgroup of head h on the same XCD).
-template <int NW, int TPL, bool PF, bool NT, bool RF = false>
+// HPW: kv heads per workgroup; a lane group then reads HPW adjacent 256-byte head rows
+// of a token (one contiguous HPW*256-byte run). Every head is reduced exactly as with
+// HPW = 1, so HPW does not change any bit of the result.
+template <int NW, int TPL, bool PF, bool NT, bool RF = false, int HPW = 1>
 __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ kv_indptr,
@@ -137,7 +140,8 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
     int fixed_split, float sm_scale, int num_kv_heads, int64_t num_slots, int part_stride,
     float* __restrict__ part_o, float* __restrict__ part_lse, bf16_t* __restrict__ o_direct) {
   constexpr int IT = 8 * TPL;
-  const int h_kv = RF ? blockIdx.y : blockIdx.x;
+  constexpr int NH = HPW * QPK;  // query heads handled by this workgroup
+  const int h_kv = (RF ? blockIdx.y : blockIdx.x) * HPW;  // first kv head
   const int b = RF ? blockIdx.x : blockIdx.y;
   const int split = blockIdx.z;
   const int tid = threadIdx.x;
@@ -151,15 +155,15 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   const int seq_len = kv_indptr[b + 1] - kv_base;
   const int n_splits = num_splits[b];
 
-  __shared__ float s_m[NW][QPK];
-  __shared__ float s_l[NW][QPK];
-  __shared__ float s_acc[NW][QPK][HEAD_DIM];
+  __shared__ float s_m[NW][NH];
+  __shared__ float s_l[NW][NH];
+  __shared__ float s_acc[NW][NH][HEAD_DIM];
 
   const int64_t out_row = static_cast<int64_t>(b) * num_q_heads + h_kv * QPK;
   if (n_splits <= 0 || seq_len <= 0) {
     // Empty request: stage 2 would write zeros (flash_decode.cu:246-249).
     if (o_direct != nullptr && split == 0) {
-      for (int i = tid; i < QPK * HEAD_DIM; i += NW * 64) o_direct[out_row * HEAD_DIM + i] = 0;
+      for (int i = tid; i < NH * HEAD_DIM; i += NW * 64) o_direct[out_row * HEAD_DIM + i] = 0;
     }
     return;
   }
@@ -169,20 +173,21 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   if (start >= seq_len) return;
   const int end = min(start + chunk, seq_len);
 
-  // Query pair, packed bf16: lane `sub` holds the dims it owns for both heads.
-  u32x4_v qv[QPK][2];
+  // Query heads, packed bf16: lane `sub` holds the dims it owns for every head
+  // (query head h uses kv head h / QPK of this workgroup).
+  u32x4_v qv[NH][2];
   {
     const u32x4_v* qb = reinterpret_cast<const u32x4_v*>(q + out_row * HEAD_DIM);
 #pragma unroll
-    for (int h = 0; h < QPK; ++h) {
+    for (int h = 0; h < NH; ++h) {
       qv[h][0] = qb[h * (HEAD_DIM / 8) + sub];
       qv[h][1] = qb[h * (HEAD_DIM / 8) + 8 + sub];
     }
   }
 
-  float m[QPK], l[QPK], acc[QPK][16];
+  float m[NH], l[NH], acc[NH][16];
 #pragma unroll
-  for (int h = 0; h < QPK; ++h) {
+  for (int h = 0; h < NH; ++h) {
     m[h] = NEG_BIG;
     l[h] = 0.0f;
 #pragma unroll
@@ -208,29 +213,35 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
       sl[t] = s;
     }
   };
-  auto load_rows = [&](const int64_t (&sl)[TPL], TileRegs<TPL>& r) {
+  auto load_rows = [&](const int64_t (&sl)[TPL], TileRegs<TPL, HPW>& r) {
 #pragma unroll
     for (int t = 0; t < TPL; ++t) {
-      if (sl[t] >= 0) {
-        const u32x4_v* kp = reinterpret_cast<const u32x4_v*>(kbase + sl[t] * row_stride);
-        const u32x4_v* vp = reinterpret_cast<const u32x4_v*>(vbase + sl[t] * row_stride);
-        r.k[t][0] = ld16<NT>(kp + sub);
-        r.k[t][1] = ld16<NT>(kp + 8 + sub);
-        r.v[t][0] = ld16<NT>(vp + sub);
-        r.v[t][1] = ld16<NT>(vp + 8 + sub);
-      } else {
-        r.k[t][0] = r.k[t][1] = r.v[t][0] = r.v[t][1] = u32x4_v{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) {
+        if (sl[t] >= 0) {
+          const u32x4_v* kp =
+              reinterpret_cast<const u32x4_v*>(kbase + sl[t] * row_stride + hh * HEAD_DIM);
+          const u32x4_v* vp =
+              reinterpret_cast<const u32x4_v*>(vbase + sl[t] * row_stride + hh * HEAD_DIM);
+          r.k[t][hh][0] = ld16<NT>(kp + sub);
+          r.k[t][hh][1] = ld16<NT>(kp + 8 + sub);
+          r.v[t][hh][0] = ld16<NT>(vp + sub);
+          r.v[t][hh][1] = ld16<NT>(vp + 8 + sub);
+        } else {
+          r.k[t][hh][0] = r.k[t][hh][1] = r.v[t][hh][0] = r.v[t][hh][1] = u32x4_v{0u, 0u, 0u, 0u};
+        }
       }
     }
   };
-  auto compute = [&](const int64_t (&sl)[TPL], const TileRegs<TPL>& r) {
+  auto compute = [&](const int64_t (&sl)[TPL], const TileRegs<TPL, HPW>& r) {
 #pragma unroll
-    for (int h = 0; h < QPK; ++h) {
+    for (int h = 0; h < NH; ++h) {
+      const int hh = h / QPK;
       float s[TPL];
       float tmax = NEG_BIG;
 #pragma unroll
       for (int t = 0; t < TPL; ++t) {
-        s[t] = group8_sum(dot16(qv[h], r.k[t])) * sm_scale;
+        s[t] = group8_sum(dot16(qv[h], r.k[t][hh])) * sm_scale;
         if (sl[t] >= 0) tmax = fmaxf(tmax, s[t]);
       }
       const float mn = fmaxf(m[h], tmax);
@@ -248,7 +259,7 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
 #pragma unroll
       for (int t = 0; t < TPL; ++t) {
         float vf[16];
-        unpack16(r.v[t], vf);
+        unpack16(r.v[t][hh], vf);
 #pragma unroll
         for (int d = 0; d < 16; ++d) acc[h][d] += s[t] * vf[d];
       }
@@ -258,7 +269,7 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   if constexpr (!PF) {
     for (int it = wave; it < n_it; it += NW) {
       int64_t sl[TPL];
-      TileRegs<TPL> r;
+      TileRegs<TPL, HPW> r;
       load_slots(it, sl);
       load_rows(sl, r);
       compute(sl, r);
@@ -266,7 +277,7 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   } else {
     // Two register sets A/B alternate; slots run two iterations ahead of compute.
     int64_t sa[TPL], sb[TPL], sn[TPL];
-    TileRegs<TPL> ra, rb;
+    TileRegs<TPL, HPW> ra, rb;
     int it = wave;
     load_slots(it, sa);
     load_slots(it + NW, sb);
@@ -289,13 +300,13 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   }
 
   // Merge the 8 token groups of the wave: lane ^ 8, ^ 16, ^ 32 (fixed order).
-  merge_with_partner<8>(m, l, acc);
-  merge_with_partner<16>(m, l, acc);
-  merge_with_partner<32>(m, l, acc);
+  merge_with_partner<8, NH>(m, l, acc);
+  merge_with_partner<16, NH>(m, l, acc);
+  merge_with_partner<32, NH>(m, l, acc);
 
   if (grp == 0) {
 #pragma unroll
-    for (int h = 0; h < QPK; ++h) {
+    for (int h = 0; h < NH; ++h) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         s_acc[wave][h][8 * sub + j] = acc[h][j];
@@ -310,7 +321,7 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   __syncthreads();
 
   // Merge the waves in increasing wave order; thread -> (head, dim).
-  for (int i = tid; i < QPK * HEAD_DIM; i += NW * 64) {
+  for (int i = tid; i < NH * HEAD_DIM; i += NW * 64) {
     const int h = i / HEAD_DIM;
     const int d = i % HEAD_DIM;
     float mx = s_m[0][h];
@@ -372,15 +383,21 @@ constexpr bool kPipelined = false;   // measured: no gain over 2 workgroups per 
 constexpr bool kNonTemporal = true;  // K/V rows are streamed once: +9% HBM throughput
 constexpr bool kRequestFastest = true;
 
-template <int NW, int TPL, bool PF, bool NT, bool RF = false>
+template <int NW, int TPL, bool PF, bool NT, bool RF = false, int HPW = 1>
 int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
                   int batch, int num_q_heads, int num_kv_heads, int64_t num_slots, int max_splits,
                   int fixed_split_size, float sm_scale, float* part_o, float* part_lse,
                   int part_stride, void* o, hipStream_t s) {
   const bool direct = (max_splits == 1);
-  const dim3 grid1 = RF ? dim3(batch, num_kv_heads, max_splits) : dim3(num_kv_heads, batch, max_splits);
-  hipLaunchKernelGGL((decode_stage1_kernel<NW, TPL, PF, NT, RF>), grid1, dim3(NW * 64), 0, s,
+  if (num_kv_heads % HPW != 0) {
+    set_error("flash_decode_fwd: %d kv heads not divisible by %d heads per workgroup",
+              num_kv_heads, HPW);
+    return SID_ERR_INVALID;
+  }
+  const int groups = num_kv_heads / HPW;
+  const dim3 grid1 = RF ? dim3(batch, groups, max_splits) : dim3(groups, batch, max_splits);
+  hipLaunchKernelGGL((decode_stage1_kernel<NW, TPL, PF, NT, RF, HPW>), grid1, dim3(NW * 64), 0, s,
                      (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr,
                      kv_indices, num_splits, fixed_split_size, sm_scale, num_kv_heads, num_slots,
                      part_stride, part_o, part_lse, direct ? (bf16_t*)o : nullptr);

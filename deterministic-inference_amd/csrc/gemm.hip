@@ -202,102 +202,299 @@ __global__ void __launch_bounds__(NW * 64) linear_kernel(
   }
 }
 
-// Wide-N, K = 1024, M <= 64 (lm_head at decode): every weight fragment of the workgroup's
-// 16*NW columns for all four chunks is requested up front (128 VGPRs), the whole x row
-// group is staged once in LDS (64 x 1032 bf16), then the chunks are reduced in order.
-// One workgroup per CU, 256 KiB of weights in flight per CU. Same per-element
-// arithmetic as linear_kernel, so the bits are identical.
-constexpr int WIDE_K = 1024;
-constexpr int WIDE_NCH = WIDE_K / KC;
-constexpr int WXS = WIDE_K + 8;
-
-template <int NW>
-__global__ void __launch_bounds__(NW * 64) linear_wide_kernel(
-    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
-    const bf16_t* __restrict__ bias, void* __restrict__ y, int64_t M, int64_t N, int out_fp32) {
-  extern __shared__ __align__(16) bf16_t wsx[];  // [rows16][WXS]
+// Partial mode: one 256-wide chunk per workgroup (blockIdx.y), fp32 tile written to
+// partials[chunk][row][col]. MBS (16-row blocks in the row group) is a compile-time
+// constant so the 8 x MBS MFMAs and their LDS reads are straight-line code; the chunk's
+// MFMA sequence is chunk_mfma's, so the partials are the bits linear_kernel folds.
+template <int NW, int MBS>
+__global__ void __launch_bounds__(NW * 64) linear_chunk_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w, int64_t M, int64_t N,
+    int64_t K, float* __restrict__ partials) {
+  __shared__ __align__(16) bf16_t sx[MBS * 16 * XS];
+  constexpr int RPP = NW * 2;  // x rows per pass: 32 threads per row
+  constexpr int PASSES = (MBS * 16 + RPP - 1) / RPP;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (16 * NW);
-  const int mrows = static_cast<int>(min<int64_t>(MROWS, M));
-  const int mbs = (mrows + 15) >> 4;
-  const int rows16 = mbs * 16;
-  const bf16_t* wrow = w + (n0 + 16 * wave + r) * WIDE_K + 8 * g;
-  const int col = 16 * wave + r;
+  const int c = blockIdx.y;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.z) * MROWS;
+  const int mrows = static_cast<int>(min<int64_t>(MROWS, M - m0));
+  const int64_t k0 = static_cast<int64_t>(c) * KC;
 
-  bf16x8_v wf[WIDE_NCH][NSTEP];
+  bf16x8_v wf[NSTEP];
+  load_w(wf, w + (n0 + 16 * wave + r) * K + 8 * g, k0);
+  bf16x8_v xv[PASSES];
+  const int vec = threadIdx.x & 31;
 #pragma unroll
-  for (int c = 0; c < WIDE_NCH; ++c) load_w(wf[c], wrow, static_cast<int64_t>(c) * KC);
-
-  // x: 128 16-byte vectors per row; NW*64 threads -> NW/2 rows per pass.
-  constexpr int VPT = MROWS * (WIDE_K / 8) / (NW * 64);  // vectors per thread for 64 rows
-  bf16x8_v xv[VPT];
-  const int vec = threadIdx.x & 127;
-  const int row0 = threadIdx.x >> 7;
-  constexpr int RPP = NW / 2;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int row = row0 + RPP * i;
-    if (row < rows16) {
-      const int64_t gr = min<int64_t>(row, M - 1);
-      xv[i] = ld_frag(x + gr * ldx + vec * 8);
-    }
+  for (int i = 0; i < PASSES; ++i) {
+    const int row = (threadIdx.x >> 5) + RPP * i;
+    const int64_t gr = min<int64_t>(m0 + min(row, MBS * 16 - 1), M - 1);  // clamped, discarded
+    xv[i] = ld_frag(x + gr * ldx + k0 + vec * 8);
   }
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int row = row0 + RPP * i;
-    if (row < rows16) *reinterpret_cast<bf16x8_v*>(&wsx[row * WXS + vec * 8]) = xv[i];
+  for (int i = 0; i < PASSES; ++i) {
+    const int row = (threadIdx.x >> 5) + RPP * i;
+    if (row < MBS * 16) *reinterpret_cast<bf16x8_v*>(&sx[row * XS + vec * 8]) = xv[i];
   }
   __syncthreads();
+  f32x4_v acc[MBS];
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) acc[mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb) {
+      const bf16x8_v af =
+          *reinterpret_cast<const bf16x8_v*>(&sx[(16 * mb + r) * XS + KSTEP * s + 8 * g]);
+      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[s], acc[mb], 0, 0, 0);
+    }
+  }
+  float* dst = partials + (static_cast<int64_t>(c) * M + m0) * N + n0 + 16 * wave + r;
+  if (mrows == MBS * 16) {  // full row group (uniform): unguarded stores
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[static_cast<int64_t>(16 * mb + 4 * g + i) * N] = acc[mb][i];
+    }
+    return;
+  }
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * mb + 4 * g + i;
+      if (row < mrows) dst[static_cast<int64_t>(row) * N] = acc[mb][i];
+    }
+  }
+}
 
-  f32x4_v total[4];
+// K of the streaming kernel below, its chunk count and LDS row stride of staged x.
+constexpr int WIDE_K = 1024;
+constexpr int WIDE_NCH = WIDE_K / KC;
+constexpr int WXS = WIDE_K + 8;
+
+// Streaming wide-N GEMM for K = 1024, M <= 64 (lm_head at decode), optionally with the
+// greedy argmax fused into its epilogue.
+//
+// A persistent grid of one 8-wave workgroup per CU stages the x row group in LDS once;
+// every wave then owns a contiguous run of 16-column wave tiles and streams its weights
+// chunk by chunk (16 columns x 256 k = 8 KiB per chunk) through a ring of three register
+// buffers, so two chunks are always in flight while the MFMAs of the third run. Each
+// chunk's MFMA sequence and the left fold of the four chunks are those of linear_kernel,
+// so the logits have the same bits. With ARGMAX, each lane keeps the best (value, column)
+// of the rows it holds over its wave's columns (the values compared are the bf16-rounded
+// logits the unfused path writes); the wave's best per row goes to a workspace
+// [waves][M] that argmax_finalize_kernel reduces. The (value, index) order is total
+// (torch's: larger value, then smaller index; NaN above everything, first NaN wins), so
+// the result does not depend on how the columns are split.
+constexpr int STREAM_WAVES = 8;
+
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v;
+  const bool bn = bv != bv;
+  if (vn || bn) {
+    if (vn && bn) return i < bi;
+    return vn;
+  }
+  return v > bv || (v == bv && i < bi);
+}
+
+template <int MBS, bool ARGMAX>
+__global__ void __launch_bounds__(STREAM_WAVES * 64) linear_stream_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
+    const bf16_t* __restrict__ bias, void* __restrict__ y, int M, int N, int out_fp32,
+    float* __restrict__ best_val, int* __restrict__ best_idx) {
+  extern __shared__ __align__(16) bf16_t lx[];  // [MBS*16][WXS]
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int gw = blockIdx.x * STREAM_WAVES + wave;
+  const int num_waves = gridDim.x * STREAM_WAVES;
+  const int tiles = N / 16;
+  const int t_begin = static_cast<int>(static_cast<int64_t>(gw) * tiles / num_waves);
+  const int t_end = static_cast<int>(static_cast<int64_t>(gw + 1) * tiles / num_waves);
+  const int units = (t_end - t_begin) * WIDE_NCH;
+
+  // Unit u = (tile t_begin + u/4, chunk u%4); loads past the end are clamped to the last
+  // unit (redundant, never consumed) so every issue point is unconditional.
+  auto unit_ptr = [&](int u) {
+    u = min(u, max(units - 1, 0));
+    const int64_t col = static_cast<int64_t>(t_begin + (u >> 2)) * 16 + r;
+    return w + col * WIDE_K + (u & 3) * KC + 8 * g;
+  };
+  bf16x8_v b0[NSTEP], b1[NSTEP], b2[NSTEP];
+  if (units > 0) {
+    load_w(b0, unit_ptr(0), 0);
+    load_w(b1, unit_ptr(1), 0);
+  }
+
+  // Stage x (rows >= M clamped to row M-1; their outputs are discarded).
+  constexpr int ROWS = MBS * 16;
+  constexpr int VPR = WIDE_K / 8;  // 16-byte vectors per row
+  constexpr int VPT = ROWS * VPR / (STREAM_WAVES * 64);
+  {
+    bf16x8_v xv[VPT];
 #pragma unroll
-  for (int c = 0; c < WIDE_NCH; ++c) {
-    f32x4_v acc[4];
+    for (int i = 0; i < VPT; ++i) {
+      const int v = threadIdx.x + i * STREAM_WAVES * 64;
+      const int row = v / VPR;
+      xv[i] = ld_frag(x + static_cast<int64_t>(min(row, M - 1)) * ldx + (v % VPR) * 8);
+    }
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < VPT; ++i) {
+      const int v = threadIdx.x + i * STREAM_WAVES * 64;
+      *reinterpret_cast<bf16x8_v*>(&lx[(v / VPR) * WXS + (v % VPR) * 8]) = xv[i];
+    }
+  }
+  __syncthreads();
+  // A wave without columns (N/16 < waves) still writes its (-inf, none) candidates.
+  if (!ARGMAX && units == 0) return;
+
+  f32x4_v total[MBS];
+  float bv[MBS][4];
+  int bi[MBS][4];
+  if constexpr (ARGMAX) {
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bv[mb][i] = -INFINITY;
+        bi[mb][i] = 0x7fffffff;
+      }
+    }
+  }
+
+  auto consume = [&](const bf16x8_v (&wf)[NSTEP], int u) {
+    const int c = u & 3;
+    f32x4_v acc[MBS];
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb) acc[mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        if (mb < mbs) {
-          const bf16x8_v af = *reinterpret_cast<const bf16x8_v*>(
-              &wsx[(16 * mb + r) * WXS + c * KC + KSTEP * s + 8 * g]);
-          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[c][s], acc[mb], 0, 0, 0);
-        }
+      for (int mb = 0; mb < MBS; ++mb) {
+        const bf16x8_v af = *reinterpret_cast<const bf16x8_v*>(
+            &lx[(16 * mb + r) * WXS + c * KC + KSTEP * s + 8 * g]);
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[s], acc[mb], 0, 0, 0);
       }
     }
+    if (c == 0) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      if (c == 0) {
-        total[mb] = acc[mb];
-      } else {
+      for (int mb = 0; mb < MBS; ++mb) total[mb] = acc[mb];
+    } else {
+#pragma unroll
+      for (int mb = 0; mb < MBS; ++mb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) total[mb][i] += acc[mb][i];
       }
     }
-  }
-  const float bv = bias != nullptr ? bf16_to_f32(bias[n0 + col]) : 0.0f;
+    if (c != 3) return;
+    const int col = (t_begin + (u >> 2)) * 16 + r;
+    const float bias_v = bias != nullptr ? bf16_to_f32(bias[col]) : 0.0f;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    if (mb < mbs) {
+    for (int mb = 0; mb < MBS; ++mb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 16 * mb + 4 * g + i;
-        if (row < mrows) {
-          float v = total[mb][i];
-          if (bias != nullptr) v += bv;
-          const int64_t off = static_cast<int64_t>(row) * N + n0 + col;
+        float v = total[mb][i];
+        if (bias != nullptr) v += bias_v;
+        const float vr = round_bf16(v);
+        if (y != nullptr && row < M) {
+          const int64_t off = static_cast<int64_t>(row) * N + col;
           if (out_fp32) {
-            static_cast<float*>(y)[off] = round_bf16(v);
+            static_cast<float*>(y)[off] = vr;
           } else {
             static_cast<bf16_t*>(y)[off] = f32_to_bf16(v);
           }
         }
+        if constexpr (ARGMAX) {
+          if (argmax_better(vr, col, bv[mb][i], bi[mb][i])) {
+            bv[mb][i] = vr;
+            bi[mb][i] = col;
+          }
+        }
       }
     }
+  };
+
+  for (int u = 0; u < units; u += 3) {
+    load_w(b2, unit_ptr(u + 2), 0);
+    consume(b0, u);
+    load_w(b0, unit_ptr(u + 3), 0);
+    if (u + 1 < units) consume(b1, u + 1);
+    load_w(b1, unit_ptr(u + 4), 0);
+    if (u + 2 < units) consume(b2, u + 2);
+  }
+
+  if constexpr (ARGMAX) {
+    // Best over the 16 column lanes of each row (lanes r = 0..15 of a row group g).
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = bv[mb][i];
+        int ix = bi[mb][i];
+#pragma unroll
+        for (int mask = 1; mask < 16; mask <<= 1) {
+          const float ov = lane_xor(v, mask);
+          const int oi = __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, ix);
+          if (argmax_better(ov, oi, v, ix)) {
+            v = ov;
+            ix = oi;
+          }
+        }
+        const int row = 16 * mb + 4 * g + i;
+        if (r == 0 && row < M) {
+          best_val[static_cast<int64_t>(gw) * M + row] = v;
+          best_idx[static_cast<int64_t>(gw) * M + row] = ix;
+        }
+      }
+    }
+  }
+}
+
+// Per row: the best of the per-wave candidates (any order gives the same answer).
+__global__ void __launch_bounds__(256) argmax_finalize_kernel(const float* __restrict__ best_val,
+                                                              const int* __restrict__ best_idx,
+                                                              int num_waves, int M,
+                                                              int64_t* __restrict__ out) {
+  const int row = blockIdx.x;
+  float v = -INFINITY;
+  int ix = 0x7fffffff;
+  for (int wv = threadIdx.x; wv < num_waves; wv += 256) {
+    const float cv = best_val[static_cast<int64_t>(wv) * M + row];
+    const int ci = best_idx[static_cast<int64_t>(wv) * M + row];
+    if (argmax_better(cv, ci, v, ix)) {
+      v = cv;
+      ix = ci;
+    }
+  }
+  for (int mask = 1; mask < 64; mask <<= 1) {
+    const float ov = lane_xor(v, mask);
+    const int oi = __builtin_amdgcn_ds_bpermute((__lane_id() ^ mask) << 2, ix);
+    if (argmax_better(ov, oi, v, ix)) {
+      v = ov;
+      ix = oi;
+    }
+  }
+  __shared__ float s_v[4];
+  __shared__ int s_i[4];
+  if ((threadIdx.x & 63) == 0) {
+    s_v[threadIdx.x >> 6] = v;
+    s_i[threadIdx.x >> 6] = ix;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 4; ++k) {
+      if (argmax_better(s_v[k], s_i[k], v, ix)) {
+        v = s_v[k];
+        ix = s_i[k];
+      }
+    }
+    out[row] = ix == 0x7fffffff ? 0 : ix;
   }
 }
 
@@ -344,6 +541,53 @@ void launch_any(int nw, const void* x, int64_t ldx, const void* w, const void* b
   }
 }
 
+// The streaming kernel serves sid_linear from this many columns up (lm_head-sized N).
+constexpr int64_t kStreamMinN = 32768;
+
+// Persistent-grid size of the streaming kernel: one workgroup per CU of the current device.
+int stream_grid() {
+  static int count[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (count[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    count[dev] = n;
+  }
+  return count[dev];
+}
+
+bool stream_shape_ok(int64_t m, int64_t n, int64_t k) {
+  return m >= 1 && m <= MROWS && k == WIDE_K && n % 16 == 0 && n < (1ll << 31);
+}
+
+template <int MBS, bool AM>
+void launch_stream_mbs(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int m,
+                       int n, int out_fp32, float* bv, int* bi, hipStream_t s) {
+  const size_t lds = static_cast<size_t>(MBS * 16) * WXS * sizeof(bf16_t);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_stream_kernel<MBS, AM>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((linear_stream_kernel<MBS, AM>), dim3(stream_grid()),
+                     dim3(STREAM_WAVES * 64), lds, s, (const bf16_t*)x, ldx, (const bf16_t*)w,
+                     (const bf16_t*)bias, y, m, n, out_fp32, bv, bi);
+}
+
+template <bool AM>
+void launch_stream(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int m,
+                   int n, int out_fp32, float* bv, int* bi, hipStream_t s) {
+  switch ((m + 15) / 16) {
+    case 1: return launch_stream_mbs<1, AM>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, s);
+    case 2: return launch_stream_mbs<2, AM>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, s);
+    case 3: return launch_stream_mbs<3, AM>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, s);
+    default: return launch_stream_mbs<4, AM>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, s);
+  }
+}
+
 }  // namespace
 }  // namespace sid
 
@@ -357,18 +601,9 @@ extern "C" int sid_linear(const void* x, int64_t ldx, const void* w, const void*
   int rc = check_shapes(x, ldx, w, m, n, k, "linear");
   if (rc != SID_OK) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (m <= MROWS && k == WIDE_K && n % 128 == 0 && n / 128 >= 512) {
-    static bool lds_ok = false;
-    const size_t lds = static_cast<size_t>(MROWS) * WXS * sizeof(bf16_t);
-    if (!lds_ok) {
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_wide_kernel<8>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-      lds_ok = true;
-    }
-    const size_t lds_used = static_cast<size_t>((m + 15) / 16 * 16) * WXS * sizeof(bf16_t);
-    hipLaunchKernelGGL(linear_wide_kernel<8>, dim3((unsigned)(n / 128)), dim3(512), lds_used, s,
-                       (const bf16_t*)x, ldx, (const bf16_t*)w, (const bf16_t*)bias, y, m, n,
-                       out_fp32);
+  if (stream_shape_ok(m, n, k) && n >= kStreamMinN) {
+    launch_stream<false>(x, ldx, w, bias, y, static_cast<int>(m), static_cast<int>(n), out_fp32,
+                         nullptr, nullptr, s);
     return check_launch("linear");
   }
   launch_any(pick_waves(n, m, false), x, ldx, w, bias, y, m, n, k, out_fp32, nullptr, s);
@@ -383,7 +618,54 @@ extern "C" int sid_linear_partials(const void* x, int64_t ldx, const void* w, fl
   int rc = check_shapes(x, ldx, w, m, n, k, "linear_partials");
   if (rc != SID_OK) return rc;
   SID_REQUIRE(k / KC <= 65535, "linear_partials: too many chunks");
-  launch_any(pick_waves(n, m, true), x, ldx, w, nullptr, nullptr, m, n, k, 0, partials,
-             static_cast<hipStream_t>(stream));
+  // Row groups of 64; a single group smaller than 64 rows gets the matching MBS.
+  const int mbs = m >= MROWS ? 4 : static_cast<int>((m + 15) / 16);
+  const dim3 grid((unsigned)(n / 64), (unsigned)(k / KC), (unsigned)((m + MROWS - 1) / MROWS));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, (const bf16_t*)x, ldx, (const bf16_t*)w, m, n, k,
+                       partials);
+  };
+  switch (mbs) {
+    case 1: go(linear_chunk_kernel<4, 1>); break;
+    case 2: go(linear_chunk_kernel<4, 2>); break;
+    case 3: go(linear_chunk_kernel<4, 3>); break;
+    default: go(linear_chunk_kernel<4, 4>); break;
+  }
   return check_launch("linear_partials");
+}
+
+extern "C" int64_t sid_linear_argmax_workspace_bytes(int64_t m) {
+  if (m < 1 || m > MROWS) return 0;
+  return static_cast<int64_t>(stream_grid()) * STREAM_WAVES * m * (sizeof(float) + sizeof(int));
+}
+
+extern "C" int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bias,
+                                 float* logits, int64_t m, int64_t n, int64_t k, void* workspace,
+                                 int64_t workspace_bytes, int64_t* out_idx, void* stream) {
+  SID_REQUIRE(m >= 0 && n >= 0 && k >= 0, "linear_argmax: negative size");
+  if (m == 0) return SID_OK;
+  SID_REQUIRE(n > 0, "linear_argmax: no columns");
+  SID_REQUIRE(out_idx != nullptr && workspace != nullptr, "linear_argmax: null pointer");
+  int rc = check_shapes(x, ldx, w, m, n, k, "linear_argmax");
+  if (rc != SID_OK) return rc;
+  SID_REQUIRE(stream_shape_ok(m, n, k),
+              "linear_argmax: needs 1 <= M <= %d and K == %d (got M=%lld, K=%lld)", MROWS, WIDE_K,
+              (long long)m, (long long)k);
+  const int64_t need = sid_linear_argmax_workspace_bytes(m);
+  SID_REQUIRE(workspace_bytes >= need, "linear_argmax: workspace %lld bytes, need %lld",
+              (long long)workspace_bytes, (long long)need);
+  SID_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+              "linear_argmax: workspace must be 16-byte aligned");
+  const int waves = stream_grid() * STREAM_WAVES;
+  float* bv = static_cast<float*>(workspace);
+  int* bi = reinterpret_cast<int*>(bv + static_cast<int64_t>(waves) * m);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  launch_stream<true>(x, ldx, w, bias, logits, static_cast<int>(m), static_cast<int>(n), 1, bv, bi,
+                      s);
+  rc = check_launch("linear_argmax");
+  if (rc != SID_OK) return rc;
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(256), 0, s, bv, bi, waves,
+                     static_cast<int>(m), out_idx);
+  return check_launch("linear_argmax finalize");
 }

@@ -192,6 +192,95 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(RowSrc xs, uint4* __restri
   }
 }
 
+// Few rows (decode): one 256-thread workgroup per row. Pass 1 spreads the memory work
+// (chunk fold, residual add) over all 256 threads, 4 columns each, into an fp32 row in
+// LDS; pass 2 reduces the sum of squares with exactly the lane layout and order of
+// rmsnorm_kernel (lpr lanes, lane j owning vectors j + i*lpr, sequential fmaf, then the
+// xor butterfly), so both kernels produce identical bits and either may serve any row.
+template <int NCH>
+__device__ __forceinline__ void load4_src(const RowSrc& s, int64_t row, int64_t col, float (&f)[4]) {
+  if constexpr (NCH == 0) {
+    const uint2 u = *reinterpret_cast<const uint2*>(s.bf + row * s.ld + col);
+    f[0] = bf16_lo(u.x); f[1] = bf16_hi(u.x); f[2] = bf16_lo(u.y); f[3] = bf16_hi(u.y);
+    return;
+  } else {
+    const float* p = s.part + row * s.ld + col;
+    if constexpr (NCH > 0) {
+      float4 a[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) a[c] = *reinterpret_cast<const float4*>(p + c * s.chunk_stride);
+      f[0] = a[0].x; f[1] = a[0].y; f[2] = a[0].z; f[3] = a[0].w;
+#pragma unroll
+      for (int c = 1; c < NCH; ++c) {
+        f[0] += a[c].x; f[1] += a[c].y; f[2] += a[c].z; f[3] += a[c].w;
+      }
+    } else {
+      float4 a = *reinterpret_cast<const float4*>(p);
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+      for (int c = 1; c < s.nchunks; ++c) {
+        p += s.chunk_stride;
+        a = *reinterpret_cast<const float4*>(p);
+        f[0] += a.x; f[1] += a.y; f[2] += a.z; f[3] += a.w;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = round_bf16(f[e]);
+  }
+}
+
+constexpr int ROWBLOCK_THREADS = 256;
+
+template <bool FUSED, int NCH>
+__global__ void __launch_bounds__(ROWBLOCK_THREADS) rmsnorm_rowblock_kernel(
+    RowSrc xs, uint2* __restrict__ residual, const uint2* __restrict__ w, uint2* __restrict__ out,
+    int hidden, int lpr, float eps) {
+  extern __shared__ float srow[];  // [hidden] fp32 row, then rstd
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int nq = hidden / 4;
+  const int64_t base = row * nq;
+  for (int u = tid; u < nq; u += ROWBLOCK_THREADS) {
+    float v[4];
+    load4_src<NCH>(xs, row, static_cast<int64_t>(u) * 4, v);
+    if constexpr (FUSED) {
+      const uint2 r = residual[base + u];
+      v[0] = bf16_lo(r.x) + v[0];
+      v[1] = bf16_hi(r.x) + v[1];
+      v[2] = bf16_lo(r.y) + v[2];
+      v[3] = bf16_hi(r.y) + v[3];
+      residual[base + u] = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+    *reinterpret_cast<float4*>(&srow[4 * u]) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int per_lane = hidden / 8 / lpr;
+    float ss = 0.0f;
+    if (tid < lpr) {
+      for (int i = 0; i < per_lane; ++i) {
+        const int c = tid + i * lpr;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = srow[8 * c + e];
+        ss = sumsq8(v, ss);
+      }
+    }
+    ss = group_sum(ss, lpr);
+    if (tid == 0) srow[hidden] = rms_rstd(ss, hidden, eps);
+  }
+  __syncthreads();
+  const float rstd = srow[hidden];
+  for (int u = tid; u < nq; u += ROWBLOCK_THREADS) {
+    const float4 v = *reinterpret_cast<const float4*>(&srow[4 * u]);
+    const uint2 wu = w[u];
+    const float y0 = (v.x * rstd) * bf16_lo(wu.x);
+    const float y1 = (v.y * rstd) * bf16_hi(wu.x);
+    const float y2 = (v.z * rstd) * bf16_lo(wu.y);
+    const float y3 = (v.w * rstd) * bf16_hi(wu.y);
+    out[base + u] = make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
+  }
+}
+
 int pick_lpr(int hidden) {
   const int nvec = hidden / 8;
   int lpr = 64;
@@ -233,40 +322,41 @@ __global__ void __launch_bounds__(256) rope_kernel(uint32_t* __restrict__ q, uin
 
 // ---- SwiGLU -------------------------------------------------------------------------------
 
-// out = bf16(bf16(silu(gate)) * up), 8 elements per thread.
+// out = bf16(bf16(silu(gate)) * up), 4 elements per thread (many small workgroups, so a
+// decode batch's few MB of chunk partials are read by every CU).
 template <int NCH>
-__global__ void __launch_bounds__(256) silu_mul_kernel(RowSrc gu, uint4* __restrict__ out,
-                                                       int64_t rows, int64_t inter_vec) {
+__global__ void __launch_bounds__(128) silu_mul_kernel(RowSrc gu, uint2* __restrict__ out,
+                                                       int64_t rows, int64_t inter_q) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= rows * inter_vec) return;
-  const int64_t r = i / inter_vec;
-  const int64_t c = i % inter_vec;
-  float g[8], u[8], y[8];
-  load8_src<NCH>(gu, r, c * 8, g);
-  load8_src<NCH>(gu, r, (inter_vec + c) * 8, u);
+  if (i >= rows * inter_q) return;
+  const int64_t r = i / inter_q;
+  const int64_t c = i % inter_q;
+  float g[4], u[4], y[4];
+  load4_src<NCH>(gu, r, c * 4, g);
+  load4_src<NCH>(gu, r, (inter_q + c) * 4, u);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = silu_mul1(g[e], u[e]);
-  out[i] = store8(y);
+  for (int e = 0; e < 4; ++e) y[e] = silu_mul1(g[e], u[e]);
+  out[i] = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
 }
 
 // ---- fused QKV epilogue -------------------------------------------------------------------
 
 // Row t of the projection is [q (HQ*128) | k (HKV*128) | v (HKV*128)]. A head is
 // handled by 16 lanes (lane j: dims 8j..8j+7, which is rmsnorm_kernel's layout for
-// hidden 128), 16 heads per block. q/k heads: per-head RMSNorm, round, RoPE (the
+// hidden 128), 8 heads per 128-thread block. q/k heads: per-head RMSNorm, round, RoPE (the
 // rotate-half partner of lane j is lane j ^ 8, one DPP row_ror:8 away), round;
 // v heads: copied. q goes to q_out [T, HQ, 128]; k and v to the pools at slots[t].
 constexpr int QD = 128;
 
 template <int NCH>
-__global__ void __launch_bounds__(256) qkv_post_kernel(
+__global__ void __launch_bounds__(128) qkv_post_kernel(
     RowSrc src, int num_q_heads, int num_kv_heads, const uint4* __restrict__ q_norm,
     const uint4* __restrict__ k_norm, float eps, const int64_t* __restrict__ positions,
     const float* __restrict__ cos_sin, int64_t max_positions, const int64_t* __restrict__ slots,
     uint4* __restrict__ q_out, uint4* __restrict__ k_cache, uint4* __restrict__ v_cache,
     int64_t num_slots) {
   const int64_t t = blockIdx.x;
-  const int head = blockIdx.y * 16 + (threadIdx.x >> 4);
+  const int head = blockIdx.y * 8 + (threadIdx.x >> 4);
   const int j = threadIdx.x & 15;
   const int heads = num_q_heads + 2 * num_kv_heads;
   // Whole 16-lane groups are uniform; the DPP/bpermute below needs every lane of a
@@ -328,6 +418,9 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
 
 using namespace sid;
 
+// Below this many rows the one-workgroup-per-row kernel is used.
+constexpr int64_t kRowBlockBelow = 1024;
+
 static int launch_rmsnorm(bool fused, RowSrc xs, void* residual, const void* w, void* out,
                           int64_t rows, int hidden, float eps, void* stream, const char* name) {
   SID_REQUIRE(rows >= 0, "%s: negative rows", name);
@@ -338,14 +431,27 @@ static int launch_rmsnorm(bool fused, RowSrc xs, void* residual, const void* w, 
   const int lpr = pick_lpr(hidden);
   SID_REQUIRE(hidden / 8 / lpr <= MAXV, "%s: hidden %d too large (max %d)", name, hidden,
               MAXV * 64 * 8);
-  // Rows per block: few rows (decode) -> one 64-lane group per block, so every row gets
-  // its own workgroup and the memory requests spread over as many CUs as possible.
-  int rpb = 256 / lpr;
-  while (rpb > 1 && rows < 1024 && rpb * lpr > 64) rpb >>= 1;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rows < kRowBlockBelow) {
+    // Decode-sized batches: a 256-thread workgroup per row (identical bits).
+    const size_t lds = (static_cast<size_t>(hidden) + 4) * sizeof(float);
+    dispatch_nch(xs, [&]<int NCH>() {
+      if (fused) {
+        hipLaunchKernelGGL((rmsnorm_rowblock_kernel<true, NCH>), dim3((unsigned)rows),
+                           dim3(ROWBLOCK_THREADS), lds, s, xs, (uint2*)residual, (const uint2*)w,
+                           (uint2*)out, hidden, lpr, eps);
+      } else {
+        hipLaunchKernelGGL((rmsnorm_rowblock_kernel<false, NCH>), dim3((unsigned)rows),
+                           dim3(ROWBLOCK_THREADS), lds, s, xs, nullptr, (const uint2*)w,
+                           (uint2*)out, hidden, lpr, eps);
+      }
+    });
+    return check_launch(name);
+  }
+  const int rpb = 256 / lpr;
   const int threads = rpb * lpr;
   const int64_t blocks = (rows + rpb - 1) / rpb;
   SID_REQUIRE(blocks < (1ll << 31), "%s: too many rows", name);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
   dispatch_nch(xs, [&]<int NCH>() {
     if (fused) {
       hipLaunchKernelGGL((rmsnorm_kernel<true, NCH>), dim3((unsigned)blocks), dim3(threads), 0, s, xs,
@@ -406,12 +512,12 @@ static int launch_silu(RowSrc gu, void* out, int64_t num_tokens, int64_t inter, 
   if (num_tokens == 0) return SID_OK;
   SID_REQUIRE((gu.bf || gu.part) && out, "%s: null pointer", name);
   SID_REQUIRE(inter > 0 && inter % 8 == 0, "%s: intermediate size must be a multiple of 8", name);
-  const int64_t total = num_tokens * (inter / 8);
-  const int64_t blocks = (total + 255) / 256;
+  const int64_t total = num_tokens * (inter / 4);
+  const int64_t blocks = (total + 127) / 128;
   SID_REQUIRE(blocks < (1ll << 31), "%s: too many elements", name);
   dispatch_nch(gu, [&]<int NCH>() {
-    hipLaunchKernelGGL(silu_mul_kernel<NCH>, dim3((unsigned)blocks), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), gu, (uint4*)out, num_tokens, inter / 8);
+    hipLaunchKernelGGL(silu_mul_kernel<NCH>, dim3((unsigned)blocks), dim3(128), 0,
+                       static_cast<hipStream_t>(stream), gu, (uint2*)out, num_tokens, inter / 4);
   });
   return check_launch(name);
 }
@@ -448,9 +554,9 @@ extern "C" int sid_qkv_post(const void* qkv, const float* partials, int nchunks,
   const int64_t ld = static_cast<int64_t>(num_q_heads + 2 * num_kv_heads) * QD;
   const RowSrc src = partials ? part_src(partials, nchunks, num_tokens, ld) : bf_src(qkv, ld);
   const int heads = num_q_heads + 2 * num_kv_heads;
-  const dim3 grid((unsigned)num_tokens, (unsigned)ceil_div(heads, 16));
+  const dim3 grid((unsigned)num_tokens, (unsigned)ceil_div(heads, 8));
   dispatch_nch(src, [&]<int NCH>() {
-    hipLaunchKernelGGL(qkv_post_kernel<NCH>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+    hipLaunchKernelGGL(qkv_post_kernel<NCH>, grid, dim3(128), 0, static_cast<hipStream_t>(stream),
                        src, num_q_heads, num_kv_heads, (const uint4*)q_norm, (const uint4*)k_norm,
                        eps, positions, cos_sin, max_positions, slots, (uint4*)q_out,
                        (uint4*)k_cache, (uint4*)v_cache, num_slots);

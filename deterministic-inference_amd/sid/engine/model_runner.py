@@ -76,14 +76,22 @@ class ModelRunner:
             "kv_indices": z(g * (cfg.max_seq_len + cfg.dvr_window_size), torch.int32),
         }
 
-    def forward(self, fb: ForwardBatch) -> torch.Tensor:
+    def forward(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
+        """Logits of the sampled rows, or (greedy=True) their greedy tokens."""
         if self.graphs is not None and fb.graph_key is not None:
-            return self.graphs.run(fb)
-        return self._forward_eager(fb)
+            return self.graphs.run(fb, greedy)
+        return self._forward_eager(fb, greedy)
 
-    def _forward_eager(self, fb: ForwardBatch) -> torch.Tensor:
+    def _forward_eager(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
         return self.model.forward(fb, self.kv_cache, self.decode_attn,
-                                  decode_backend=self.cfg.decode_backend)
+                                  decode_backend=self.cfg.decode_backend, greedy=greedy)
+
+    def step(self, fb: ForwardBatch) -> torch.Tensor:
+        """forward + sample -> int64 tokens [R]. An all-greedy batch takes the fused
+        lm_head + argmax path (same tokens as sampling the logits; no logits written)."""
+        if fb.all_greedy:
+            return self.forward(fb, greedy=True)
+        return self.sample(fb, self.forward(fb))
 
     def prepare_decode(self, reqs: list, invariant: bool) -> ForwardBatch:
         """build_decode_batch, into the graph-static buffers when graphs are enabled."""
@@ -128,26 +136,27 @@ class GraphCache:
         self.decode_static = DecodeStatic(cfg.max_decode_batch,
                                           cfg.max_decode_batch * cfg.max_seq_len, runner.device)
 
-    def run(self, fb: ForwardBatch) -> torch.Tensor:
-        entry = self.graphs.get(fb.graph_key)
+    def run(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
+        key = (fb.graph_key, greedy)
+        entry = self.graphs.get(key)
         if entry is None:
-            entry = self._capture(fb)
-            self.graphs[fb.graph_key] = entry
+            entry = self._capture(fb, greedy)
+            self.graphs[key] = entry
             while len(self.graphs) > self.max_graphs:
                 self.graphs.popitem(last=False)
         else:
-            self.graphs.move_to_end(fb.graph_key)
-        graph, logits = entry
+            self.graphs.move_to_end(key)
+        graph, out = entry
         graph.replay()
-        return logits
+        return out
 
-    def _capture(self, fb: ForwardBatch):
+    def _capture(self, fb: ForwardBatch, greedy: bool):
         runner = self.runner
         # One eager pass first (lazy initialisation inside torch ops happens outside the
         # capture); it computes exactly what the replay will recompute.
-        runner._forward_eager(fb)
+        runner._forward_eager(fb, greedy)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self.pool):
-            logits = runner._forward_eager(fb)
-        return graph, logits
+            out = runner._forward_eager(fb, greedy)
+        return graph, out

@@ -36,10 +36,11 @@ _SIGNATURES = {
     "sid_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
     "sid_build_decode_indices": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
+    "sid_linear_argmax": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
 }
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
-            *_SIGNATURES)
-ABI_VERSION = 4
+            "sid_linear_argmax_workspace_bytes", *_SIGNATURES)
+ABI_VERSION = 5
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -70,6 +71,8 @@ class NativeLib:
         self.lib.sid_abi_version.argtypes = []
         self.lib.sid_extend_attention_workspace_bytes.restype = ctypes.c_int64
         self.lib.sid_extend_attention_workspace_bytes.argtypes = [_i32, _i64, _i32, _i32, _i32, _i32]
+        self.lib.sid_linear_argmax_workspace_bytes.restype = ctypes.c_int64
+        self.lib.sid_linear_argmax_workspace_bytes.argtypes = [_i64]
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.argtypes = argtypes
@@ -211,6 +214,26 @@ class NativeLib:
         _check(tuple(partials.shape) == (k // 256, m, n), "partials must be [K/256, M, N]")
         self._call("sid_linear_partials", x.data_ptr(), x.stride(0) if m > 1 else k,
                    w.data_ptr(), partials.data_ptr(), m, n, k, _stream(x))
+
+    def linear_argmax_workspace_bytes(self, m: int) -> int:
+        return int(self.lib.sid_linear_argmax_workspace_bytes(m))
+
+    def linear_argmax(self, x, w, bias, logits, workspace, out) -> None:
+        m, k, n = self._linear_check(x, w)
+        if bias is not None:
+            _gpu(bias, "bias", torch.bfloat16)
+            _check(bias.numel() == n, "bias must have N entries")
+        if logits is not None:
+            _gpu(logits, "logits", torch.float32)
+            _check(tuple(logits.shape) == (m, n), "logits must be [M, N]")
+        _gpu(workspace, "workspace")
+        _gpu(out, "out", torch.int64)
+        _check(out.numel() == m, "out must have M entries")
+        self._call("sid_linear_argmax", x.data_ptr(), x.stride(0) if m > 1 else k, w.data_ptr(),
+                   bias.data_ptr() if bias is not None else None,
+                   logits.data_ptr() if logits is not None else None, m, n, k,
+                   workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                   out.data_ptr(), _stream(x))
 
     @staticmethod
     def _linear_check(x, w):

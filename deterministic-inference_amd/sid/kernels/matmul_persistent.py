@@ -59,3 +59,26 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor,
         out = torch.empty(k // 256, m, n, dtype=torch.float32, device=x.device)
     load_ext().linear_partials(x, weight, out)
     return out
+
+
+def linear_argmax_supported(m: int, k: int) -> bool:
+    """Shapes the fused lm_head + greedy argmax kernel takes (decode-sized M, K = 1024)."""
+    return 1 <= m <= 64 and k == 1024
+
+
+def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                  logits: Optional[torch.Tensor] = None,
+                  workspace: Optional[torch.Tensor] = None,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """argmax(x @ weight^T + bias, dim=-1) as int64 [M], the logits being exactly those of
+    linear(..., out_fp32=True) (written to `logits` when given). Greedy sampling fused into
+    the lm_head GEMM; needs linear_argmax_supported(M, K)."""
+    m, k = x.shape
+    ext = load_ext()
+    if workspace is None:
+        workspace = torch.empty(ext.linear_argmax_workspace_bytes(m), dtype=torch.uint8,
+                                device=x.device)
+    if out is None:
+        out = torch.empty(m, dtype=torch.int64, device=x.device)
+    ext.linear_argmax(x, weight, bias, logits, workspace, out)
+    return out

@@ -15,8 +15,9 @@ import torch
 from sid.config import ModelConfig
 from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.kernels.extend_attention import extend_attention_fwd
-from sid.kernels.matmul_persistent import linear, linear_partials
-from sid.kernels.ops import (embedding, fused_add_rmsnorm_partials, gather_rows, qkv_post,
+from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_supported,
+                                            linear_partials)
+from sid.kernels.ops import (argmax_rows, embedding, fused_add_rmsnorm_partials, gather_rows, qkv_post,
                              silu_mul, silu_mul_partials)
 from sid.kernels.rmsnorm import fused_add_rmsnorm, rmsnorm
 from sid.kernels.rope import RotaryEmbedding
@@ -67,8 +68,10 @@ class Qwen3Model:
 
     @torch.inference_mode()
     def forward(self, fb: ForwardBatch, kv_cache, decode_attn,
-                decode_backend: str = "hip") -> torch.Tensor:
-        """fp32 logits [R, vocab] for the sampled rows (bf16-rounded values).
+                decode_backend: str = "hip", greedy: bool = False) -> torch.Tensor:
+        """fp32 logits [R, vocab] for the sampled rows (bf16-rounded values); with
+        greedy=True, the greedy tokens int64 [R] instead (argmax of those logits, fused into
+        the lm_head GEMM for decode-sized R).
 
         Same op order as sid/model/qwen3.py:88-115; the residual add + RMSNorm that follows
         each o / down projection consumes the projection directly (fused), and the down
@@ -98,4 +101,8 @@ class Qwen3Model:
             else:
                 x, residual = fused_add_rmsnorm(linear(act, lw["down"]), residual, next_w, eps)
         rows = x if fb.sample_indices is None else gather_rows(x, fb.sample_indices)
+        if greedy:
+            if linear_argmax_supported(rows.shape[0], rows.shape[1]):
+                return linear_argmax(rows, self.w["lm_head"])
+            return argmax_rows(linear(rows, self.w["lm_head"], out_fp32=True))
         return linear(rows, self.w["lm_head"], out_fp32=True)

@@ -201,6 +201,20 @@ int sid_gather_rows(const void* table, const int64_t* idx, void* out, int64_t n,
                     int64_t row_elems, int64_t table_rows, void* stream);
 
 /*
+ * Greedy lm_head: out_idx[r] = argmax over columns of (x @ w^T + bias)[r, :],
+ * the logits taken as sid_linear computes them (bf16-rounded, fp32 storage)
+ * and compared with sid_argmax_rows's order. Fuses the lm_head projection
+ * (sid/model/qwen3.py:114-115) with the greedy branch of sample()
+ * (sid/engine/sampler.py:38) for an all-greedy batch. logits may be NULL (not
+ * written) or fp32 [M, N]. Needs 1 <= M <= 64, K == 1024; workspace of
+ * sid_linear_argmax_workspace_bytes(M) bytes, 16-byte aligned.
+ */
+int64_t sid_linear_argmax_workspace_bytes(int64_t m);
+int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bias, float* logits,
+                      int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                      int64_t* out_idx, void* stream);
+
+/*
  * out[r] = argmax(logits[r, :]) with first-index tie-break; fp32 logits
  * [rows, cols] with row stride ld; out int64 [rows]. NaN compares greater
  * than every number (torch.argmax semantics). Replaces the greedy branch of

@@ -79,15 +79,60 @@ def test_partials_fold_equals_linear(m, n, k):
 
 
 @pytest.mark.parametrize("m", [1, 16, 33, 64])
-def test_wide_lm_head_path_bitwise_matches_tiled(m):
-    """lm_head-shaped GEMMs (K=1024, huge N, M<=64) take the wide kernel; its bits equal the
-    tiled kernel's (checked on the first 128 columns computed through the tiled path)."""
+def test_stream_lm_head_path_bitwise_matches_tiled(m):
+    """lm_head-shaped GEMMs (K=1024, N >= 32768, M<=64) take the persistent streaming kernel;
+    its bits equal the tiled kernel's (checked on the first and last 4096 columns, which
+    the tiled kernel computes separately), for fp32 and bf16 outputs."""
     from sid.kernels.matmul_persistent import linear
     torch.manual_seed(6)
+    print(f"m={m}", flush=True)
     x = torch.randn(m, 1024, device="cuda", dtype=torch.bfloat16)
     w = (torch.randn(151936, 1024, device="cuda") * 0.05).to(torch.bfloat16)
-    full = linear(x, w, out_fp32=True)              # wide kernel (N/128 >= 512)
-    part = linear(x, w[:4096].contiguous(), out_fp32=True)  # tiled kernel (N/128 < 512)
-    assert torch.equal(full[:, :4096], part)
+    full = linear(x, w, out_fp32=True)              # streaming kernel
+    head = linear(x, w[:4096].contiguous(), out_fp32=True)  # tiled kernel (small N)
+    tail = linear(x, w[-4096:].contiguous(), out_fp32=True)
+    assert torch.equal(full[:, :4096], head)
+    assert torch.equal(full[:, -4096:], tail)
+    assert torch.equal(linear(x, w), full.to(torch.bfloat16))
     ref = x.float().cpu() @ w[:2048].float().cpu().t()
     torch.testing.assert_close(full[:, :2048].cpu(), ref, atol=3e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("m,n", [(1, 151936), (7, 151936), (33, 65536), (64, 151936), (64, 4096)])
+def test_linear_argmax_matches_linear_then_argmax(m, n):
+    """Fused lm_head + greedy argmax == argmax_rows(linear(..., out_fp32=True)), and the
+    optional logits output equals linear's."""
+    from sid.kernels.matmul_persistent import linear, linear_argmax
+    from sid.kernels.ops import argmax_rows
+    torch.manual_seed(7 + m)
+    print(f"m={m} n={n}", flush=True)
+    x = torch.randn(m, 1024, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(n, 1024, device="cuda") * 0.05).to(torch.bfloat16)
+    logits = linear(x, w, out_fp32=True)
+    want = argmax_rows(logits)
+    assert torch.equal(linear_argmax(x, w), want)
+    lg = torch.empty(m, n, device="cuda")
+    assert torch.equal(linear_argmax(x, w, logits=lg), want)
+    assert torch.equal(lg, logits)
+
+
+def test_linear_argmax_ties_and_nan():
+    """Equal maxima -> first column; a NaN logit wins over every number, first NaN first
+    (torch.argmax semantics), also when the tied columns land in different waves."""
+    from sid.kernels.matmul_persistent import linear_argmax
+    torch.manual_seed(8)
+    n = 151936
+    x = torch.randn(4, 1024, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(n, 1024, device="cuda") * 0.01).to(torch.bfloat16)
+    hot = (x[0].float() / x[0].float().norm()).to(torch.bfloat16)
+    for c in (150000, 70001, 70000, 123):   # identical rows: identical logits for every x
+        w[c] = hot
+    got = linear_argmax(x, w).cpu()
+    assert got[0].item() == 123
+    want = torch.argmax(x.float().cpu() @ w.float().cpu().t(), dim=-1)
+    assert got[0].item() == want[0].item()
+    w[90000, 5] = float("nan")
+    w[80000, 7] = float("nan")
+    got = linear_argmax(x, w).cpu()
+    assert (got == 80000).all()
+

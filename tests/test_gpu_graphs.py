@@ -48,7 +48,10 @@ def test_decode_graph_equals_eager(invariant):
             assert (fb.graph_key is not None) == graphs
             lg = runner.forward(fb)
             logs.append(lg.clone())
-            for r, t in zip(active, runner.sample(fb, lg).tolist()):
+            toks = runner.sample(fb, lg).tolist()
+            # fused lm_head + argmax (its own graph) picks the same tokens
+            assert fb.all_greedy and runner.step(fb).tolist() == toks
+            for r, t in zip(active, toks):
                 r.output_ids.append(t)
         outs[graphs] = (logs, [r.output_ids for r in reqs])
     assert outs[True][1] == outs[False][1]

@@ -80,3 +80,34 @@ def test_silu_mul():
     torch.testing.assert_close(out.float().cpu(), ref.float(), atol=2e-2, rtol=2e-2)
     exact = (out.cpu() == ref).float().mean().item()
     assert exact > 0.99, exact
+
+
+@pytest.mark.parametrize("hidden", [1024, 2048, 4096, 96 * 8])
+def test_rmsnorm_row_layouts_bitwise(hidden):
+    """Below 1024 rows each row gets its own 256-thread workgroup; from 1024 rows up, the
+    lane-group kernel runs. Both must give the same bits for a row (batch invariance)."""
+    from sid.kernels.rmsnorm import fused_add_rmsnorm, rmsnorm
+    torch.manual_seed(hidden)
+    x = torch.randn(1100, hidden, device="cuda", dtype=torch.bfloat16) * 3
+    r = torch.randn(1100, hidden, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(hidden, device="cuda", dtype=torch.bfloat16)
+    print(f"hidden={hidden}", flush=True)
+    big = rmsnorm(x, w, 1e-6)
+    small = rmsnorm(x[:70].clone(), w, 1e-6)
+    assert torch.equal(small, big[:70])
+    hb, rb = fused_add_rmsnorm(x.clone(), r.clone(), w, 1e-6)
+    hs, rs = fused_add_rmsnorm(x[:5].clone(), r[:5].clone(), w, 1e-6)
+    assert torch.equal(rs, rb[:5]) and torch.equal(hs, hb[:5])
+
+
+def test_fused_add_rmsnorm_partials_row_layouts_bitwise():
+    from sid.kernels.matmul_persistent import linear_partials
+    from sid.kernels.ops import fused_add_rmsnorm_partials
+    torch.manual_seed(5)
+    x = torch.randn(1030, 3072, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(1024, 3072, device="cuda") * 0.03).to(torch.bfloat16)
+    nw = torch.randn(1024, device="cuda", dtype=torch.bfloat16)
+    res = torch.randn(1030, 1024, device="cuda", dtype=torch.bfloat16)
+    hb, rb = fused_add_rmsnorm_partials(linear_partials(x, w), res.clone(), nw, 1e-6)
+    hs, rs = fused_add_rmsnorm_partials(linear_partials(x[:64].clone(), w), res[:64].clone(), nw, 1e-6)
+    assert torch.equal(rs, rb[:64]) and torch.equal(hs, hb[:64])
