@@ -61,10 +61,10 @@ def _attn_case(q, k, v, indptr, idx, lens):
     out = {}
     for name, inv in (("nondet", False), ("fixed256", True)):
         us = _time_us(lambda: attn.forward(q, k, v, indptr, idx, seq, max(lens), D ** -0.5, inv))
-        ns, grid, _ = attn.plan(seq, max(lens), inv)
+        ns, grid, _, seg, slots = attn.plan(seq, max(lens), inv)
         out[name] = {"us_per_call": round(us, 2), "GB_s": round(bytes_ / us / 1e3, 1),
                      "frac_of_hbm_peak": round(bytes_ / us / 1e3 / HBM_PEAK_GBS, 4),
-                     "grid_splits": grid}
+                     "grid_splits": grid, "segment_tokens": seg, "grid_slots": slots}
     return out, attn, seq
 
 

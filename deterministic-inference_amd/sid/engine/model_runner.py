@@ -99,12 +99,10 @@ class ModelRunner:
             return build_decode_batch(reqs, self.kv_cache, self.device, invariant)
         fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant,
                                 static=self.graphs.decode_static)
-        bucket = 0
-        if invariant:  # the fixed-256 grid depends on the longest request; bucket it
-            bucket = 256
-            while bucket < fb.max_seq_len:
-                bucket *= 2
-            fb.max_seq_len = bucket
+        # The attention grid depends on the longest request (fixed-256 splits, or the
+        # segment count of the heuristic splits): bucket it so a graph serves a range.
+        bucket = seq_bucket(fb.max_seq_len)
+        fb.max_seq_len = bucket
         fb.graph_key = ("decode", len(reqs), invariant, bucket)
         return fb
 
@@ -117,6 +115,17 @@ class ModelRunner:
     def sample(self, fb: ForwardBatch, logits: torch.Tensor) -> torch.Tensor:
         return _sample(logits, fb.temperatures, fb.top_ks, fb.top_ps, fb.seeds,
                        fb.sample_positions, all_greedy=fb.all_greedy)
+
+
+def seq_bucket(n: int) -> int:
+    """Smallest of 256 * {1, 1.5, 2, 3, 4, 6, ...} >= n (graph key of a decode batch)."""
+    b = 256
+    while True:
+        if b >= n:
+            return b
+        if b + b // 2 >= n:
+            return b + b // 2
+        b *= 2
 
 
 class GraphCache:

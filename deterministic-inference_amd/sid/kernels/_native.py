@@ -36,11 +36,14 @@ _SIGNATURES = {
     "sid_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
     "sid_build_decode_indices": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
+    "sid_flash_decode_segments_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
+                                      _i32, _i32, _i32, _i32, _f32, _vp, _vp, _i32, _i32, _vp,
+                                      _vp],
     "sid_linear_argmax": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
 }
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
             "sid_linear_argmax_workspace_bytes", *_SIGNATURES)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -89,7 +92,10 @@ class NativeLib:
 
     def flash_decode_fwd(self, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                          max_splits: int, fixed_split_size: int, sm_scale: float,
-                         part_o, part_lse, o) -> None:
+                         part_o, part_lse, o, segment_size: int = 0,
+                         grid_slots: int | None = None) -> None:
+        """segment_size / grid_slots: see sid_flash_decode_segments_fwd (defaults: one
+        segment per split, grid of max_splits slots = the reference's partition)."""
         _gpu(q, "q", torch.bfloat16)
         _check(q.dim() == 3, "q must be [B, HQ, D]")
         b, hq, d = q.shape
@@ -112,9 +118,11 @@ class NativeLib:
                "part_lse workspace shape mismatch")
         _gpu(o, "o", torch.bfloat16)
         _check(o.shape == q.shape, "o must have q's shape")
-        self._call("sid_flash_decode_fwd", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                   kv_indptr.data_ptr(), kv_indices.data_ptr(), num_splits.data_ptr(), b, hq, hkv,
-                   d, k_cache.shape[0], int(max_splits), int(fixed_split_size), float(sm_scale),
+        slots = int(max_splits) if grid_slots is None else int(grid_slots)
+        self._call("sid_flash_decode_segments_fwd", q.data_ptr(), k_cache.data_ptr(),
+                   v_cache.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                   num_splits.data_ptr(), b, hq, hkv, d, k_cache.shape[0], int(max_splits),
+                   int(fixed_split_size), int(segment_size), slots, float(sm_scale),
                    part_o.data_ptr(), part_lse.data_ptr(), part_o.shape[0], part_o.shape[2],
                    o.data_ptr(), _stream(q))
 

@@ -10,8 +10,11 @@ with the device's compute-unit count as its input):
 * batch_invariant: fixed 256-token splits, ``ceil(len / 256)`` per request, grid
   ``ceil(max_len / 256)``; a request's result depends only on its own length.
 
-On MI355X (256 CUs) a batch of 64 with 8 KV heads gets one split per request; the
-kernel then writes the output directly and skips the merge pass.
+MI355X addition: the kernel's workgroup reads all KV heads of a token range (whole
+2 KiB pool rows), so a split is further cut into segments of at most ``seg`` tokens,
+one workgroup each. batch_invariant uses seg = 256 = the split size (the reference's
+partition, independent of the batch); nondet/dvr take the largest of 256/128/64 that
+still gives at least one workgroup per CU for the batch's (bucketed) longest request.
 """
 
 from __future__ import annotations
@@ -34,6 +37,42 @@ def heuristic_splits(batch: int, num_kv_heads: int, cu_count: int, max_kv_splits
     return max(1, min(splits, max_kv_splits))
 
 
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+SEGMENT_SIZES = (256, 128, 64)
+MAX_GRID_SLOTS = 1024  # kernel limit on partial slots per request
+
+
+def segment_size(batch: int, max_len: int, cu_count: int) -> int:
+    """nondet/dvr segment length: the largest of SEGMENT_SIZES whose grid
+    (batch x segments of the longest request) still has one workgroup per CU."""
+    for seg in SEGMENT_SIZES:
+        if batch * -(-max_len // seg) >= cu_count:
+            return seg
+    return SEGMENT_SIZES[-1]
+
+
+def nondet_geometry(batch: int, max_len: int, num_kv_heads: int, cu_count: int,
+                    max_kv_splits: int) -> tuple[int, int, int]:
+    """(grid splits, segment size, grid slots) of the nondet/dvr plan. A request of length
+    n <= max_len gets s = min(splits, ceil(n/32)) splits of chunk
+    ceil(ceil(n/s)/32)*32 <= chunk_max tokens, each cut into ceil(chunk/seg) segments, so
+    splits * ceil(chunk_max/seg) slots cover every request."""
+    splits = heuristic_splits(batch, num_kv_heads, cu_count, max_kv_splits)
+    chunk_max = max(32, _cdiv(_cdiv(max_len, splits), 32) * 32)
+    seg = segment_size(batch, max_len, cu_count)
+    return splits, seg, splits * max(1, _cdiv(chunk_max, seg))
+
+
+def workspace_slots(max_seq_len: int, max_kv_splits: int, invariant_split_size: int) -> int:
+    """Partial slots per request the workspace must hold for any plan."""
+    nondet = -(-max_seq_len // SEGMENT_SIZES[-1]) + max_kv_splits
+    inv = -(-max_seq_len // invariant_split_size)
+    return min(max(nondet, inv), MAX_GRID_SLOTS)
+
+
 class DecodeAttention:
     """Owns the persistent split workspace (fixed pointers across steps)."""
 
@@ -45,7 +84,7 @@ class DecodeAttention:
         self.max_kv_splits = max_kv_splits
         self.invariant_split_size = invariant_split_size
         self.invariant_max_splits = -(-max_seq_len // invariant_split_size)
-        self.ws_splits = max(max_kv_splits, self.invariant_max_splits)
+        self.ws_splits = workspace_slots(max_seq_len, max_kv_splits, invariant_split_size)
         self.part_o = torch.empty(max_batch, num_q_heads, self.ws_splits, head_dim,
                                   dtype=torch.float32, device=device)
         self.part_lse = torch.empty(max_batch, num_q_heads, self.ws_splits,
@@ -65,15 +104,19 @@ class DecodeAttention:
         return _cu_count(idx)
 
     def plan(self, seq_lens: torch.Tensor, max_seq_len: int, invariant: bool):
-        """(num_splits int32 [B] on device, grid splits, fixed split size)."""
+        """(num_splits int32 [B] on device, grid splits, fixed split size, segment size,
+        grid slots). max_seq_len bounds every request's length (host-side, no sync)."""
         bs = seq_lens.shape[0]
+        max_len = max(int(max_seq_len), 1)
         if invariant:
             tile = self.invariant_split_size
             num_splits = ((seq_lens + tile - 1) // tile).to(torch.int32)
-            return num_splits, max(1, -(-max_seq_len // tile)), tile
-        splits = heuristic_splits(bs, self.num_kv_heads, self.cu_count(), self.max_kv_splits)
+            grid = max(1, -(-max_len // tile))
+            return num_splits, grid, tile, tile, grid
+        splits, seg, slots = nondet_geometry(bs, max_len, self.num_kv_heads, self.cu_count(),
+                                             self.max_kv_splits)
         num_splits = torch.clamp((seq_lens + 31) // 32, max=splits).to(torch.int32)
-        return num_splits, splits, 0
+        return num_splits, splits, 0, seg, slots
 
     def forward(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, seq_lens: torch.Tensor,
@@ -84,11 +127,14 @@ class DecodeAttention:
         # One plan per forward: every layer sees the same seq_lens tensor.
         key = (invariant, max_seq_len, bs)
         if self._plan_src is seq_lens and self._plan[0] == key:
-            num_splits, grid_splits, fixed = self._plan[1]
+            plan = self._plan[1]
         else:
-            num_splits, grid_splits, fixed = self.plan(seq_lens, max_seq_len, invariant)
-            self._plan_src, self._plan = seq_lens, (key, (num_splits, grid_splits, fixed))
+            plan = self.plan(seq_lens, max_seq_len, invariant)
+            self._plan_src, self._plan = seq_lens, (key, plan)
+        num_splits, grid_splits, fixed, seg, slots = plan
+        assert slots <= self.part_o.shape[2], "decode plan exceeds the split workspace"
         o = torch.empty_like(q)
         self.ext.flash_decode_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
-                                  grid_splits, fixed, sm_scale, self.part_o, self.part_lse, o)
+                                  grid_splits, fixed, sm_scale, self.part_o, self.part_lse, o,
+                                  segment_size=seg, grid_slots=slots)
         return o

@@ -57,9 +57,11 @@ int sid_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_c
  * [B]; part_o fp32 [part_batch, HQ, part_stride, D]; part_lse fp32
  * [part_batch, HQ, part_stride]. fixed_split_size > 0 gives fixed-size splits
  * (batch-invariant mode), 0 the heuristic geometry
- * ceil(ceil(len / n) / 32) * 32. Requires HQ == 2 * HKV, D == 128,
- * part_batch >= B, part_stride >= max_splits >= 1. Slots outside [0, S) read
- * slot 0. When max_splits == 1 the workspace is not touched.
+ * ceil(ceil(len / n) / 32) * 32. Requires HKV == 8, HQ == 16, D == 128
+ * (the Qwen3 attention shape), part_batch >= B, part_stride >= max_splits >=
+ * 1. Slots outside [0, S) read slot 0. When max_splits == 1 the workspace is
+ * not touched. Equals sid_flash_decode_segments_fwd with segment_size 0 and
+ * grid_slots = max_splits.
  * Replaces flash_decode_fwd, sid/csrc/flash_decode.cu:307-376.
  */
 int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -68,6 +70,29 @@ int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache
                          int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
                          float sm_scale, float* part_o, float* part_lse, int part_batch,
                          int part_stride, void* o, void* stream);
+
+/*
+ * sid_flash_decode_fwd with every KV split cut into segments of at most
+ * segment_size tokens (0: one segment per split), each computed by its own
+ * workgroup; stage 2 merges all of a request's segments in token order.
+ * Partial slot y of a request is segment y % sps of split y / sps, where
+ * sps = ceil(chunk / min(segment_size, chunk)); grid_slots (<= part_stride)
+ * slots are launched per request, so grid_slots must cover
+ * max over requests of n_splits * sps (slots past a request's last segment
+ * are empty and skipped). Same arguments and limits otherwise. The segment
+ * size sets how many workgroups share a long split (the reference's grid is
+ * one workgroup per head and split; here a workgroup reads all heads of its
+ * tokens), and it is part of the reduction order: with a fixed split size
+ * and a fixed segment size the result depends on the request alone. When
+ * grid_slots == 1 the workspace is not touched.
+ */
+int sid_flash_decode_segments_fwd(const void* q, const void* k_cache, const void* v_cache,
+                                  const int32_t* kv_indptr, const int32_t* kv_indices,
+                                  const int32_t* num_splits, int batch, int num_q_heads,
+                                  int num_kv_heads, int head_dim, int64_t num_slots,
+                                  int max_splits, int fixed_split_size, int segment_size,
+                                  int grid_slots, float sm_scale, float* part_o, float* part_lse,
+                                  int part_batch, int part_stride, void* o, void* stream);
 
 /*
  * Varlen causal attention over the paged pool (prefill, DVR verify). q, o:

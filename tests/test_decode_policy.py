@@ -1,0 +1,78 @@
+"""Host-side decode-attention policy (no GPU): split heuristic, segment size, the grid's
+slot count covering every request's segments, and the graph-key sequence buckets."""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+
+from sid.engine.model_runner import seq_bucket
+from sid.kernels.decode_attention import (MAX_GRID_SLOTS, SEGMENT_SIZES, heuristic_splits,
+                                          nondet_geometry, segment_size, workspace_slots)
+
+
+def _segments(n: int, splits: int, fixed: int, seg: int) -> list[tuple[int, int]]:
+    """Token ranges of a request's segments, by walking its splits token by token."""
+    s = min(splits, -(-n // 32)) if fixed == 0 else -(-n // fixed)
+    if fixed:
+        chunk = fixed
+    else:
+        per = -(-n // s)
+        chunk = -(-per // 32) * 32
+    out = []
+    for i in range(s):
+        a, b = i * chunk, min((i + 1) * chunk, n)
+        while a < b:
+            out.append((a, min(a + seg, b)))
+            a = min(a + seg, b)
+    return out
+
+
+def test_heuristic_splits_matches_reference_formula_cases():
+    # reference decode_attention.py:73-74 on 256 CUs, 8 KV heads, max 16 splits
+    assert heuristic_splits(64, 8, 256, 16) == 1
+    assert heuristic_splits(8, 8, 256, 16) == 8
+    assert heuristic_splits(1, 8, 256, 16) == 16
+    assert heuristic_splits(3, 8, 256, 16) == 16
+    assert heuristic_splits(33, 8, 256, 16) == 2
+
+
+def test_segment_size_prefers_long_segments_when_grid_is_full():
+    assert segment_size(64, 2049, 256) == 256
+    assert segment_size(8, 2049, 256) == 64
+    assert segment_size(4, 8192, 256) == 128
+    assert segment_size(1, 10, 256) == SEGMENT_SIZES[-1]
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_nondet_slots_cover_every_request(seed):
+    rng = random.Random(seed)
+    bs = rng.choice([1, 2, 3, 8, 17, 64, 200])
+    max_len = rng.choice([1, 31, 32, 33, 255, 256, 257, 1000, 2049, 8191])
+    lens = [rng.randint(1, max_len) for _ in range(bs)]
+    lens[0] = max_len
+    splits, seg, slots = nondet_geometry(bs, max_len, 8, 256, 16)
+    need = max(len(_segments(n, splits, 0, seg)) for n in lens)
+    assert need <= slots <= workspace_slots(max_len, 16, 256)
+    assert sum(b - a for a, b in _segments(max_len, splits, 0, seg)) == max_len
+
+
+def test_invariant_segments_are_the_256_splits():
+    for n in (1, 255, 256, 257, 5000):
+        segs = _segments(n, 0, 256, 256)
+        assert len(segs) == -(-n // 256) and all(b - a <= 256 for a, b in segs)
+
+
+def test_workspace_slots_capped():
+    assert workspace_slots(10 ** 6, 16, 256) == MAX_GRID_SLOTS
+
+
+def test_seq_bucket():
+    prev = 0
+    for n in range(1, 20000, 7):
+        b = seq_bucket(n)
+        assert b >= n and b >= prev
+        prev = b
+    assert [seq_bucket(n) for n in (1, 256, 257, 384, 385, 2049, 3073)] == [
+        256, 256, 384, 384, 512, 3072, 4096]

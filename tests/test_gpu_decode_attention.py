@@ -26,15 +26,28 @@ def _ext():
     return load_ext()
 
 
-def _run(q, k, v, indptr, idx, num_splits, grid, fixed):
+def _run(q, k, v, indptr, idx, num_splits, grid, fixed, seg=0, slots=None):
     bs = q.shape[0]
-    ws = max(grid, 1)
-    part_o = torch.empty(bs, HQ, ws, D, device="cuda", dtype=torch.float32)
-    part_lse = torch.empty(bs, HQ, ws, device="cuda", dtype=torch.float32)
+    slots = grid if slots is None else slots
+    part_o = torch.full((bs, HQ, max(slots, 1), D), float("nan"), device="cuda")
+    part_lse = torch.full((bs, HQ, max(slots, 1)), float("nan"), device="cuda")
     o = torch.empty_like(q)
     ns = torch.tensor(num_splits, dtype=torch.int32, device="cuda")
-    _ext().flash_decode_fwd(q, k, v, indptr, idx, ns, grid, fixed, SCALE, part_o, part_lse, o)
+    _ext().flash_decode_fwd(q, k, v, indptr, idx, ns, grid, fixed, SCALE, part_o, part_lse, o,
+                            segment_size=seg, grid_slots=slots)
     return o
+
+
+def _slots(seq_lens, num_splits, fixed, seg):
+    """Partial slots the segmented grid needs (max over requests of n_splits * sps)."""
+    best = 1
+    for n, s in zip(seq_lens, num_splits):
+        if n <= 0 or s <= 0:
+            continue
+        chunk = fixed if fixed > 0 else -(-(-(-n // s)) // 32) * 32
+        sl = min(seg, chunk) if seg > 0 else chunk
+        best = max(best, s * -(-chunk // sl))
+    return best
 
 
 def _policy(seq_lens, policy):
@@ -63,6 +76,36 @@ def test_decode_vs_oracle(seq_lens, policy):
     out = _run(q, k, v, indptr, idx, ns, grid, fixed)
     ref = decode_attention_ref(q, k, v, indptr, idx, SCALE)
     assert_close_bf16(out, ref)
+
+
+@pytest.mark.parametrize("seq_lens", CASES, ids=lambda s: f"b{len(s)}_max{max(s)}")
+@pytest.mark.parametrize("policy", ["heuristic", "fixed256", "splits1", "splits8"])
+@pytest.mark.parametrize("seg", [64, 128, 256])
+def test_decode_segments_vs_oracle(seq_lens, policy, seg):
+    """Splits cut into segments of <= seg tokens (one workgroup each), merged in token
+    order by stage 2. Workspace pre-filled with NaN: a slot read but never written, or a
+    token dropped, shows up."""
+    q, k, v, indptr, idx = decode_inputs(seq_lens)
+    ns, grid, fixed = _policy(seq_lens, policy)
+    slots = _slots(seq_lens, ns, fixed, seg)
+    print(f"lens={seq_lens[:4]} policy={policy} seg={seg} slots={slots}", flush=True)
+    out = _run(q, k, v, indptr, idx, ns, grid, fixed, seg, slots)
+    ref = decode_attention_ref(q, k, v, indptr, idx, SCALE)
+    assert_close_bf16(out, ref)
+
+
+@pytest.mark.parametrize("invariant", [False, True])
+@pytest.mark.parametrize("lens", [[1, 2049, 300], [4096] * 3, [33] * 70, [777] * 9])
+def test_planned_decode_vs_oracle(invariant, lens):
+    """DecodeAttention's own plan (splits, segment size, grid slots) covers every token."""
+    from sid.kernels.decode_attention import DecodeAttention
+    q, k, v, indptr, idx = decode_inputs(lens, seed=5)
+    attn = DecodeAttention(len(lens), HQ, HKV, D, 16, 256, 8192, "cuda")
+    seq = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    _, _, _, seg, slots = attn.plan(seq, max(lens), invariant)
+    print(f"lens={lens[:3]} invariant={invariant} seg={seg} slots={slots}", flush=True)
+    out = attn.forward(q, k, v, indptr, idx, seq, max(lens), SCALE, invariant)
+    assert_close_bf16(out, decode_attention_ref(q, k, v, indptr, idx, SCALE))
 
 
 def test_direct_single_split_equals_two_stage():
