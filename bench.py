@@ -7,9 +7,10 @@ kernel), the 28-layer forward (every op a HIP kernel), greedy sampling, tokens b
 host. The request state is rolled back after each step so every timed step has identical
 work (context 2049). Prints one JSON line with:
   value        decode tokens/s of the whole step
-  roofline     the decode-attention kernel (dominant: ~93% of the step's bytes), its average
-               launch duration measured with HIP events on the launch stream, algorithmic
-               bytes per launch (K + V rows read + kv_indices + q + o) / duration, vs 8 TB/s
+  roofline     the decode-attention op (stage 1 + its merge pass; dominant: ~93% of the
+               step's bytes), its average duration measured with HIP events on the launch
+               stream, algorithmic bytes per call (K + V rows read + kv_indices + q + o) /
+               duration, vs 8 TB/s
   cpu_baseline the CPU oracle (fp32 torch restatement of the step) on a bounded sample
 """
 
@@ -154,16 +155,17 @@ def attention_roofline(wl, reps):
     achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-            "kernel": "decode_stage1_kernel (split-KV flash decode, 1 split at B=64)",
+            "kernel": "decode_stage1_kernel + decode_stage2_kernel (all-heads segments of "
+                      "<= 256 tokens, then the in-order merge)",
             "avg_launch_us": round(avg_ms * 1e3, 2), "bytes_per_launch": bytes_launch,
             "launches_timed": launches}
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "decode_stage1_b64_ctx2048_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "decode_attention_b64_ctx2048_traffic.json"
 
 
 def measured_traffic():
-    """HBM bytes per launch of the decode-attention kernel from the committed rocprofv3
+    """HBM bytes per call of decode attention (both stages) from the committed rocprofv3
     --pmc FETCH_SIZE / WRITE_SIZE runs (scaled by the copy calibration), or None."""
     try:
         return json.loads(TRAFFIC_FILE.read_text())["traffic_bytes_per_launch"]
