@@ -305,7 +305,7 @@ template <int MBS, bool ARGMAX>
 __global__ void __launch_bounds__(STREAM_WAVES * 64) linear_stream_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ bias, void* __restrict__ y, int M, int N, int out_fp32,
-    float* __restrict__ best_val, int* __restrict__ best_idx) {
+    float* __restrict__ best_val, int* __restrict__ best_idx, int cand_rows, int row0) {
   extern __shared__ __align__(16) bf16_t lx[];  // [MBS*16][WXS]
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -448,8 +448,8 @@ __global__ void __launch_bounds__(STREAM_WAVES * 64) linear_stream_kernel(
         }
         const int row = 16 * mb + 4 * g + i;
         if (r == 0 && row < M) {
-          best_val[static_cast<int64_t>(gw) * M + row] = v;
-          best_idx[static_cast<int64_t>(gw) * M + row] = ix;
+          best_val[static_cast<int64_t>(gw) * cand_rows + row0 + row] = v;
+          best_idx[static_cast<int64_t>(gw) * cand_rows + row0 + row] = ix;
         }
       }
     }
@@ -558,13 +558,18 @@ int stream_grid() {
   return count[dev];
 }
 
+// Row groups of up to 64 rows are streamed one after the other (the weights are re-read
+// per group); up to this many rows that still beats the tiled kernel on lm_head shapes.
+constexpr int64_t kStreamMaxM = 256;
+
 bool stream_shape_ok(int64_t m, int64_t n, int64_t k) {
-  return m >= 1 && m <= MROWS && k == WIDE_K && n % 16 == 0 && n < (1ll << 31);
+  return m >= 1 && m <= kStreamMaxM && k == WIDE_K && n % 16 == 0 && n < (1ll << 31);
 }
 
 template <int MBS, bool AM>
-void launch_stream_mbs(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int m,
-                       int n, int out_fp32, float* bv, int* bi, hipStream_t s) {
+void launch_stream_mbs(const bf16_t* x, int64_t ldx, const void* w, const void* bias, void* y,
+                       int m, int n, int out_fp32, float* bv, int* bi, int cand_rows, int row0,
+                       hipStream_t s) {
   const size_t lds = static_cast<size_t>(MBS * 16) * WXS * sizeof(bf16_t);
   static bool attr_set = false;
   if (!attr_set) {
@@ -573,18 +578,30 @@ void launch_stream_mbs(const void* x, int64_t ldx, const void* w, const void* bi
     attr_set = true;
   }
   hipLaunchKernelGGL((linear_stream_kernel<MBS, AM>), dim3(stream_grid()),
-                     dim3(STREAM_WAVES * 64), lds, s, (const bf16_t*)x, ldx, (const bf16_t*)w,
-                     (const bf16_t*)bias, y, m, n, out_fp32, bv, bi);
+                     dim3(STREAM_WAVES * 64), lds, s, x, ldx, (const bf16_t*)w,
+                     (const bf16_t*)bias, y, m, n, out_fp32, bv, bi, cand_rows, row0);
 }
 
+// One launch per 64-row group; group g reads x rows 64g.., writes y rows 64g.. and the
+// candidate rows 64g.. of the [waves][m] workspace.
 template <bool AM>
 void launch_stream(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int m,
                    int n, int out_fp32, float* bv, int* bi, hipStream_t s) {
-  switch ((m + 15) / 16) {
-    case 1: return launch_stream_mbs<1, AM>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, s);
-    case 2: return launch_stream_mbs<2, AM>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, s);
-    case 3: return launch_stream_mbs<3, AM>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, s);
-    default: return launch_stream_mbs<4, AM>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, s);
+  for (int r0 = 0; r0 < m; r0 += MROWS) {
+    const int mg = min(MROWS, m - r0);
+    const bf16_t* xg = static_cast<const bf16_t*>(x) + static_cast<int64_t>(r0) * ldx;
+    void* yg = nullptr;
+    if (y != nullptr) {
+      const int64_t off = static_cast<int64_t>(r0) * n;
+      yg = out_fp32 ? static_cast<void*>(static_cast<float*>(y) + off)
+                    : static_cast<void*>(static_cast<bf16_t*>(y) + off);
+    }
+    switch ((mg + 15) / 16) {
+      case 1: launch_stream_mbs<1, AM>(xg, ldx, w, bias, yg, mg, n, out_fp32, bv, bi, m, r0, s); break;
+      case 2: launch_stream_mbs<2, AM>(xg, ldx, w, bias, yg, mg, n, out_fp32, bv, bi, m, r0, s); break;
+      case 3: launch_stream_mbs<3, AM>(xg, ldx, w, bias, yg, mg, n, out_fp32, bv, bi, m, r0, s); break;
+      default: launch_stream_mbs<4, AM>(xg, ldx, w, bias, yg, mg, n, out_fp32, bv, bi, m, r0, s); break;
+    }
   }
 }
 
@@ -636,7 +653,7 @@ extern "C" int sid_linear_partials(const void* x, int64_t ldx, const void* w, fl
 }
 
 extern "C" int64_t sid_linear_argmax_workspace_bytes(int64_t m) {
-  if (m < 1 || m > MROWS) return 0;
+  if (m < 1 || m > kStreamMaxM) return 0;
   return static_cast<int64_t>(stream_grid()) * STREAM_WAVES * m * (sizeof(float) + sizeof(int));
 }
 
@@ -650,7 +667,7 @@ extern "C" int sid_linear_argmax(const void* x, int64_t ldx, const void* w, cons
   int rc = check_shapes(x, ldx, w, m, n, k, "linear_argmax");
   if (rc != SID_OK) return rc;
   SID_REQUIRE(stream_shape_ok(m, n, k),
-              "linear_argmax: needs 1 <= M <= %d and K == %d (got M=%lld, K=%lld)", MROWS, WIDE_K,
+              "linear_argmax: needs 1 <= M <= %d and K == %d (got M=%lld, K=%lld)", (int)kStreamMaxM, WIDE_K,
               (long long)m, (long long)k);
   const int64_t need = sid_linear_argmax_workspace_bytes(m);
   SID_REQUIRE(workspace_bytes >= need, "linear_argmax: workspace %lld bytes, need %lld",

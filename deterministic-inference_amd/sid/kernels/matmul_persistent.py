@@ -62,8 +62,8 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor,
 
 
 def linear_argmax_supported(m: int, k: int) -> bool:
-    """Shapes the fused lm_head + greedy argmax kernel takes (decode-sized M, K = 1024)."""
-    return 1 <= m <= 64 and k == 1024
+    """Shapes the fused lm_head + greedy argmax kernel takes (M <= 256, K = 1024)."""
+    return 1 <= m <= 256 and k == 1024
 
 
 def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,

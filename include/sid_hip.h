@@ -231,7 +231,7 @@ int sid_gather_rows(const void* table, const int64_t* idx, void* out, int64_t n,
  * and compared with sid_argmax_rows's order. Fuses the lm_head projection
  * (sid/model/qwen3.py:114-115) with the greedy branch of sample()
  * (sid/engine/sampler.py:38) for an all-greedy batch. logits may be NULL (not
- * written) or fp32 [M, N]. Needs 1 <= M <= 64, K == 1024; workspace of
+ * written) or fp32 [M, N]. Needs 1 <= M <= 256, K == 1024; workspace of
  * sid_linear_argmax_workspace_bytes(M) bytes, 16-byte aligned.
  */
 int64_t sid_linear_argmax_workspace_bytes(int64_t m);

@@ -78,9 +78,10 @@ def test_partials_fold_equals_linear(m, n, k):
     assert torch.equal(fold.to(torch.bfloat16), linear(x, w))
 
 
-@pytest.mark.parametrize("m", [1, 16, 33, 64])
+@pytest.mark.parametrize("m", [1, 16, 33, 64, 100, 128, 256])
 def test_stream_lm_head_path_bitwise_matches_tiled(m):
-    """lm_head-shaped GEMMs (K=1024, N >= 32768, M<=64) take the persistent streaming kernel;
+    """lm_head-shaped GEMMs (K=1024, N >= 32768, M<=256 in 64-row groups) take the persistent
+    streaming kernel;
     its bits equal the tiled kernel's (checked on the first and last 4096 columns, which
     the tiled kernel computes separately), for fp32 and bf16 outputs."""
     from sid.kernels.matmul_persistent import linear
@@ -98,7 +99,8 @@ def test_stream_lm_head_path_bitwise_matches_tiled(m):
     torch.testing.assert_close(full[:, :2048].cpu(), ref, atol=3e-2, rtol=2e-2)
 
 
-@pytest.mark.parametrize("m,n", [(1, 151936), (7, 151936), (33, 65536), (64, 151936), (64, 4096)])
+@pytest.mark.parametrize("m,n", [(1, 151936), (7, 151936), (33, 65536), (64, 151936), (64, 4096),
+                                 (128, 151936), (200, 65536)])
 def test_linear_argmax_matches_linear_then_argmax(m, n):
     """Fused lm_head + greedy argmax == argmax_rows(linear(..., out_fp32=True)), and the
     optional logits output equals linear's."""
