@@ -88,45 +88,66 @@ struct Ctx {
   int r, g, wave, lane, tid;
 };
 
-// One 64-key tile starting at absolute key t0 folded into `st` (online softmax).
-__device__ __forceinline__ void tile_step(RowState& st, const Ctx& c, int t0,
-                                          const bf16x8_v (&qf)[4], float sm_scale, bf16_t* sK,
-                                          bf16_t* sVt) {
-  __syncthreads();  // previous tile fully consumed
-  // K tile, row-major: vector v = tid + 256*i -> key v/16, 16-byte chunk v%16.
+// Global -> register staging of one 64-key tile (K row-major, V for the transposed copy).
+// Loaded one tile ahead of the math, so the next tile's HBM round trip overlaps the
+// current tile's MFMAs; 8 x 16 bytes per thread.
+struct TileRegs {
+  u32x4_v k[4];
+  u32x4_v v[4];
+};
+
+// Pool slots of the split's keys, staged in LDS once per split (s_idx[j] = slot of key
+// split_start + j; 0 past the sequence or out of range), so a tile's K/V loads wait on
+// LDS rather than on a global index load.
+__device__ __forceinline__ void stage_slots(int32_t* s_idx, const Ctx& c, int split_start) {
+  const int pos = split_start + c.tid;
+  int32_t slot = pos < c.kv_len ? c.idx[pos] : 0;
+  if (slot < 0 || slot >= c.num_slots) slot = 0;
+  s_idx[c.tid] = slot;
+}
+
+__device__ __forceinline__ void load_tile(TileRegs& r, const Ctx& c, const int32_t* s_idx,
+                                          int k0) {
+  // K: vector v = tid + 256*i -> key v/16, 16-byte chunk v%16 (k0: tile offset in split).
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int v = c.tid + 256 * i;
-    const int key = v >> 4;
-    const int ch = v & 15;
-    const int pos = t0 + key;
-    int64_t slot = pos < c.kv_len ? static_cast<int64_t>(c.idx[pos]) : 0;
-    if (slot < 0 || slot >= c.num_slots) slot = 0;
-    const uint4 kv =
-        reinterpret_cast<const uint4*>(c.k_cache + slot * c.row_stride + c.h_kv * D)[ch];
-    *reinterpret_cast<uint4*>(&sK[key * KS_STRIDE + ch * 8]) = kv;
+    const int64_t slot = s_idx[k0 + (v >> 4)];
+    r.k[i] = reinterpret_cast<const u32x4_v*>(c.k_cache + slot * c.row_stride + c.h_kv * D)[v & 15];
   }
-  // V tile, transposed: lane -> key, wave w -> 16-byte chunks 4w .. 4w+3.
-  {
-    const int key = c.lane;
-    const int pos = t0 + key;
-    int64_t slot = pos < c.kv_len ? static_cast<int64_t>(c.idx[pos]) : 0;
-    if (slot < 0 || slot >= c.num_slots) slot = 0;
-    const uint4* vp = reinterpret_cast<const uint4*>(c.v_cache + slot * c.row_stride + c.h_kv * D);
+  // V: lane -> key, wave w -> 16-byte chunks 4w .. 4w+3.
+  const int64_t slot = s_idx[k0 + c.lane];
+  const u32x4_v* vp =
+      reinterpret_cast<const u32x4_v*>(c.v_cache + slot * c.row_stride + c.h_kv * D);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ch = 4 * c.wave + i;
-      const uint4 vv = vp[ch];
-      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+  for (int i = 0; i < 4; ++i) r.v[i] = vp[4 * c.wave + i];
+}
+
+__device__ __forceinline__ void store_tile(const TileRegs& r, const Ctx& c, bf16_t* sK,
+                                           bf16_t* sVt) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sVt[(ch * 8 + 2 * e) * VT_STRIDE + key] = static_cast<bf16_t>(w4[e] & 0xffffu);
-        sVt[(ch * 8 + 2 * e + 1) * VT_STRIDE + key] = static_cast<bf16_t>(w4[e] >> 16);
-      }
+  for (int i = 0; i < 4; ++i) {
+    const int v = c.tid + 256 * i;
+    *reinterpret_cast<u32x4_v*>(&sK[(v >> 4) * KS_STRIDE + (v & 15) * 8]) = r.k[i];
+  }
+  const int key = c.lane;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ch = 4 * c.wave + i;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = r.v[i][e];
+      sVt[(ch * 8 + 2 * e) * VT_STRIDE + key] = static_cast<bf16_t>(w & 0xffffu);
+      sVt[(ch * 8 + 2 * e + 1) * VT_STRIDE + key] = static_cast<bf16_t>(w >> 16);
     }
   }
-  __syncthreads();
+}
 
+// The 64-key tile starting at absolute key t0, already in LDS, folded into `st` (online
+// softmax).
+__device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
+                                          const bf16x8_v (&qf)[4], float sm_scale,
+                                          const bf16_t* sK, const bf16_t* sVt) {
   // S^T blocks: lane holds logits of its query for keys 8g..8g+7 (s[0..7]) and
   // 32+8g..32+8g+7 (s[8..15]). MFMA row m of key block j holds key
   // 32*(j/2) + 8*(m/4) + 4*(j%2) + m%4.
@@ -194,6 +215,26 @@ __device__ __forceinline__ void tile_step(RowState& st, const Ctx& c, int t0,
   }
 }
 
+// Keys [t_begin, t_end) of one split (t_begin = split start, at most KSPLIT keys) folded
+// into `st` tile by tile, with the next tile's loads in flight during each tile's math.
+__device__ __forceinline__ void run_tiles(RowState& st, const Ctx& c, int t_begin, int t_end,
+                                          const bf16x8_v (&qf)[4], float sm_scale, bf16_t* sK,
+                                          bf16_t* sVt, int32_t* s_idx) {
+  if (t_begin >= t_end) return;
+  __syncthreads();  // previous split's tiles done with s_idx
+  stage_slots(s_idx, c, t_begin);
+  __syncthreads();
+  TileRegs r;
+  load_tile(r, c, s_idx, 0);
+  for (int t0 = t_begin; t0 < t_end; t0 += BN) {
+    __syncthreads();  // previous tile's math done with the LDS tiles
+    store_tile(r, c, sK, sVt);
+    __syncthreads();
+    if (t0 + BN < t_end) load_tile(r, c, s_idx, t0 + BN - t_begin);
+    tile_math(st, c, t0, qf, sm_scale, sK, sVt);
+  }
+}
+
 // part_* layout: [split][total_q][HQ]; part_a holds the unnormalised accumulator
 // (128 dims), part_ml = (m, l). Lane holds dims 16*db + 4*g .. +3 of its row.
 __global__ void __launch_bounds__(256) extend_attention_kernel(
@@ -205,6 +246,7 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
     float* __restrict__ part_ml) {
   __shared__ __align__(16) bf16_t sK[BN * KS_STRIDE];
   __shared__ __align__(16) bf16_t sVt[D * VT_STRIDE];
+  __shared__ int32_t s_idx[KSPLIT];
 
   const int b = blockIdx.x;
   const int h_kv = blockIdx.y;
@@ -259,8 +301,8 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   if (fanout) {
     RowState st;
     fresh(st);
-    const int t_end = min(visible_end, (split + 1) * KSPLIT);
-    for (int t0 = split * KSPLIT; t0 < t_end; t0 += BN) tile_step(st, c, t0, qf, sm_scale, sK, sVt);
+    run_tiles(st, c, split * KSPLIT, min(visible_end, (split + 1) * KSPLIT), qf, sm_scale, sK, sVt,
+              s_idx);
     if (!c.row_ok) return;
     const int64_t pr = static_cast<int64_t>(split) * total_q * num_q_heads + prow;
     float* pa = part_a + pr * D;
@@ -279,8 +321,8 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   for (int sp = 0; sp < nsplits; ++sp) {
     RowState st;
     fresh(st);
-    const int t_end = min(visible_end, (sp + 1) * KSPLIT);
-    for (int t0 = sp * KSPLIT; t0 < t_end; t0 += BN) tile_step(st, c, t0, qf, sm_scale, sK, sVt);
+    run_tiles(st, c, sp * KSPLIT, min(visible_end, (sp + 1) * KSPLIT), qf, sm_scale, sK, sVt,
+              s_idx);
     fold(run, st.m, st.l, st.acc);
   }
   if (!c.row_ok) return;
@@ -294,46 +336,73 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   }
 }
 
-// Fold the fanned-out split states of every (query row, head) in split order.
-// One 64-lane wave per (row, head): lane (r, g) with r = 0 holds... every lane
-// reproduces the per-lane layout of the attention kernel (dims 16*db + 4*g + i)
-// so fold() runs on exactly the same operands.
+// Fold the fanned-out split states of every (query row, head) in split order. Grid:
+// x = request, y = groups of 4 (row, head) items of that request; one 64-lane wave per
+// item. The wave first copies up to MERGE_CHUNK splits' states into LDS with one round of
+// independent loads, then folds them from LDS. Every lane reproduces the per-lane layout
+// of the attention kernel (dims 16*db + 4*g + i), so fold() runs on exactly the same
+// operands in the same order as the sequential path.
+constexpr int MERGE_CHUNK = 16;
+
 __global__ void __launch_bounds__(256) extend_merge_kernel(
-    const int32_t* __restrict__ qo_indptr, const int32_t* __restrict__ kv_indptr, int batch,
+    const int32_t* __restrict__ qo_indptr, const int32_t* __restrict__ kv_indptr,
     int num_q_heads, int64_t total_q, const float* __restrict__ part_a,
     const float* __restrict__ part_ml, bf16_t* __restrict__ o) {
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // (row, head)
+  __shared__ __align__(16) float s_a[4][MERGE_CHUNK][D];
+  __shared__ float s_ml[4][MERGE_CHUNK][2];
+  const int b = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int local = blockIdx.y * 4 + wave;  // (row, head) within the request
   const int lane = threadIdx.x & 63;
-  if (item >= total_q * num_q_heads) return;
-  const int64_t row = item / num_q_heads;
-  // Locate the row's request (binary search over qo_indptr).
-  int lo = 0, hi = batch;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (qo_indptr[mid] <= row) lo = mid; else hi = mid;
-  }
-  const int b = lo;
-  const int extend_len = qo_indptr[b + 1] - qo_indptr[b];
+  const int q_start = qo_indptr[b];
+  const int extend_len = qo_indptr[b + 1] - q_start;
   const int kv_len = kv_indptr[b + 1] - kv_indptr[b];
+  const bool valid = local < extend_len * num_q_heads;
+  const int64_t item = static_cast<int64_t>(q_start) * num_q_heads + local;
   const int prefix = kv_len - extend_len;
-  const int qr = static_cast<int>(row - qo_indptr[b]);
+  const int qr = local / num_q_heads;
   const int mtile = qr / BQ;
   const int last_row = min(extend_len, (mtile + 1) * BQ) - 1;
   const int visible_end = min(kv_len, prefix + last_row + 1);
-  const int nsplits = ceil_div(visible_end, KSPLIT);
-  // Lane layout of the attention kernel: g = lane / 16 owns dims 16*db + 4*g + i.
-  const int g = lane >> 4;
+  const int nsplits = valid ? ceil_div(visible_end, KSPLIT) : 0;
+  const int64_t sp_stride = total_q * num_q_heads;
+  const int g = lane >> 4;  // lane layout of the attention kernel
+
   RowState run;
   fresh(run);
-  for (int sp = 0; sp < nsplits; ++sp) {
-    const int64_t pr = static_cast<int64_t>(sp) * total_q * num_q_heads + item;
-    const float* pa = part_a + pr * D;
-    f32x4_v a[8];
-#pragma unroll
-    for (int db = 0; db < 8; ++db) a[db] = *reinterpret_cast<const f32x4_v*>(pa + 16 * db + 4 * g);
-    fold(run, part_ml[2 * pr], part_ml[2 * pr + 1], a);
+  // Uniform over the block: every wave takes part in every barrier.
+  int max_splits = nsplits;
+  {
+    __shared__ int s_n[4];
+    if (lane == 0) s_n[wave] = nsplits;
+    __syncthreads();
+    max_splits = max(max(s_n[0], s_n[1]), max(s_n[2], s_n[3]));
   }
-  if ((lane & 15) != 0) return;  // 4 lanes (g = 0..3) write the 128 dims
+  for (int c0 = 0; c0 < max_splits; c0 += MERGE_CHUNK) {
+    const int n = min(MERGE_CHUNK, nsplits - c0);  // this wave's splits in the chunk
+    __syncthreads();  // previous chunk folded
+    for (int e = lane; e < n * (D / 4); e += 64) {
+      const int sp = e / (D / 4);
+      const int j = e % (D / 4);
+      const int64_t pr = static_cast<int64_t>(c0 + sp) * sp_stride + item;
+      *reinterpret_cast<f32x4_v*>(&s_a[wave][sp][4 * j]) =
+          *reinterpret_cast<const f32x4_v*>(part_a + pr * D + 4 * j);
+    }
+    if (lane < 2 * max(n, 0)) {
+      const int sp = lane >> 1;
+      const int64_t pr = static_cast<int64_t>(c0 + sp) * sp_stride + item;
+      s_ml[wave][sp][lane & 1] = part_ml[2 * pr + (lane & 1)];
+    }
+    __syncthreads();
+    for (int sp = 0; sp < n; ++sp) {
+      f32x4_v a[8];
+#pragma unroll
+      for (int db = 0; db < 8; ++db)
+        a[db] = *reinterpret_cast<const f32x4_v*>(&s_a[wave][sp][16 * db + 4 * g]);
+      fold(run, s_ml[wave][sp][0], s_ml[wave][sp][1], a);
+    }
+  }
+  if (!valid || (lane & 15) != 0) return;  // 4 lanes (g = 0..3) write the 128 dims
   bf16_t* op = o + item * D;
 #pragma unroll
   for (int db = 0; db < 8; ++db) {
@@ -396,10 +465,10 @@ extern "C" int sid_extend_attention_fwd(const void* q, const void* k_cache, cons
                        num_kv_heads, num_slots, sm_scale, mtiles, total_q, (bf16_t*)o, pa, pml);
     int rc = check_launch("extend_attention");
     if (rc != SID_OK) return rc;
-    const int64_t items = total_q * num_q_heads;
-    SID_REQUIRE((items + 3) / 4 < (1ll << 31), "extend_attention: too many rows");
-    hipLaunchKernelGGL(extend_merge_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s,
-                       qo_indptr, kv_indptr, batch, num_q_heads, total_q, pa, pml, (bf16_t*)o);
+    const int64_t groups = (static_cast<int64_t>(max_extend_len) * num_q_heads + 3) / 4;
+    SID_REQUIRE(groups <= 65535, "extend_attention: too many rows per request for the merge");
+    hipLaunchKernelGGL(extend_merge_kernel, dim3(batch, (unsigned)groups), dim3(256), 0, s,
+                       qo_indptr, kv_indptr, num_q_heads, total_q, pa, pml, (bf16_t*)o);
     return check_launch("extend_attention merge");
   }
   SID_REQUIRE(mtiles <= 65535, "extend_attention: grid too large");
