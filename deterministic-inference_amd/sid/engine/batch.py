@@ -18,6 +18,7 @@ from typing import Optional
 import numpy as np
 import torch
 
+from sid.config import DUMMY_TOKEN_ID
 from sid.engine.request import Request
 from sid.kernels.jit import load_ext
 
@@ -50,6 +51,7 @@ class ForwardBatch:
     invariant: bool = False
     all_greedy: Optional[bool] = None  # host-known: every row has temperature 0
     graph_key: Optional[tuple] = None  # set when the inputs live in graph-static buffers
+    real_rows: Optional[int] = None    # rows of real requests when padded (decode graphs)
 
 
 class DecodeStatic:
@@ -121,10 +123,27 @@ def build_prefill_batch(reqs: list, kv, device: str, invariant: bool) -> Forward
     )
 
 
+def batch_bucket(bs: int, max_bs: int) -> int:
+    """Padded decode batch size of a graph: 1, 2, 4, 8, then steps of 8 up to 64, of 16 up
+    to 128, of 32 beyond (at most max_bs). Padding rows are empty requests."""
+    if bs <= 8:
+        b = 1
+        while b < bs:
+            b *= 2
+    else:
+        step = 8 if bs <= 64 else 16 if bs <= 128 else 32
+        b = -(-bs // step) * step
+    return max(bs, min(b, max_bs))
+
+
 def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
-                       static: Optional[DecodeStatic] = None) -> ForwardBatch:
+                       static: Optional[DecodeStatic] = None,
+                       pad_to: Optional[int] = None) -> ForwardBatch:
     """One new token per request; attention covers the full sequence including the
-    position being written now. With `static`, the batch lives in its fixed buffers."""
+    position being written now. With `static`, the batch lives in its fixed buffers and
+    may be padded to `pad_to` rows: padding rows are empty requests (sequence length 0,
+    table row -1, KV slot -1, greedy), whose attention output is zero and whose tokens the
+    caller ignores; real rows' results do not depend on them."""
     bs = len(reqs)
     pos = np.fromiter((r.prompt_len + r.num_output - 1 for r in reqs), dtype=np.int64, count=bs)
     for r, p in zip(reqs, pos.tolist()):
@@ -146,25 +165,32 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         d_temps, d_topp = _to_device([temps, top_ps], np.float32, device)
         kv_indices = torch.empty(total, dtype=torch.int32, device=device)
     else:
-        assert bs <= static.max_bs and total <= static.kv_indices.numel()
+        n = bs if pad_to is None else pad_to
+        assert bs <= n <= static.max_bs and total <= static.kv_indices.numel()
         mb = static.max_bs
         static.copied.synchronize()
         h64 = static.h64.numpy()
+        pad64 = (DUMMY_TOKEN_ID, 0, -1, -1, 1, -1, 0)  # ids, pos, rows, slots, spos, top_k, seed
         for i, a in enumerate((ids, pos, rows, new_slots, pos + 1, top_ks, seeds)):
             h64[i, :bs] = a
+            h64[i, bs:n] = pad64[i]
         h32 = static.h32.numpy()
         h32[:bs + 1] = indptr
+        h32[bs + 1:n + 1] = indptr[-1]
         h32[mb + 1:mb + 1 + bs] = seq_lens
+        h32[mb + 1 + bs:mb + 1 + n] = 0
         hf = static.hf32.numpy()
         hf[0, :bs] = temps
         hf[1, :bs] = top_ps
+        hf[0, bs:n] = 0.0
+        hf[1, bs:n] = 1.0
         static.i64.copy_(static.h64, non_blocking=True)
         static.i32.copy_(static.h32, non_blocking=True)
         static.f32.copy_(static.hf32, non_blocking=True)
         static.copied.record()
-        d_ids, d_pos, d_rows, d_slots, d_spos, d_topk, d_seed = (static.i64[i, :bs] for i in range(7))
-        d_indptr, d_lens = static.i32[:bs + 1], static.i32[mb + 1:mb + 1 + bs]
-        d_temps, d_topp = static.f32[0, :bs], static.f32[1, :bs]
+        d_ids, d_pos, d_rows, d_slots, d_spos, d_topk, d_seed = (static.i64[i, :n] for i in range(7))
+        d_indptr, d_lens = static.i32[:n + 1], static.i32[mb + 1:mb + 1 + n]
+        d_temps, d_topp = static.f32[0, :n], static.f32[1, :n]
         kv_indices = static.kv_indices[:total]
     load_ext().build_decode_indices(kv.req_to_token_gpu, d_rows, d_slots, d_indptr, kv_indices)
     return ForwardBatch(
@@ -175,4 +201,5 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         sample_indices=None, sample_positions=d_spos,
         temperatures=d_temps, top_ks=d_topk, top_ps=d_topp, seeds=d_seed,
         invariant=invariant, all_greedy=bool((temps == 0).all()),
+        real_rows=bs if d_ids.shape[0] != bs else None,
     )

@@ -13,7 +13,8 @@ from collections import OrderedDict
 import torch
 
 from sid.config import EngineConfig, Mode, ModelConfig
-from sid.engine.batch import DecodeStatic, ForwardBatch, ForwardMode, build_decode_batch
+from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_bucket,
+                              build_decode_batch)
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
 from sid.kernels.decode_attention import DecodeAttention
@@ -77,10 +78,13 @@ class ModelRunner:
         }
 
     def forward(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
-        """Logits of the sampled rows, or (greedy=True) their greedy tokens."""
+        """Logits of the sampled rows, or (greedy=True) their greedy tokens; rows of batch
+        padding are dropped."""
         if self.graphs is not None and fb.graph_key is not None:
-            return self.graphs.run(fb, greedy)
-        return self._forward_eager(fb, greedy)
+            out = self.graphs.run(fb, greedy)
+        else:
+            out = self._forward_eager(fb, greedy)
+        return out if fb.real_rows is None else out[:fb.real_rows]
 
     def _forward_eager(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
         return self.model.forward(fb, self.kv_cache, self.decode_attn,
@@ -97,13 +101,14 @@ class ModelRunner:
         """build_decode_batch, into the graph-static buffers when graphs are enabled."""
         if self.graphs is None:
             return build_decode_batch(reqs, self.kv_cache, self.device, invariant)
+        pad = batch_bucket(len(reqs), self.graphs.decode_static.max_bs)
         fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant,
-                                static=self.graphs.decode_static)
+                                static=self.graphs.decode_static, pad_to=pad)
         # The attention grid depends on the longest request (fixed-256 splits, or the
         # segment count of the heuristic splits): bucket it so a graph serves a range.
         bucket = seq_bucket(fb.max_seq_len)
         fb.max_seq_len = bucket
-        fb.graph_key = ("decode", len(reqs), invariant, bucket)
+        fb.graph_key = ("decode", pad, invariant, bucket)
         return fb
 
     def tag_verify(self, fb: ForwardBatch) -> ForwardBatch:
@@ -113,8 +118,9 @@ class ModelRunner:
         return fb
 
     def sample(self, fb: ForwardBatch, logits: torch.Tensor) -> torch.Tensor:
-        return _sample(logits, fb.temperatures, fb.top_ks, fb.top_ps, fb.seeds,
-                       fb.sample_positions, all_greedy=fb.all_greedy)
+        r = logits.shape[0]  # real rows (batch padding already dropped by forward)
+        return _sample(logits, fb.temperatures[:r], fb.top_ks[:r], fb.top_ps[:r], fb.seeds[:r],
+                       fb.sample_positions[:r], all_greedy=fb.all_greedy)
 
 
 def seq_bucket(n: int) -> int:

@@ -25,8 +25,8 @@ from sid.kernels.rope import RotaryEmbedding
 
 # Token counts up to this (decode batches, the 4 x 32 DVR verify pass) use split-K
 # projections whose chunk partials are folded by the consuming fused kernel; larger ones
-# (prefill) use direct GEMMs.
-SPLIT_K_MAX_TOKENS = 128
+# (prefill) use direct GEMMs. Both give identical bits.
+SPLIT_K_MAX_TOKENS = 256
 
 
 class Qwen3Model:

@@ -76,3 +76,16 @@ def test_seq_bucket():
         prev = b
     assert [seq_bucket(n) for n in (1, 256, 257, 384, 385, 2049, 3073)] == [
         256, 256, 384, 384, 512, 3072, 4096]
+
+
+def test_batch_bucket():
+    from sid.engine.batch import batch_bucket
+    sizes = set()
+    for bs in range(1, 257):
+        b = batch_bucket(bs, 256)
+        assert bs <= b <= 256
+        sizes.add(b)
+    assert len(sizes) <= 24  # few graphs for any mix of batch sizes
+    assert [batch_bucket(n, 256) for n in (1, 3, 5, 9, 64, 65, 129, 250)] == [
+        1, 4, 8, 16, 64, 80, 160, 256]
+    assert batch_bucket(100, 96) == 100  # never below the real size
