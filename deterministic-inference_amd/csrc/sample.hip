@@ -87,6 +87,271 @@ __global__ void __launch_bounds__(kThreads) argmax_kernel(const float* __restric
   }
 }
 
+// ---- stochastic sampling (temperature / top-k / top-p / seeded Gumbel-max) ---------------
+//
+// One 1024-thread workgroup per row; the reference's sample() (sid/engine/sampler.py:32-69)
+// with its truncation made exact:
+//   temperature <= 0: the greedy argmax above (first index, NaN wins).
+//   otherwise p = softmax(logits / T) (max, then the sum of exp(x - max) in a fixed order,
+//   p = exp(x - max) / sum); tokens are ranked by (p descending, index ascending); rank r is
+//   kept iff r < top_k (top_k <= 0: no limit) and the probability mass of the ranks before
+//   it is <= top_p (top_p >= 1: no limit); rank 0 is always kept. The draw is
+//   argmax over kept tokens of log(p + 1e-10) + gumbel(seed, position, token), with the
+//   reference's int64 hash (sid/engine/sampler.py:22-29) and first-index ties.
+// The mass before a rank is accumulated in 64-bit fixed point (units of 2^-48, each p
+// rounded down), so it is an exact integer sum: the cut does not depend on any summation
+// order. (The reference sums a float cumsum in sorted order; the two differ only when the
+// mass lands within rounding of top_p.) The cut is found without sorting: p >= 0, so the
+// bits of p order like p, and a 4-level 8-bit radix select over those bits, with per-wave
+// LDS histograms of (count, fixed-point mass), descends to the key of the last kept rank;
+// the keys of the row are written once to the workspace by the softmax pass. Equal keys at
+// the cut are ranked by index with a block-wide scan.
+constexpr int kSampleThreads = 1024;
+constexpr int kSampleWaves = kSampleThreads / 64;
+constexpr double kMassUnit = 281474976710656.0;  // 2^48
+constexpr float kSampleEps = 1e-10f;
+
+__device__ __forceinline__ uint64_t mass_of(uint32_t key) {
+  return static_cast<uint64_t>(static_cast<double>(__uint_as_float(key)) * kMassUnit);
+}
+
+// The reference's Gumbel noise for (seed, position, column): int64 arithmetic with
+// wraparound, floor modulo 2^24 (= the low 24 bits in two's complement), u / 2^24.
+__device__ __forceinline__ float seeded_gumbel(int64_t seed, int64_t pos, int64_t col) {
+  const uint64_t step = (static_cast<uint64_t>(seed) * 19349663ull) ^
+                        (static_cast<uint64_t>(pos) * 73856093ull);
+  const uint64_t h = (step * 8589934591ull) ^ (static_cast<uint64_t>(col) * 479001599ull);
+  const float u = static_cast<float>(h & 0xffffffull) / 16777216.0f;
+  return -logf(-logf(u + kSampleEps) + kSampleEps);
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  for (int mask = 1; mask < 64; mask <<= 1) v = fmaxf(v, lane_xor(v, mask));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < kSampleWaves; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+
+// Fixed-order float sum: xor butterfly inside each wave, then the waves in order.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  for (int mask = 1; mask < 64; mask <<= 1) v += lane_xor(v, mask);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < kSampleWaves; ++w) r += red[w];
+  return r;
+}
+
+// Best (value, index) of the block under better(); every thread gets the result.
+__device__ __forceinline__ void block_best(float& bv, int64_t& bi, float* s_v, int64_t* s_i) {
+  for (int mask = 1; mask < 64; mask <<= 1) {
+    const float ov = lane_xor(bv, mask);
+    const int lo = __builtin_amdgcn_ds_bpermute((__lane_id() ^ mask) << 2, static_cast<int>(bi));
+    const int hi = __builtin_amdgcn_ds_bpermute((__lane_id() ^ mask) << 2, static_cast<int>(bi >> 32));
+    const int64_t oi = (static_cast<int64_t>(hi) << 32) | static_cast<uint32_t>(lo);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    s_v[threadIdx.x >> 6] = bv;
+    s_i[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  bv = s_v[0];
+  bi = s_i[0];
+  for (int w = 1; w < kSampleWaves; ++w) {
+    if (better(s_v[w], s_i[w], bv, bi)) {
+      bv = s_v[w];
+      bi = s_i[w];
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kSampleThreads) sample_kernel(
+    const float* __restrict__ logits, int64_t ld, const float* __restrict__ temps,
+    const int64_t* __restrict__ top_ks, const float* __restrict__ top_ps,
+    const int64_t* __restrict__ seeds, const int64_t* __restrict__ positions, int64_t cols,
+    uint32_t* __restrict__ keys_ws, int64_t* __restrict__ out) {
+  __shared__ uint32_t h_cnt[kSampleWaves][256];
+  __shared__ uint64_t h_mass[kSampleWaves][256];
+  __shared__ float s_red[kSampleWaves];
+  __shared__ float s_bv[kSampleWaves];
+  __shared__ int64_t s_bi[kSampleWaves];
+  __shared__ int64_t s_scan[kSampleThreads];
+  __shared__ uint64_t s_sel[4];  // prefix, count above, mass above, count in final bin
+  __shared__ int64_t s_cut;
+
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const float* row = logits + r * ld;
+  const float t = temps[r];
+
+  float bv = -INFINITY;
+  int64_t bi = cols;
+  if (!(t > 0.0f)) {  // greedy row
+    for (int64_t c = tid; c < cols; c += kSampleThreads) {
+      const float v = row[c];
+      if (better(v, c, bv, bi)) {
+        bv = v;
+        bi = c;
+      }
+    }
+    block_best(bv, bi, s_bv, s_bi);
+    if (tid == 0) out[r] = bi < cols ? bi : 0;
+    return;
+  }
+
+  // softmax of logits / t; keys = bits of p
+  float mx = -INFINITY;
+  for (int64_t c = tid; c < cols; c += kSampleThreads) mx = fmaxf(mx, row[c] / t);
+  mx = block_max(mx, s_red);
+  float part = 0.0f;
+  for (int64_t c = tid; c < cols; c += kSampleThreads) part += expf(row[c] / t - mx);
+  const float sum = block_sum(part, s_red);
+  uint32_t* keys = keys_ws + r * cols;
+  for (int64_t c = tid; c < cols; c += kSampleThreads)
+    keys[c] = __float_as_uint(expf(row[c] / t - mx) / sum);
+
+  const int64_t k = top_ks[r];
+  const uint64_t k_lim = (k > 0 && k < cols) ? static_cast<uint64_t>(k) : static_cast<uint64_t>(cols);
+  const float tp = top_ps[r];
+  const bool p_lim = tp < 1.0f;
+  const uint64_t mass_lim = p_lim ? (tp > 0.0f ? static_cast<uint64_t>(static_cast<double>(tp) * kMassUnit) : 0ull)
+                                  : ~0ull;
+  uint32_t v_cut = 0;       // key of the last kept rank
+  int64_t idx_cut = cols;   // among keys == v_cut, indices <= idx_cut are kept
+  const bool truncate = p_lim || k_lim < static_cast<uint64_t>(cols);
+  if (truncate) {
+    __syncthreads();  // keys visible to the block
+    uint32_t prefix = 0, pmask = 0;
+    uint64_t cnt_above = 0, mass_above = 0, final_cnt = 0;
+    for (int level = 0; level < 4; ++level) {
+      const int shift = 24 - 8 * level;
+      for (int i = tid; i < kSampleWaves * 256; i += kSampleThreads) {
+        (&h_cnt[0][0])[i] = 0;
+        (&h_mass[0][0])[i] = 0;
+      }
+      __syncthreads();
+      for (int64_t c = tid; c < cols; c += kSampleThreads) {
+        const uint32_t key = keys[c];
+        if ((key & pmask) == prefix) {
+          const int b = (key >> shift) & 255;
+          atomicAdd(&h_cnt[wave][b], 1u);
+          atomicAdd(reinterpret_cast<unsigned long long*>(&h_mass[wave][b]),
+                    static_cast<unsigned long long>(mass_of(key)));
+        }
+      }
+      __syncthreads();
+      if (tid < 256) {  // integer totals: exact in any order
+        uint32_t cn = 0;
+        uint64_t ms = 0;
+        for (int w = 0; w < kSampleWaves; ++w) {
+          cn += h_cnt[w][tid];
+          ms += h_mass[w][tid];
+        }
+        h_cnt[0][tid] = cn;
+        h_mass[0][tid] = ms;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        // Highest bin first (larger p); the bin holding the last kept rank is the last
+        // non-empty bin whose first rank is kept: rank cnt_above with cnt_above ranks and
+        // mass_above before it. Rank 0 is always kept, so such a bin exists.
+        int chosen = -1;
+        for (int b = 255; b >= 0; --b) {
+          const uint64_t cn = h_cnt[0][b];
+          if (cn == 0) continue;
+          const uint64_t ms = h_mass[0][b];
+          chosen = b;
+          const bool next_kept = cnt_above + cn < k_lim && mass_above + ms <= mass_lim;
+          int nb = b - 1;
+          while (nb >= 0 && h_cnt[0][nb] == 0) --nb;
+          if (!next_kept || nb < 0) break;
+          cnt_above += cn;
+          mass_above += ms;
+        }
+        prefix |= static_cast<uint32_t>(chosen) << shift;
+        pmask |= 0xffu << shift;
+        final_cnt = h_cnt[0][chosen];
+        s_sel[0] = prefix;
+        s_sel[1] = cnt_above;
+        s_sel[2] = mass_above;
+        s_sel[3] = final_cnt;
+      }
+      __syncthreads();
+      prefix = static_cast<uint32_t>(s_sel[0]);
+      pmask |= 0xffu << shift;
+      cnt_above = s_sel[1];
+      mass_above = s_sel[2];
+      final_cnt = s_sel[3];
+    }
+    v_cut = prefix;
+    // Ties at the cut: how many of the final_cnt equal keys are kept (>= 1).
+    uint64_t n_keep = final_cnt;
+    if (k_lim - cnt_above < n_keep) n_keep = k_lim - cnt_above;
+    const uint64_t q = mass_of(v_cut);
+    if (p_lim && q > 0) {
+      const uint64_t by_mass = (mass_lim - mass_above) / q + 1;
+      if (by_mass < n_keep) n_keep = by_mass;
+    }
+    if (n_keep < final_cnt) {
+      // Index of the n_keep-th tie in index order: contiguous chunks, block scan.
+      const int64_t chunk = (cols + kSampleThreads - 1) / kSampleThreads;
+      const int64_t c0 = min(cols, chunk * tid);
+      const int64_t c1 = min(cols, c0 + chunk);
+      int64_t mine = 0;
+      for (int64_t c = c0; c < c1; ++c) mine += keys[c] == v_cut;
+      s_scan[tid] = mine;
+      __syncthreads();
+      for (int off = 1; off < kSampleThreads; off <<= 1) {  // inclusive scan
+        const int64_t add = tid >= off ? s_scan[tid - off] : 0;
+        __syncthreads();
+        s_scan[tid] += add;
+        __syncthreads();
+      }
+      const int64_t before = s_scan[tid] - mine;
+      const int64_t want = static_cast<int64_t>(n_keep) - 1;  // 0-based tie position
+      if (want >= before && want < before + mine) {
+        int64_t seen = before;
+        for (int64_t c = c0; c < c1; ++c) {
+          if (keys[c] == v_cut) {
+            if (seen == want) {
+              s_cut = c;
+              break;
+            }
+            ++seen;
+          }
+        }
+      }
+      __syncthreads();
+      idx_cut = s_cut;
+    }
+  }
+
+  const int64_t seed = seeds[r];
+  const int64_t pos = positions[r];
+  for (int64_t c = tid; c < cols; c += kSampleThreads) {
+    const uint32_t key = keys[c];
+    const bool keep = !truncate || key > v_cut || (key == v_cut && c <= idx_cut);
+    if (!keep) continue;
+    const float s = logf(__uint_as_float(key) + kSampleEps) + seeded_gumbel(seed, pos, c);
+    if (better(s, c, bv, bi)) {
+      bv = s;
+      bi = c;
+    }
+  }
+  block_best(bv, bi, s_bv, s_bi);
+  if (tid == 0) out[r] = bi < cols ? bi : 0;
+}
+
 }  // namespace
 }  // namespace sid
 
@@ -103,4 +368,32 @@ extern "C" int sid_argmax_rows(const float* logits, int64_t ld, int64_t* out, in
   hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), logits, ld, out, cols);
   return check_launch("argmax_rows");
+}
+
+
+extern "C" int64_t sid_sample_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return rows * cols * static_cast<int64_t>(sizeof(uint32_t));
+}
+
+extern "C" int sid_sample_rows(const float* logits, int64_t ld, const float* temperatures,
+                               const int64_t* top_ks, const float* top_ps, const int64_t* seeds,
+                               const int64_t* positions, int64_t rows, int64_t cols,
+                               void* workspace, int64_t workspace_bytes, int64_t* out,
+                               void* stream) {
+  SID_REQUIRE(rows >= 0 && cols >= 0, "sample_rows: negative size");
+  if (rows == 0) return SID_OK;
+  SID_REQUIRE(logits && temperatures && top_ks && top_ps && seeds && positions && out,
+              "sample_rows: null pointer");
+  SID_REQUIRE(cols > 0 && ld >= cols, "sample_rows: bad row stride %lld for %lld columns",
+              (long long)ld, (long long)cols);
+  SID_REQUIRE(rows < (1ll << 31) && cols < (1ll << 31), "sample_rows: too large");
+  const int64_t need = sid_sample_workspace_bytes(rows, cols);
+  SID_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "sample_rows: workspace %lld bytes, need %lld", (long long)workspace_bytes,
+              (long long)need);
+  hipLaunchKernelGGL(sample_kernel, dim3((unsigned)rows), dim3(kSampleThreads), 0,
+                     static_cast<hipStream_t>(stream), logits, ld, temperatures, top_ks, top_ps,
+                     seeds, positions, cols, static_cast<uint32_t*>(workspace), out);
+  return check_launch("sample_rows");
 }

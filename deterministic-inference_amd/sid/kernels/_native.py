@@ -39,11 +39,12 @@ _SIGNATURES = {
     "sid_flash_decode_segments_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
                                       _i32, _i32, _i32, _i32, _f32, _vp, _vp, _i32, _i32, _vp,
                                       _vp],
+    "sid_sample_rows": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp],
     "sid_linear_argmax": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
 }
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
-            "sid_linear_argmax_workspace_bytes", *_SIGNATURES)
-ABI_VERSION = 6
+            "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes", *_SIGNATURES)
+ABI_VERSION = 7
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -76,6 +77,8 @@ class NativeLib:
         self.lib.sid_extend_attention_workspace_bytes.argtypes = [_i32, _i64, _i32, _i32, _i32, _i32]
         self.lib.sid_linear_argmax_workspace_bytes.restype = ctypes.c_int64
         self.lib.sid_linear_argmax_workspace_bytes.argtypes = [_i64]
+        self.lib.sid_sample_workspace_bytes.restype = ctypes.c_int64
+        self.lib.sid_sample_workspace_bytes.argtypes = [_i64, _i64]
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.argtypes = argtypes
@@ -324,6 +327,24 @@ class NativeLib:
         _check(out.numel() == logits.shape[0], "out must have one entry per row")
         self._call("sid_argmax_rows", logits.data_ptr(), logits.stride(0), out.data_ptr(),
                    logits.shape[0], logits.shape[1], _stream(out))
+
+    def sample_rows(self, logits, temperatures, top_ks, top_ps, seeds, positions, out) -> None:
+        _check(logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2
+               and logits.stride(1) == 1, "logits must be 2-D fp32 on the GPU, unit column stride")
+        r, v = logits.shape
+        for name, t, dt in (("temperatures", temperatures, torch.float32),
+                            ("top_ks", top_ks, torch.int64), ("top_ps", top_ps, torch.float32),
+                            ("seeds", seeds, torch.int64), ("positions", positions, torch.int64),
+                            ("out", out, torch.int64)):
+            _gpu(t, name, dt)
+            _check(t.numel() == r, f"{name} must have one entry per row")
+        if r == 0:
+            return
+        ws = torch.empty(int(self.lib.sid_sample_workspace_bytes(r, v)), dtype=torch.uint8,
+                         device=logits.device)
+        self._call("sid_sample_rows", logits.data_ptr(), logits.stride(0), temperatures.data_ptr(),
+                   top_ks.data_ptr(), top_ps.data_ptr(), seeds.data_ptr(), positions.data_ptr(),
+                   r, v, ws.data_ptr(), ws.numel(), out.data_ptr(), _stream(logits))
 
     def build_decode_indices(self, req_to_token, rows, new_slots, kv_indptr, kv_indices) -> None:
         _gpu(req_to_token, "req_to_token", torch.int32)

@@ -36,6 +36,16 @@ def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor, top_ks: torch.Tensor,
+                top_ps: torch.Tensor, seeds: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    """Per-row greedy / temperature + top-k + top-p + seeded Gumbel-max draw (HIP)."""
+    out = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
+    load_ext().sample_rows(logits.contiguous(), temperatures.float().contiguous(),
+                           top_ks.long().contiguous(), top_ps.float().contiguous(),
+                           seeds.long().contiguous(), positions.long().contiguous(), out)
+    return out
+
+
 def silu_mul_partials(partials: torch.Tensor) -> torch.Tensor:
     """SwiGLU straight from the gate_up projection's chunk partials [C, T, 2I] -> [T, I]."""
     _, t, two_i = partials.shape

@@ -226,6 +226,25 @@ int sid_gather_rows(const void* table, const int64_t* idx, void* out, int64_t n,
                     int64_t row_elems, int64_t table_rows, void* stream);
 
 /*
+ * Per-row sampling over fp32 logits [rows, cols] (row stride ld), the
+ * reference's sample(), sid/engine/sampler.py:32-69: temperature <= 0 gives the
+ * greedy argmax (as sid_argmax_rows); otherwise p = softmax(logits / T), ranks
+ * by (p descending, index ascending), rank r kept iff r < top_k (top_k <= 0:
+ * no limit) and the mass of the ranks before it <= top_p (top_p >= 1: no
+ * limit; mass summed exactly in units of 2^-48, each p rounded down), rank 0
+ * always kept, token = argmax over kept columns of log(p + 1e-10) +
+ * gumbel(seed, position, column) (the reference's int64 hash,
+ * sampler.py:22-29; first index on ties). temperatures, top_ps fp32 [rows];
+ * top_ks, seeds, positions int64 [rows]; out int64 [rows]. workspace:
+ * sid_sample_workspace_bytes(rows, cols) bytes.
+ */
+int64_t sid_sample_workspace_bytes(int64_t rows, int64_t cols);
+int sid_sample_rows(const float* logits, int64_t ld, const float* temperatures,
+                    const int64_t* top_ks, const float* top_ps, const int64_t* seeds,
+                    const int64_t* positions, int64_t rows, int64_t cols, void* workspace,
+                    int64_t workspace_bytes, int64_t* out, void* stream);
+
+/*
  * Greedy lm_head: out_idx[r] = argmax over columns of (x @ w^T + bias)[r, :],
  * the logits taken as sid_linear computes them (bf16-rounded, fp32 storage)
  * and compared with sid_argmax_rows's order. Fuses the lm_head projection

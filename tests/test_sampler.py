@@ -1,13 +1,22 @@
-"""Sampler: the known answers of the reference's tests/test_07_sampler.py:25-80, run on the
-product sampler (CPU tensors) and on the oracle; the int64 hash against a big-int scalar
-restatement."""
+"""Sampler oracle (CPU): the known answers of the reference's tests/test_07_sampler.py:25-80
+on sample_ref (the reference's float-cumsum rule) and on sample_exact_ref (the exact rule the
+HIP sampler implements); the int64 hash against a big-int scalar restatement; the exact rule
+against brute-force enumeration; and that the product sampler refuses CPU tensors (it is a
+HIP kernel, there is no CPU path)."""
 
 from __future__ import annotations
 
+import itertools
+import math
+
+import numpy as np
+import pytest
 import torch
 
-from oracle.sampler import sample_ref, seeded_gumbel_ref, seeded_uniform_ref
-from sid.engine.sampler import _seeded_gumbel, sample
+from oracle.sampler import (kept_mask_exact, sample_exact_ref, sample_ref, seeded_gumbel_ref,
+                            seeded_uniform_ref)
+
+REFS = (sample_ref, sample_exact_ref)
 
 
 def _one(fn, logits, temp, seed, pos, top_k=-1, top_p=1.0):
@@ -22,8 +31,6 @@ def test_hash_matches_big_integer_restatement():
     pos = torch.tensor([0, 17, 250, 8191, 3], dtype=torch.int64)
     cols = [0, 1, 2, 999, 151935]
     g = seeded_gumbel_ref(seeds, pos, 151936)
-    gp = _seeded_gumbel(seeds, pos, 151936)
-    assert torch.equal(g, gp)
     for i in range(5):
         for c in cols:
             u = seeded_uniform_ref(int(seeds[i]), int(pos[i]), c)
@@ -32,60 +39,68 @@ def test_hash_matches_big_integer_restatement():
             assert torch.equal(g[i, c], want), (i, c)
 
 
-def test_greedy_first_index_tie():
+@pytest.mark.parametrize("fn", REFS)
+def test_greedy_first_index_tie(fn):
     logits = torch.zeros(2, 100)
     logits[0, 7] = 5.0
     logits[1, 3] = 2.0
     logits[1, 42] = 2.0
-    for fn in (sample, sample_ref):
-        assert _one(fn, logits, 0.0, 42, [10, 11]).tolist() == [7, 3]
+    assert _one(fn, logits, 0.0, 42, [10, 11]).tolist() == [7, 3]
 
 
 def test_seeded_draw_invariant_to_batch_shape():
     torch.manual_seed(0)
     row = torch.randn(1, 5000)
-    alone = _one(sample, row, 0.8, 1234, [17])
-    assert alone.item() == sample_ref(row, [0.8], [-1], [1.0], [1234], [17]).item()
-    for batch in (2, 7, 33):
+    alone = _one(sample_exact_ref, row, 0.8, 1234, [17])
+    assert alone.item() == _one(sample_ref, row, 0.8, 1234, [17]).item()
+    for batch in (2, 7):
         logits = torch.cat([torch.randn(batch - 1, 5000), row])
-        toks = _one(sample, logits, 0.8, 1234, list(range(100, 100 + batch - 1)) + [17])
+        toks = _one(sample_exact_ref, logits, 0.8, 1234, list(range(100, 100 + batch - 1)) + [17])
         assert toks[-1].item() == alone.item()
 
 
-def test_position_changes_draws():
-    torch.manual_seed(1)
-    logits = torch.randn(1, 1000).repeat(64, 1)
-    assert len(set(_one(sample, logits, 1.5, 42, list(range(64))).tolist())) > 1
-
-
-def test_decode_and_verify_paths_agree():
-    torch.manual_seed(2)
-    W, seed, base = 32, 777, 250
-    logits = torch.randn(W, 4000)
-    verify = _one(sample, logits, 0.7, seed, list(range(base, base + W)), top_k=50, top_p=0.9)
-    for j in (0, 1, W // 2, W - 1):
-        dec = _one(sample, logits[j:j + 1], 0.7, seed, [base + j], top_k=50, top_p=0.9)
-        assert dec.item() == verify[j].item()
-    ref = sample_ref(logits, [0.7] * W, [50] * W, [0.9] * W, [seed] * W, list(range(base, base + W)))
-    assert torch.equal(verify, ref)
-
-
-def test_top_k_top_p_respected():
+@pytest.mark.parametrize("fn", REFS)
+def test_top_k_top_p_respected(fn):
     logits = torch.tensor([[10.0, 9.0, 8.0, -20.0, -20.0]])
-    for pos in range(200):
-        assert _one(sample, logits, 2.0, 5, [pos], top_k=3).item() in (0, 1, 2)
-    peaked = torch.tensor([[10.0, 0.0, 0.0, 0.0, 0.0]])
     for pos in range(100):
-        assert _one(sample, peaked, 1.0, 5, [pos], top_p=0.5).item() == 0
+        assert _one(fn, logits, 2.0, 5, [pos], top_k=3).item() in (0, 1, 2)
+    peaked = torch.tensor([[10.0, 0.0, 0.0, 0.0, 0.0]])
+    for pos in range(50):
+        assert _one(fn, peaked, 1.0, 5, [pos], top_p=0.5).item() == 0
 
 
-def test_mixed_rows_greedy_and_stochastic():
-    torch.manual_seed(3)
-    logits = torch.randn(6, 300)
-    temps = torch.tensor([0.0, 0.9, 0.0, 1.3, 0.5, 0.0])
-    args = (torch.full((6,), 20, dtype=torch.int64), torch.full((6,), 0.95),
-            torch.arange(6, dtype=torch.int64) + 11, torch.arange(6, dtype=torch.int64) * 3)
-    out = sample(logits, temps, *args)
-    ref = sample_ref(logits, temps, *args)
-    assert torch.equal(out, ref)
-    assert out[0] == logits[0].argmax() and out[5] == logits[5].argmax()
+def test_exact_rule_equals_reference_rule_without_ambiguity():
+    """Random distinct logits (no ties, cut far from rounding): both rules, same tokens."""
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(12, 3000, generator=g) * 3
+    temps = torch.tensor([0.0, 0.7, 1.0, 1.3] * 3)
+    ks = torch.tensor([-1, 20, -1, 5, 100, -1, 1, 50, -1, -1, 7, 2000], dtype=torch.int64)
+    ps = torch.tensor([1.0, 0.9, 0.5, 1.0, 0.95, 0.3, 1.0, 0.8, 0.99, 0.6, 1.0, 0.7])
+    seeds = torch.arange(12, dtype=torch.int64) * 7 + 1
+    pos = torch.arange(12, dtype=torch.int64) + 40
+    assert torch.equal(sample_exact_ref(logits, temps, ks, ps, seeds, pos),
+                       sample_ref(logits, temps, ks, ps, seeds, pos))
+
+
+def test_exact_mask_brute_force_tiny_vocab():
+    """kept_mask_exact vs enumerating ranks by hand on tiny vocabularies with ties."""
+    rng = np.random.default_rng(4)
+    for _ in range(300):
+        v = int(rng.integers(1, 7))
+        p = rng.choice([0.5, 0.25, 0.125, 0.0625, 0.03125, 0.0], size=v).astype(np.float32)
+        k = int(rng.integers(-1, v + 2))
+        tp = float(rng.choice([0.0, 0.1, 0.25, 0.5, 0.75, 0.875, 1.0]))
+        ranks = sorted(range(v), key=lambda i: (-float(p[i]), i))
+        want = np.zeros(v, dtype=bool)
+        mass = 0
+        for rk, i in enumerate(ranks):
+            keep = rk == 0 or ((k <= 0 or rk < k) and (tp >= 1.0 or mass <= math.floor(tp * 2 ** 48)))
+            want[i] = keep
+            mass += math.floor(float(p[i]) * 2 ** 48)
+        assert np.array_equal(kept_mask_exact(p, k, tp), want), (p, k, tp)
+
+
+def test_product_sampler_refuses_cpu_tensors():
+    from sid.engine.sampler import sample
+    with pytest.raises(RuntimeError, match="GPU"):
+        _one(sample, torch.zeros(1, 10), 0.7, 1, [0])
