@@ -1,0 +1,187 @@
+// Native executor of one Qwen3 forward over an extend batch (prefill or DVR verify): the
+// kernel sequence of sid/model/qwen3.py:88-115 (this build's Qwen3Model.forward for
+// non-decode batches) issued from C++, so a forward costs ~3 us of host time per launch
+// instead of a Python op per kernel. It calls the library's own entry points in the same
+// order with the same buffers' contents, so its results are bit-identical to the Python
+// driver's (checked by the GPU tests). All temporaries come from one caller workspace.
+#include "common.h"
+
+#include <algorithm>
+
+namespace sid {
+namespace {
+
+constexpr int64_t kAlign = 256;
+
+struct Carver {
+  char* base;
+  int64_t used = 0;
+  int64_t cap;
+  void* take(int64_t bytes) {
+    used = (used + kAlign - 1) / kAlign * kAlign;
+    void* p = base ? base + used : nullptr;
+    used += bytes;
+    return p;
+  }
+};
+
+struct Layout {
+  void* resid;
+  void* x;
+  void* proj;     // split-K partials (fp32) or a bf16 projection output
+  void* q;
+  void* attn;
+  void* act;
+  void* ext_ws;
+  int64_t ext_ws_bytes;
+  void* rows;
+  void* argmax_ws;
+  int64_t argmax_ws_bytes;
+  int64_t total;
+};
+
+Layout plan(const sid_qwen3_model* m, const sid_extend_batch* b, void* ws) {
+  const int64_t t = b->num_tokens;
+  const int64_t h = m->hidden;
+  const int64_t wq = static_cast<int64_t>(m->num_q_heads + 2 * m->num_kv_heads) * m->head_dim;
+  const int64_t ao = static_cast<int64_t>(m->num_q_heads) * m->head_dim;
+  const int64_t inter = m->intermediate;
+  const bool split = t <= m->split_k_max_tokens;
+  const int64_t r = b->sample_indices ? b->num_samples : t;
+  Carver c{static_cast<char*>(ws), 0, 0};
+  Layout l{};
+  l.resid = c.take(t * h * 2);
+  l.x = c.take(t * h * 2);
+  int64_t proj = 0;
+  if (split) {
+    proj = std::max({h / 256 * wq, ao / 256 * h, h / 256 * 2 * inter, inter / 256 * h}) * t * 4;
+  } else {
+    proj = std::max(wq, 2 * inter) * t * 2;
+  }
+  l.proj = c.take(proj);
+  l.q = c.take(t * ao * 2);
+  l.attn = c.take(t * ao * 2);
+  l.act = c.take(t * inter * 2);
+  const int64_t kvmax = b->max_kv_len > 0 ? b->max_kv_len : b->num_kv_indices;
+  l.ext_ws_bytes = sid_extend_attention_workspace_bytes(b->batch, t, m->num_q_heads,
+                                                        m->num_kv_heads,
+                                                        std::max(b->max_extend_len, 1),
+                                                        static_cast<int>(kvmax));
+  l.ext_ws = l.ext_ws_bytes > 0 ? c.take(l.ext_ws_bytes) : nullptr;
+  l.rows = b->sample_indices ? c.take(r * h * 2) : nullptr;
+  l.argmax_ws_bytes = sid_linear_argmax_workspace_bytes(r);
+  l.argmax_ws = l.argmax_ws_bytes > 0 ? c.take(l.argmax_ws_bytes) : nullptr;
+  l.total = c.used;
+  return l;
+}
+
+#define SID_TRY(call)               \
+  do {                              \
+    const int rc_ = (call);         \
+    if (rc_ != SID_OK) return rc_;  \
+  } while (0)
+
+}  // namespace
+}  // namespace sid
+
+using namespace sid;
+
+extern "C" int64_t sid_qwen3_extend_workspace_bytes(const sid_qwen3_model* m,
+                                                    const sid_extend_batch* b) {
+  if (m == nullptr || b == nullptr || b->num_tokens <= 0) return 0;
+  return plan(m, b, nullptr).total;
+}
+
+extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_extend_batch* b,
+                                        void* workspace, int64_t workspace_bytes, float* logits,
+                                        int64_t* greedy_tokens, void* stream) {
+  SID_REQUIRE(m && b, "qwen3_extend_forward: null descriptor");
+  SID_REQUIRE(b->num_tokens >= 0 && b->batch >= 0, "qwen3_extend_forward: negative size");
+  if (b->num_tokens == 0) return SID_OK;
+  SID_REQUIRE(m->layers && m->embed && m->final_norm && m->lm_head && m->cos_sin,
+              "qwen3_extend_forward: null weight");
+  SID_REQUIRE(b->input_ids && b->positions && b->out_slots && b->qo_indptr && b->kv_indptr &&
+                  b->kv_indices,
+              "qwen3_extend_forward: null batch field");
+  SID_REQUIRE(logits || greedy_tokens, "qwen3_extend_forward: no output");
+  const int64_t t = b->num_tokens;
+  const int64_t r = b->sample_indices ? b->num_samples : t;
+  SID_REQUIRE(r > 0, "qwen3_extend_forward: no sampled rows");
+  SID_REQUIRE(logits || r <= 256, "qwen3_extend_forward: greedy over %lld rows needs a logits buffer",
+              (long long)r);
+  const Layout l = plan(m, b, workspace);
+  SID_REQUIRE(workspace && workspace_bytes >= l.total,
+              "qwen3_extend_forward: workspace %lld bytes, need %lld",
+              (long long)workspace_bytes, (long long)l.total);
+  const int h = m->hidden;
+  const int hq = m->num_q_heads, hkv = m->num_kv_heads, d = m->head_dim;
+  const int64_t wq = static_cast<int64_t>(hq + 2 * hkv) * d;
+  const int64_t ao = static_cast<int64_t>(hq) * d;
+  const int64_t inter = m->intermediate;
+  const float eps = m->rms_eps;
+  const bool split = t <= m->split_k_max_tokens;
+  float* part = static_cast<float*>(l.proj);
+  const int kvmax = static_cast<int>(b->max_kv_len > 0 ? b->max_kv_len : b->num_kv_indices);
+
+  // residual = embed[ids]; x = rmsnorm(residual, input_ln of layer 0)
+  SID_TRY(sid_gather_rows(m->embed, b->input_ids, l.resid, t, h, m->vocab, stream));
+  SID_TRY(sid_rmsnorm(l.resid, m->layers[0].input_ln, l.x, t, h, eps, stream));
+  for (int i = 0; i < m->num_layers; ++i) {
+    const sid_qwen3_layer& lw = m->layers[i];
+    // qkv projection -> q/k-norm, RoPE, KV-cache write
+    if (split) {
+      SID_TRY(sid_linear_partials(l.x, h, lw.qkv, part, t, wq, h, stream));
+      SID_TRY(sid_qkv_post(nullptr, part, h / 256, t, hq, hkv, d, lw.q_norm, lw.k_norm, eps,
+                           b->positions, m->cos_sin, m->max_positions, b->out_slots, l.q,
+                           lw.k_cache, lw.v_cache, m->num_slots, stream));
+    } else {
+      SID_TRY(sid_linear(l.x, h, lw.qkv, nullptr, l.proj, t, wq, h, 0, stream));
+      SID_TRY(sid_qkv_post(l.proj, nullptr, 0, t, hq, hkv, d, lw.q_norm, lw.k_norm, eps,
+                           b->positions, m->cos_sin, m->max_positions, b->out_slots, l.q,
+                           lw.k_cache, lw.v_cache, m->num_slots, stream));
+    }
+    SID_TRY(sid_extend_attention_fwd(l.q, lw.k_cache, lw.v_cache, b->qo_indptr, b->kv_indptr,
+                                     b->kv_indices, b->batch, t, hq, hkv, d, m->num_slots,
+                                     std::max(b->max_extend_len, 1), kvmax, m->sm_scale,
+                                     l.ext_ws, l.ext_ws_bytes, l.attn, stream));
+    // o projection; residual += o; x = rmsnorm(residual, post_ln)
+    if (split) {
+      SID_TRY(sid_linear_partials(l.attn, ao, lw.o, part, t, h, ao, stream));
+      SID_TRY(sid_fused_add_rmsnorm_partials(part, static_cast<int>(ao / 256), l.resid,
+                                             lw.post_ln, l.x, t, h, eps, stream));
+    } else {
+      SID_TRY(sid_linear(l.attn, ao, lw.o, nullptr, l.x, t, h, ao, 0, stream));
+      SID_TRY(sid_fused_add_rmsnorm(l.x, l.resid, lw.post_ln, t, h, eps, stream));
+    }
+    // act = silu(gate) * up
+    if (split) {
+      SID_TRY(sid_linear_partials(l.x, h, lw.gate_up, part, t, 2 * inter, h, stream));
+      SID_TRY(sid_silu_mul_partials(part, h / 256, l.act, t, inter, stream));
+    } else {
+      SID_TRY(sid_linear(l.x, h, lw.gate_up, nullptr, l.proj, t, 2 * inter, h, 0, stream));
+      SID_TRY(sid_silu_mul(l.proj, l.act, t, inter, stream));
+    }
+    // down projection; residual += down; x = rmsnorm(residual, next input_ln / final norm)
+    const void* next_w = i + 1 < m->num_layers ? m->layers[i + 1].input_ln : m->final_norm;
+    if (split) {
+      SID_TRY(sid_linear_partials(l.act, inter, lw.down, part, t, h, inter, stream));
+      SID_TRY(sid_fused_add_rmsnorm_partials(part, static_cast<int>(inter / 256), l.resid,
+                                             next_w, l.x, t, h, eps, stream));
+    } else {
+      SID_TRY(sid_linear(l.act, inter, lw.down, nullptr, l.x, t, h, inter, 0, stream));
+      SID_TRY(sid_fused_add_rmsnorm(l.x, l.resid, next_w, t, h, eps, stream));
+    }
+  }
+  const void* rows = l.x;
+  if (b->sample_indices) {
+    SID_TRY(sid_gather_rows(l.x, b->sample_indices, l.rows, r, h, t, stream));
+    rows = l.rows;
+  }
+  if (greedy_tokens && r <= 256) {
+    return sid_linear_argmax(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, l.argmax_ws,
+                             l.argmax_ws_bytes, greedy_tokens, stream);
+  }
+  SID_TRY(sid_linear(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, 1, stream));
+  if (greedy_tokens) return sid_argmax_rows(logits, m->vocab, greedy_tokens, r, m->vocab, stream);
+  return SID_OK;
+}

@@ -270,6 +270,175 @@ __global__ void __launch_bounds__(NW * 64) linear_chunk_kernel(
   }
 }
 
+// ---- large-M tiled GEMM (prefill) ---------------------------------------------------------
+//
+// 128 x 128 output tile per 4-wave workgroup (wave (wm, wn): 64 x 64 = 4 x 4 MFMA blocks),
+// K streamed in 64-deep sub-tiles through double-buffered LDS (the next sub-tile's x and w
+// rows are loaded into registers while the current one's MFMAs run). Every output element
+// sees the canonical order: each 256-wide chunk accumulated from zero by 8 MFMA k-steps in
+// increasing k (two per sub-tile), the chunk sums left-folded c0 + c1 + ..., then + bias and
+// one rounding; the operand layout per MFMA is linear_kernel's. So the bits equal
+// sid_linear's for any M, while the tile reuse (each x row feeds 128 columns, each weight
+// row 128 rows) makes large M MFMA-bound instead of bound by re-reading operands.
+constexpr int TT_K = 64;
+constexpr int TT_KS = TT_K + 8;        // LDS row stride (bf16): 144 bytes
+constexpr int TT_SUB_PER_CHUNK = KC / TT_K;
+
+// WM x WN waves; wave (wm, wn) owns MB x NB MFMA blocks = (16 MB) x (16 NB) outputs.
+template <int WM, int WN, int MB, int NB>
+__global__ void __launch_bounds__(WM * WN * 64) linear_tiled_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
+    const bf16_t* __restrict__ bias, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
+    int out_fp32) {
+  constexpr int TM = WM * MB * 16;
+  constexpr int TN = WN * NB * 16;
+  constexpr int THREADS = WM * WN * 64;
+  constexpr int LA = TM * (TT_K / 8) / THREADS;  // 16-byte x vectors per thread per sub-tile
+  constexpr int LB = TN * (TT_K / 8) / THREADS;
+  static_assert(LA * THREADS == TM * (TT_K / 8) && LB * THREADS == TN * (TT_K / 8), "tile");
+  __shared__ __align__(16) bf16_t sa[2][TM * TT_KS];
+  __shared__ __align__(16) bf16_t sb[2][TN * TT_KS];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * TN;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * TM;
+
+  // Sub-tile loads (8 vectors of 16 bytes per 64-deep row). Rows past M (x) or N (w) are
+  // clamped to the last valid row; their results are dropped.
+  const bf16_t* xrow[LA];
+  const bf16_t* wrow[LB];
+  int arow[LA], avec[LA], brow[LB], bvec[LB];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int v = tid + THREADS * i;
+    arow[i] = v >> 3;
+    avec[i] = v & 7;
+    xrow[i] = x + min<int64_t>(m0 + arow[i], M - 1) * ldx + avec[i] * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < LB; ++i) {
+    const int v = tid + THREADS * i;
+    brow[i] = v >> 3;
+    bvec[i] = v & 7;
+    wrow[i] = w + min<int64_t>(n0 + brow[i], N - 1) * K + bvec[i] * 8;
+  }
+  bf16x8_v ra[LA], rb[LB];
+  auto load_sub = [&](int kt) {
+    const int64_t k0 = static_cast<int64_t>(kt) * TT_K;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) ra[i] = ld_frag(xrow[i] + k0);
+#pragma unroll
+    for (int i = 0; i < LB; ++i) rb[i] = ld_frag(wrow[i] + k0);
+  };
+  auto store_sub = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      *reinterpret_cast<bf16x8_v*>(&sa[buf][arow[i] * TT_KS + avec[i] * 8]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < LB; ++i)
+      *reinterpret_cast<bf16x8_v*>(&sb[buf][brow[i] * TT_KS + bvec[i] * 8]) = rb[i];
+  };
+
+  f32x4_v acc[MB][NB], tot[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  const int nsub = static_cast<int>(K / TT_K);
+  load_sub(0);
+  store_sub(0);
+  __syncthreads();
+  for (int kt = 0; kt < nsub; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nsub) load_sub(kt + 1);
+#pragma unroll
+    for (int s = 0; s < TT_K / KSTEP; ++s) {
+      bf16x8_v af[MB], bfv[NB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        af[mb] = *reinterpret_cast<const bf16x8_v*>(
+            &sa[cur][(MB * 16 * wm + 16 * mb + r) * TT_KS + KSTEP * s + 8 * g]);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        bfv[nb] = *reinterpret_cast<const bf16x8_v*>(
+            &sb[cur][(NB * 16 * wn + 16 * nb + r) * TT_KS + KSTEP * s + 8 * g]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mb], bfv[nb], acc[mb][nb], 0, 0, 0);
+      }
+    }
+    if (kt % TT_SUB_PER_CHUNK == TT_SUB_PER_CHUNK - 1) {  // chunk complete: fold, restart
+      const bool first = kt < TT_SUB_PER_CHUNK;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          if (first) {
+            tot[mb][nb] = acc[mb][nb];
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tot[mb][nb][i] += acc[mb][nb][i];
+          }
+          acc[mb][nb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+      }
+    }
+    if (kt + 1 < nsub) {
+      store_sub(cur ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // Lane holds rows 16*mb + 4*g + i, column 16*nb + r of the wave's block.
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t col = n0 + NB * 16 * wn + 16 * nb + r;
+    if (col >= N) continue;
+    const float bv = bias != nullptr ? bf16_to_f32(bias[col]) : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + MB * 16 * wm + 16 * mb + 4 * g + i;
+        if (row >= M) continue;
+        float v = tot[mb][nb][i];
+        if (bias != nullptr) v += bv;
+        if (out_fp32) {
+          static_cast<float*>(y)[row * N + col] = round_bf16(v);
+        } else {
+          static_cast<bf16_t*>(y)[row * N + col] = f32_to_bf16(v);
+        }
+      }
+    }
+  }
+}
+
+template <int WM, int WN, int MB, int NB>
+void launch_tiled(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
+                  int64_t n, int64_t k, int out_fp32, hipStream_t s) {
+  constexpr int TM = WM * MB * 16, TN = WN * NB * 16;
+  const dim3 grid((unsigned)((n + TN - 1) / TN), (unsigned)((m + TM - 1) / TM));
+  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB>), grid, dim3(WM * WN * 64), 0, s,
+                     (const bf16_t*)x, ldx, (const bf16_t*)w, (const bf16_t*)bias, y, m, n, k,
+                     out_fp32);
+}
+
+// sid_linear takes the tiled kernel from this many rows up: 8 waves (4 x 2), each 32 x 64
+// outputs (a 128 x 128 tile), or 32 x 32 (128 x 64) when 128 x 128 tiles would leave fewer
+// than two workgroups per CU. (Measured on prefill shapes: 25-29% of the bf16 MFMA peak at
+// M >= 2048 vs 8% for the 64-row-group kernel; 4 waves of 64 x 64 held both accumulator
+// sets in AGPRs at one wave per SIMD and reached 13%.)
+constexpr int64_t kTiledMinM = 256;
+constexpr int64_t kTiledWideMinTiles = 512;
+
 // K of the streaming kernel below, its chunk count and LDS row stride of staged x.
 constexpr int WIDE_K = 1024;
 constexpr int WIDE_NCH = WIDE_K / KC;
@@ -621,6 +790,16 @@ extern "C" int sid_linear(const void* x, int64_t ldx, const void* w, const void*
   if (stream_shape_ok(m, n, k) && n >= kStreamMinN) {
     launch_stream<false>(x, ldx, w, bias, y, static_cast<int>(m), static_cast<int>(n), out_fp32,
                          nullptr, nullptr, s);
+    return check_launch("linear");
+  }
+  if (m >= kTiledMinM) {
+    SID_REQUIRE((m + 63) / 64 <= 65535, "linear: too many rows");
+    const int64_t wide_tiles = ((m + 127) / 128) * ((n + 127) / 128);
+    if (wide_tiles >= kTiledWideMinTiles) {
+      launch_tiled<4, 2, 2, 4>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
+    } else {
+      launch_tiled<4, 2, 2, 2>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
+    }
     return check_launch("linear");
   }
   launch_any(pick_waves(n, m, false), x, ldx, w, bias, y, m, n, k, out_fp32, nullptr, s);

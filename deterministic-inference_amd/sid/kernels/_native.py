@@ -43,8 +43,9 @@ _SIGNATURES = {
     "sid_linear_argmax": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
 }
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
-            "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes", *_SIGNATURES)
-ABI_VERSION = 7
+            "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes",
+            "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward", *_SIGNATURES)
+ABI_VERSION = 8
 
 
 def _check(cond: bool, msg: str) -> None:

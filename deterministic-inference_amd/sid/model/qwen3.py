@@ -38,6 +38,10 @@ class Qwen3Model:
                                     mcfg.rope_theta, device)
         self.sm_scale = mcfg.head_dim ** -0.5
         self.invariant_gemm = False
+        # Prefill / verify batches go through the native executor (one library call per
+        # forward); False keeps the op-by-op Python driver below (identical bits).
+        self.native_extend = True
+        self._native = None
 
     def set_batch_invariant(self, enabled: bool) -> None:
         # Every GEMM here already reduces in an M-independent order (see
@@ -76,6 +80,8 @@ class Qwen3Model:
         Same op order as sid/model/qwen3.py:88-115; the residual add + RMSNorm that follows
         each o / down projection consumes the projection directly (fused), and the down
         projection of layer i feeds layer i+1's input norm (or the final norm)."""
+        if self.native_extend and fb.mode != ForwardMode.DECODE:
+            return self._native_forward(fb, kv_cache, greedy)
         cfg = self.cfg
         eps = cfg.rms_norm_eps
         layers = self.w["layers"]
@@ -106,3 +112,10 @@ class Qwen3Model:
                 return linear_argmax(rows, self.w["lm_head"])
             return argmax_rows(linear(rows, self.w["lm_head"], out_fp32=True))
         return linear(rows, self.w["lm_head"], out_fp32=True)
+
+    def _native_forward(self, fb: ForwardBatch, kv_cache, greedy: bool) -> torch.Tensor:
+        from sid.model.native import NativeQwen3
+        key = (id(kv_cache), tuple(kv_cache.layer(0)[0].shape))
+        if self._native is None or self._native.key != key:
+            self._native = NativeQwen3(self, kv_cache, SPLIT_K_MAX_TOKENS)
+        return self._native.forward(fb, greedy)

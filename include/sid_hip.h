@@ -259,6 +259,72 @@ int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bia
                       int64_t* out_idx, void* stream);
 
 /*
+ * Native executor of one Qwen3 forward over an extend batch (prefill or DVR
+ * verify): the kernel sequence of sid/model/qwen3.py:88-115 issued from C++
+ * (embedding, per layer: qkv projection + q/k-norm + RoPE + cache write,
+ * extend attention, o projection + residual add + RMSNorm, gate_up + SwiGLU,
+ * down projection + residual add + RMSNorm; then the sampled rows' lm_head).
+ * Results are bit-identical to issuing the same entry points one by one. It
+ * has no counterpart of its own in the reference, whose forward is Python.
+ * Projections of <= split_k_max_tokens tokens use the split-K path. Outputs:
+ * logits fp32 [R, vocab] and/or greedy_tokens int64 [R] (R = num_samples, or
+ * num_tokens without sample_indices; greedy without logits needs R <= 256).
+ */
+typedef struct {
+  const void* input_ln;
+  const void* qkv;
+  const void* q_norm;
+  const void* k_norm;
+  const void* o;
+  const void* post_ln;
+  const void* gate_up;
+  const void* down;
+  void* k_cache;
+  void* v_cache;
+} sid_qwen3_layer;
+
+typedef struct {
+  int num_layers;
+  int hidden;
+  int num_q_heads;
+  int num_kv_heads;
+  int head_dim;
+  int intermediate;
+  int vocab;
+  float rms_eps;
+  float sm_scale;
+  int split_k_max_tokens;
+  int64_t num_slots;
+  int64_t max_positions;
+  const float* cos_sin;
+  const void* embed;
+  const void* final_norm;
+  const void* lm_head;
+  const sid_qwen3_layer* layers;
+} sid_qwen3_model;
+
+typedef struct {
+  int64_t num_tokens;
+  int batch;
+  int max_extend_len;
+  int max_kv_len;  /* <= 0: num_kv_indices */
+  int64_t num_kv_indices;
+  const int64_t* input_ids;
+  const int64_t* positions;
+  const int64_t* out_slots;
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int64_t* sample_indices; /* NULL: every token row */
+  int64_t num_samples;
+} sid_extend_batch;
+
+int64_t sid_qwen3_extend_workspace_bytes(const sid_qwen3_model* m, const sid_extend_batch* b);
+int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_extend_batch* b, void* workspace,
+                             int64_t workspace_bytes, float* logits, int64_t* greedy_tokens,
+                             void* stream);
+
+/*
  * out[r] = argmax(logits[r, :]) with first-index tie-break; fp32 logits
  * [rows, cols] with row stride ld; out int64 [rows]. NaN compares greater
  * than every number (torch.argmax semantics). Replaces the greedy branch of
