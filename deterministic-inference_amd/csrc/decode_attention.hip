@@ -112,9 +112,10 @@ __host__ __device__ __forceinline__ bool segment_range(int seq_len, int n_splits
   return start < end;
 }
 
-// NW waves per workgroup; TPL tokens per wave iteration; PF: software pipeline (the next
-// iteration's rows load while this one computes; twice the tile registers).
-template <int NW, int TPL, bool PF>
+// NW waves per workgroup; TPL tokens per wave iteration. (A software-pipelined variant,
+// the next iteration's rows loading during this one's math, doubled the tile registers,
+// lowered occupancy and measured no faster.)
+template <int NW, int TPL>
 __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ kv_indptr,
@@ -231,28 +232,11 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
     }
   };
 
-  if constexpr (!PF) {
-    for (int t0 = start + wave * TPL; t0 < end; t0 += IT) {
-      bool ok[TPL];
-      TileRegs<TPL> r;
-      load_tile(t0, ok, r);
-      compute(ok, r);
-    }
-  } else {
-    // Two register tiles alternate: the next iteration's rows load during this one's math.
-    bool sa[TPL], sb[TPL];
-    TileRegs<TPL> ra, rb;
-    int t0 = start + wave * TPL;
-    if (t0 < end) load_tile(t0, sa, ra);
-    while (t0 < end) {
-      if (t0 + IT < end) load_tile(t0 + IT, sb, rb);
-      compute(sa, ra);
-      t0 += IT;
-      if (t0 >= end) break;
-      if (t0 + IT < end) load_tile(t0 + IT, sa, ra);
-      compute(sb, rb);
-      t0 += IT;
-    }
+  for (int t0 = start + wave * TPL; t0 < end; t0 += IT) {
+    bool ok[TPL];
+    TileRegs<TPL> r;
+    load_tile(t0, ok, r);
+    compute(ok, r);
   }
 
 #pragma unroll
@@ -344,16 +328,15 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_kernel(
 // in-segment reduction order; they are constants, independent of batch and policy).
 constexpr int kWaves = 4;
 constexpr int kTokPerLane = 4;
-constexpr bool kPipelined = false;
 
-template <int NW = kWaves, int TPL = kTokPerLane, bool PF = kPipelined>
+template <int NW = kWaves, int TPL = kTokPerLane>
 int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
                   int batch, int64_t num_slots, int fixed_split_size, int seg, int grid_slots,
                   float sm_scale, float* part_o, float* part_lse, int part_stride, void* o,
                   hipStream_t s) {
   const bool direct = (grid_slots == 1);
-  hipLaunchKernelGGL((decode_stage1_kernel<NW, TPL, PF>), dim3(batch, grid_slots),
+  hipLaunchKernelGGL((decode_stage1_kernel<NW, TPL>), dim3(batch, grid_slots),
                      dim3(NW * 64), 0, s, (const bf16_t*)q, (const bf16_t*)k_cache,
                      (const bf16_t*)v_cache, kv_indptr, kv_indices, num_splits, fixed_split_size,
                      seg, sm_scale, num_slots, part_stride, part_o, part_lse,

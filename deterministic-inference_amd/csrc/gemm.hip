@@ -10,20 +10,16 @@
 // sid/kernels/matmul_persistent.py:1-9 buys with a separate slow kernel is
 // here true of the one fast kernel).
 //
-// Tiling (decode: M <= 64 rows per row group; weights are the HBM stream):
-//   * workgroup = 4 waves = 64 output columns (wave w owns MFMA column block w)
-//     x one row group of up to 64 rows;
-//   * the row group's x chunk (64 x 256 bf16 = 32 KiB) is staged in LDS and
-//     shared by the 4 waves, and each wave streams its weight rows straight
-//     into MFMA B operands (16-byte loads, every weight byte read once);
-//   * direct mode (sid_linear): a workgroup walks every chunk, prefetching the
-//     next chunk's weights and x into registers while the MFMAs of the current
-//     one run, and folds in registers;
-//   * partial mode (sid_linear_partials): one chunk per workgroup (4..12x more
-//     workgroups for K = 1024..3072, which the small-N decode projections need
-//     to fill 256 CUs) writing its fp32 chunk tile to partials[c][m][n]; the
-//     consumer kernel folds the chunks in order (see norm_rope.hip). No
-//     cross-workgroup synchronisation: the kernel boundary orders the two.
+// Kernels (all with that order):
+//   * linear_chunk_kernel: split-K partials for decode-sized M (sid_linear_partials): one
+//     256-wide chunk of 64 columns per 4-wave workgroup, x chunk staged in LDS, weights
+//     streamed straight into MFMA B operands; writes partials[c][m][n], which the consumer
+//     kernel folds in chunk order (norm_rope.hip). No cross-workgroup synchronisation.
+//   * linear_kernel: direct y for M < 256 in 64-row groups, every chunk of a column tile
+//     in one workgroup with the next chunk's operands prefetched during the MFMAs;
+//   * linear_tiled_kernel: direct y for M >= 256 (prefill), LDS-tiled 128 x 128 / 128 x 64;
+//   * linear_stream_kernel: lm_head-shaped N (persistent grid, x staged once per CU), with
+//     an optional fused greedy argmax.
 #include "common.h"
 
 namespace sid {
@@ -100,20 +96,17 @@ __device__ __forceinline__ void chunk_mfma(f32x4_v (&acc)[4], const bf16x8_v (&w
   }
 }
 
-// partials == nullptr: direct mode (all chunks, y written). Otherwise partial mode:
-// chunk blockIdx.y only, fp32 tile written to partials[chunk][row][col].
-// NW waves per workgroup = 16*NW columns sharing one staged x chunk.
-// PF: prefetch the next chunk's weights and x during the current chunk's MFMAs (more
-// registers, fewer resident workgroups) instead of loading at the top of each chunk.
-template <int NW, bool PF = true>
+// Direct y = x w^T (+ bias) for one 64-row group and 16*NW columns: every chunk in order,
+// the next chunk's weights and x prefetched into registers during the current chunk's
+// MFMAs. NW waves share one staged x chunk.
+template <int NW>
 __global__ void __launch_bounds__(NW * 64) linear_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ bias, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
-    int out_fp32, float* __restrict__ partials) {
+    int out_fp32) {
   __shared__ __align__(16) bf16_t sx[MROWS * XS];
 
   const int nchunks = static_cast<int>(K / KC);
-  const bool partial = partials != nullptr;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
@@ -126,8 +119,8 @@ __global__ void __launch_bounds__(NW * 64) linear_kernel(
   const bf16_t* wrow = w + (n0 + 16 * wave + r) * K + 8 * g;
   const int col = 16 * wave + r;
 
-  const int c_begin = partial ? static_cast<int>(blockIdx.y) : 0;
-  const int c_end = partial ? c_begin + 1 : nchunks;
+  const int c_begin = 0;
+  const int c_end = nchunks;
 
   bf16x8_v wf[NSTEP];
   bf16x8_v xr[8];
@@ -136,19 +129,13 @@ __global__ void __launch_bounds__(NW * 64) linear_kernel(
 
   f32x4_v total[4];
   for (int c = c_begin; c < c_end; ++c) {
-    if (c != c_begin) {
-      __syncthreads();  // previous chunk's x fully consumed
-      if constexpr (!PF) {
-        load_w(wf, wrow, static_cast<int64_t>(c) * KC);
-        load_x<NW>(xr, x, ldx, m0, M, rows16, static_cast<int64_t>(c) * KC);
-      }
-    }
+    if (c != c_begin) __syncthreads();  // previous chunk's x fully consumed
     store_x<NW>(sx, xr, rows16);
     __syncthreads();
     bf16x8_v wcur[NSTEP];
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) wcur[s] = wf[s];
-    if (PF && c + 1 < c_end) {  // prefetch the next chunk while this one computes
+    if (c + 1 < c_end) {  // prefetch the next chunk while this one computes
       load_w(wf, wrow, static_cast<int64_t>(c + 1) * KC);
       load_x<NW>(xr, x, ldx, m0, M, rows16, static_cast<int64_t>(c + 1) * KC);
     }
@@ -166,20 +153,6 @@ __global__ void __launch_bounds__(NW * 64) linear_kernel(
   }
 
   // Lane holds rows 16*mb + 4*g + i of column `col`.
-  if (partial) {
-    float* dst = partials + (static_cast<int64_t>(c_begin) * M + m0) * N + n0 + col;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      if (mb < mbs) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = 16 * mb + 4 * g + i;
-          if (row < mrows) dst[static_cast<int64_t>(row) * N] = total[mb][i];
-        }
-      }
-    }
-    return;
-  }
   const float bv = bias != nullptr ? bf16_to_f32(bias[n0 + col]) : 0.0f;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
@@ -683,30 +656,28 @@ int check_shapes(const void* x, int64_t ldx, const void* w, int64_t m, int64_t n
   return SID_OK;
 }
 
-template <int NW, bool PF = true>
+template <int NW>
 void launch_linear(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
-                   int64_t n, int64_t k, int out_fp32, float* partials, hipStream_t stream) {
-  const dim3 grid((unsigned)(n / (16 * NW)), partials ? (unsigned)(k / KC) : 1u,
-                  (unsigned)((m + MROWS - 1) / MROWS));
-  hipLaunchKernelGGL((linear_kernel<NW, PF>), grid, dim3(NW * 64), 0, stream, (const bf16_t*)x, ldx,
-                     (const bf16_t*)w, (const bf16_t*)bias, y, m, n, k, out_fp32, partials);
+                   int64_t n, int64_t k, int out_fp32, hipStream_t stream) {
+  const dim3 grid((unsigned)(n / (16 * NW)), 1u, (unsigned)((m + MROWS - 1) / MROWS));
+  hipLaunchKernelGGL((linear_kernel<NW>), grid, dim3(NW * 64), 0, stream, (const bf16_t*)x, ldx,
+                     (const bf16_t*)w, (const bf16_t*)bias, y, m, n, k, out_fp32);
 }
 
 // Waves per workgroup: more waves share one staged x chunk (less L2->LDS traffic per
 // weight byte) but leave fewer workgroups; wide direct GEMMs (lm_head, prefill) use 8.
 // (16 waves would cap the kernel at 128 VGPRs and spill.)
-int pick_waves(int64_t n, int64_t m, bool partial) {
-  if (partial) return 4;
+int pick_waves(int64_t n, int64_t m) {
   const int64_t groups = (m + MROWS - 1) / MROWS;
   if (n % 128 == 0 && (n / 128) * groups >= 512) return 8;
   return 4;
 }
 
 void launch_any(int nw, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
-                int64_t m, int64_t n, int64_t k, int out_fp32, float* partials, hipStream_t s) {
+                int64_t m, int64_t n, int64_t k, int out_fp32, hipStream_t s) {
   switch (nw) {
-    case 8: return launch_linear<8>(x, ldx, w, bias, y, m, n, k, out_fp32, partials, s);
-    default: return launch_linear<4>(x, ldx, w, bias, y, m, n, k, out_fp32, partials, s);
+    case 8: return launch_linear<8>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
+    default: return launch_linear<4>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
   }
 }
 
@@ -802,7 +773,7 @@ extern "C" int sid_linear(const void* x, int64_t ldx, const void* w, const void*
     }
     return check_launch("linear");
   }
-  launch_any(pick_waves(n, m, false), x, ldx, w, bias, y, m, n, k, out_fp32, nullptr, s);
+  launch_any(pick_waves(n, m), x, ldx, w, bias, y, m, n, k, out_fp32, s);
   return check_launch("linear");
 }
 
