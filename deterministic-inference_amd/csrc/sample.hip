@@ -102,14 +102,16 @@ __global__ void __launch_bounds__(kThreads) argmax_kernel(const float* __restric
 // rounded down), so it is an exact integer sum: the cut does not depend on any summation
 // order. (The reference sums a float cumsum in sorted order; the two differ only when the
 // mass lands within rounding of top_p.) The cut is found without sorting: p >= 0, so the
-// bits of p order like p, and a 4-level 8-bit radix select over those bits, with per-wave
-// LDS histograms of (count, fixed-point mass), descends to the key of the last kept rank;
-// the keys of the row are written once to the workspace by the softmax pass. Equal keys at
-// the cut are ranked by index with a block-wide scan.
+// bits of p order like p, and a 4-level 8-bit radix select over those bits, with LDS
+// histograms of (count, fixed-point mass), descends to the key of the last kept rank; the
+// keys of the row are written once to the workspace (only when a limit applies: with no
+// top-k / top-p limit every token is kept and the draw reads p straight from the logits).
+// Equal keys at the cut are ranked by index with a block-wide scan.
 constexpr int kSampleThreads = 1024;
 constexpr int kSampleWaves = kSampleThreads / 64;
 constexpr double kMassUnit = 281474976710656.0;  // 2^48
 constexpr float kSampleEps = 1e-10f;
+constexpr int kHistCopies = 16;
 
 __device__ __forceinline__ uint64_t mass_of(uint32_t key) {
   return static_cast<uint64_t>(static_cast<double>(__uint_as_float(key)) * kMassUnit);
@@ -117,12 +119,56 @@ __device__ __forceinline__ uint64_t mass_of(uint32_t key) {
 
 // The reference's Gumbel noise for (seed, position, column): int64 arithmetic with
 // wraparound, floor modulo 2^24 (= the low 24 bits in two's complement), u / 2^24.
-__device__ __forceinline__ float seeded_gumbel(int64_t seed, int64_t pos, int64_t col) {
+// Only the low 24 bits of the hash are used, and the low bits of a product depend only on
+// the low bits of its factors, so the per-column part is a 32-bit multiply and the
+// per-row part (gumbel_row) is computed once.
+__device__ __forceinline__ uint32_t gumbel_row(int64_t seed, int64_t pos) {
   const uint64_t step = (static_cast<uint64_t>(seed) * 19349663ull) ^
                         (static_cast<uint64_t>(pos) * 73856093ull);
-  const uint64_t h = (step * 8589934591ull) ^ (static_cast<uint64_t>(col) * 479001599ull);
-  const float u = static_cast<float>(h & 0xffffffull) / 16777216.0f;
+  return static_cast<uint32_t>(step * 8589934591ull);
+}
+
+__device__ __forceinline__ float seeded_gumbel(uint32_t row_hash, int col) {
+  const uint32_t h = row_hash ^ (static_cast<uint32_t>(col) * 479001599u);
+  const float u = static_cast<float>(h & 0xffffffu) / 16777216.0f;
   return -logf(-logf(u + kSampleEps) + kSampleEps);
+}
+
+// Calls f(value, column) for every column of a row: 16-byte loads, UNROLL of them in flight
+// per thread, when the row is 16-byte aligned (else one element per load). Which thread sees
+// which column is fixed by the row's alignment and length alone.
+template <int UNROLL, typename F>
+__device__ __forceinline__ void for_each_col(const float* __restrict__ row, int cols, F&& f) {
+  const int tid = threadIdx.x;
+  int vec = 0;
+  if ((reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+    const float4* row4 = reinterpret_cast<const float4*>(row);
+    const int n4 = cols >> 2;
+    constexpr int kStep = kSampleThreads * UNROLL;
+    int base = 0;
+    for (; base + kStep <= n4; base += kStep) {
+      float4 v[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) v[u] = row4[base + u * kSampleThreads + tid];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int c = 4 * (base + u * kSampleThreads + tid);
+        f(v[u].x, c);
+        f(v[u].y, c + 1);
+        f(v[u].z, c + 2);
+        f(v[u].w, c + 3);
+      }
+    }
+    for (int i = base + tid; i < n4; i += kSampleThreads) {
+      const float4 v = row4[i];
+      f(v.x, 4 * i);
+      f(v.y, 4 * i + 1);
+      f(v.z, 4 * i + 2);
+      f(v.w, 4 * i + 3);
+    }
+    vec = 4 * n4;
+  }
+  for (int c = vec + tid; c < cols; c += kSampleThreads) f(row[c], c);
 }
 
 __device__ __forceinline__ float block_max(float v, float* red) {
@@ -179,8 +225,11 @@ __global__ void __launch_bounds__(kSampleThreads) sample_kernel(
     const int64_t* __restrict__ top_ks, const float* __restrict__ top_ps,
     const int64_t* __restrict__ seeds, const int64_t* __restrict__ positions, int64_t cols,
     uint32_t* __restrict__ keys_ws, int64_t* __restrict__ out) {
-  __shared__ uint32_t h_cnt[kSampleWaves][256];
-  __shared__ uint64_t h_mass[kSampleWaves][256];
+  // Radix histograms, one copy per lane & 15 (so at most 4 lanes of a wave instruction can
+  // hit one address); rows padded to 257 entries so equal bins of different copies fall in
+  // different LDS banks.
+  __shared__ uint32_t h_cnt[kHistCopies][257];
+  __shared__ uint64_t h_mass[kHistCopies][257];
   __shared__ float s_red[kSampleWaves];
   __shared__ float s_bv[kSampleWaves];
   __shared__ int64_t s_bi[kSampleWaves];
@@ -190,35 +239,34 @@ __global__ void __launch_bounds__(kSampleThreads) sample_kernel(
 
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int copy = tid & (kHistCopies - 1);
+  const int ncols = static_cast<int>(cols);
   const float* row = logits + r * ld;
   const float t = temps[r];
 
   float bv = -INFINITY;
   int64_t bi = cols;
   if (!(t > 0.0f)) {  // greedy row
-    for (int64_t c = tid; c < cols; c += kSampleThreads) {
-      const float v = row[c];
+    for_each_col<8>(row, ncols, [&](float v, int c) {
       if (better(v, c, bv, bi)) {
         bv = v;
         bi = c;
       }
-    }
+    });
     block_best(bv, bi, s_bv, s_bi);
     if (tid == 0) out[r] = bi < cols ? bi : 0;
     return;
   }
 
-  // softmax of logits / t; keys = bits of p
+  // softmax of logits / t. Division by t > 0 is monotone (correct rounding preserves
+  // order), so max(x / t) = max(x) / t and the first pass needs no division.
   float mx = -INFINITY;
-  for (int64_t c = tid; c < cols; c += kSampleThreads) mx = fmaxf(mx, row[c] / t);
-  mx = block_max(mx, s_red);
+  for_each_col<8>(row, ncols, [&](float v, int) { mx = fmaxf(mx, v); });
+  mx = block_max(mx, s_red) / t;
   float part = 0.0f;
-  for (int64_t c = tid; c < cols; c += kSampleThreads) part += expf(row[c] / t - mx);
+  for_each_col<4>(row, ncols, [&](float v, int) { part += expf(v / t - mx); });
   const float sum = block_sum(part, s_red);
   uint32_t* keys = keys_ws + r * cols;
-  for (int64_t c = tid; c < cols; c += kSampleThreads)
-    keys[c] = __float_as_uint(expf(row[c] / t - mx) / sum);
 
   const int64_t k = top_ks[r];
   const uint64_t k_lim = (k > 0 && k < cols) ? static_cast<uint64_t>(k) : static_cast<uint64_t>(cols);
@@ -230,30 +278,34 @@ __global__ void __launch_bounds__(kSampleThreads) sample_kernel(
   int64_t idx_cut = cols;   // among keys == v_cut, indices <= idx_cut are kept
   const bool truncate = p_lim || k_lim < static_cast<uint64_t>(cols);
   if (truncate) {
+    // keys = bits of p (p >= 0, so they order like p), written once, read by every level
+    for_each_col<4>(row, ncols, [&](float v, int c) {
+      keys[c] = __float_as_uint(expf(v / t - mx) / sum);
+    });
     __syncthreads();  // keys visible to the block
     uint32_t prefix = 0, pmask = 0;
     uint64_t cnt_above = 0, mass_above = 0, final_cnt = 0;
     for (int level = 0; level < 4; ++level) {
       const int shift = 24 - 8 * level;
-      for (int i = tid; i < kSampleWaves * 256; i += kSampleThreads) {
+      for (int i = tid; i < kHistCopies * 257; i += kSampleThreads) {
         (&h_cnt[0][0])[i] = 0;
         (&h_mass[0][0])[i] = 0;
       }
       __syncthreads();
-      for (int64_t c = tid; c < cols; c += kSampleThreads) {
-        const uint32_t key = keys[c];
+      for_each_col<8>(reinterpret_cast<const float*>(keys), ncols, [&](float kv, int) {
+        const uint32_t key = __float_as_uint(kv);
         if ((key & pmask) == prefix) {
           const int b = (key >> shift) & 255;
-          atomicAdd(&h_cnt[wave][b], 1u);
-          atomicAdd(reinterpret_cast<unsigned long long*>(&h_mass[wave][b]),
+          atomicAdd(&h_cnt[copy][b], 1u);
+          atomicAdd(reinterpret_cast<unsigned long long*>(&h_mass[copy][b]),
                     static_cast<unsigned long long>(mass_of(key)));
         }
-      }
+      });
       __syncthreads();
       if (tid < 256) {  // integer totals: exact in any order
         uint32_t cn = 0;
         uint64_t ms = 0;
-        for (int w = 0; w < kSampleWaves; ++w) {
+        for (int w = 0; w < kHistCopies; ++w) {
           cn += h_cnt[w][tid];
           ms += h_mass[w][tid];
         }
@@ -336,17 +388,23 @@ __global__ void __launch_bounds__(kSampleThreads) sample_kernel(
     }
   }
 
-  const int64_t seed = seeds[r];
-  const int64_t pos = positions[r];
-  for (int64_t c = tid; c < cols; c += kSampleThreads) {
-    const uint32_t key = keys[c];
-    const bool keep = !truncate || key > v_cut || (key == v_cut && c <= idx_cut);
-    if (!keep) continue;
-    const float s = logf(__uint_as_float(key) + kSampleEps) + seeded_gumbel(seed, pos, c);
+  const uint32_t row_hash = gumbel_row(seeds[r], positions[r]);
+  auto draw = [&](uint32_t key, int c) {
+    const float s = logf(__uint_as_float(key) + kSampleEps) + seeded_gumbel(row_hash, c);
     if (better(s, c, bv, bi)) {
       bv = s;
       bi = c;
     }
+  };
+  if (truncate) {
+    for_each_col<4>(reinterpret_cast<const float*>(keys), ncols, [&](float kv, int c) {
+      const uint32_t key = __float_as_uint(kv);
+      if (key > v_cut || (key == v_cut && c <= idx_cut)) draw(key, c);
+    });
+  } else {  // every token kept: p straight from the logits (same bits as the keys)
+    for_each_col<4>(row, ncols, [&](float v, int c) {
+      draw(__float_as_uint(expf(v / t - mx) / sum), c);
+    });
   }
   block_best(bv, bi, s_bv, s_bi);
   if (tid == 0) out[r] = bi < cols ? bi : 0;
