@@ -99,9 +99,7 @@ class DecodeWorkload:
         fb = self.build()
         toks = self.runner.step(fb).tolist()
         # roll the state back: release this step's slots (LIFO: the next step reuses them)
-        rows = [r.req_row for r in self.reqs]
-        pos = [r.kv_len for r in self.reqs]
-        self.kv.free(self.kv.req_to_token[rows, pos])
+        self.kv.free(self.torch.from_numpy(fb.new_slots_host))
         return toks
 
 
@@ -122,6 +120,7 @@ def attention_roofline(wl, reps):
     on torch's current stream (the launch stream), over reps x 28 layer pools."""
     torch = wl.torch
     fb = wl.build()
+    fb.build_indices()
     mcfg = wl.runner.mcfg
     attn = wl.runner.decode_attn
     q = torch.randn(len(wl.reqs), mcfg.num_q_heads, mcfg.head_dim, device="cuda").to(torch.bfloat16)
@@ -151,7 +150,7 @@ def attention_roofline(wl, reps):
     bytes_launch = (rows * mcfg.num_kv_heads * mcfg.head_dim * 2 * 2   # K + V rows
                     + rows * 4                                           # kv_indices
                     + 2 * b * mcfg.num_q_heads * mcfg.head_dim * 2)      # q in, o out
-    wl.kv.free(wl.kv.req_to_token[[r.req_row for r in wl.reqs], [r.kv_len for r in wl.reqs]])
+    wl.kv.free(torch.from_numpy(fb.new_slots_host))
     achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
@@ -182,6 +181,7 @@ def cpu_baseline(wl):
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
     fb = wl.build()
+    fb.build_indices()
     w = wl.runner.model.w
     wc = {"embed": w["embed"].cpu(), "norm": w["norm"].cpu(), "lm_head": w["embed"].cpu(),
           "layers": [{k: v.cpu() for k, v in w["layers"][i].items()} for i in range(2)]}
@@ -194,7 +194,7 @@ def cpu_baseline(wl):
              "out_slots": (indptr[1:] - 1).long(), "kv_indptr": indptr,
              "kv_indices": torch.arange(rows, dtype=torch.int32),
              "sample_indices": torch.arange(len(wl.reqs))}
-    wl.kv.free(wl.kv.req_to_token[[r.req_row for r in wl.reqs], [r.kv_len for r in wl.reqs]])
+    wl.kv.free(torch.from_numpy(fb.new_slots_host))
     mcfg = wl.runner.mcfg
 
     def timed(layers):

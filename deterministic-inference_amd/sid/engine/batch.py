@@ -5,8 +5,9 @@ prefill of P tokens generates position P; a decode step feeding output_ids[N-1] 
 position P+N-1) generates P+N; verify row j of a window starting at verified_len v
 generates P+v+j. (A mismatch here would make every verify window fail at index 0.)
 
-Host work per decode step is O(B) Python plus three host->device copies; the kv_indices
-of the whole batch are built on the device from the request->token table by one kernel.
+Host work per decode step is O(B) Python plus one host->device copy (graph-static
+buffers; three without them); the kv_indices of the whole batch are built on the device
+from the request->token table by one kernel.
 """
 
 from __future__ import annotations
@@ -52,34 +53,54 @@ class ForwardBatch:
     all_greedy: Optional[bool] = None  # host-known: every row has temperature 0
     graph_key: Optional[tuple] = None  # set when the inputs live in graph-static buffers
     real_rows: Optional[int] = None    # rows of real requests when padded (decode graphs)
+    # decode batches in the graph-static buffers: build_decode_indices arguments, run at the
+    # start of the forward (inside the graph) instead of by the builder
+    index_build: Optional[tuple] = None
+    new_slots_host: Optional[np.ndarray] = None  # decode: the KV slots taken by this step
+
+    def build_indices(self) -> None:
+        """Enqueue the deferred kv_indices build (a no-op when the builder already ran it).
+        The forward calls this first; a caller that reads kv_indices without a forward
+        calls it itself."""
+        if self.index_build is not None:
+            load_ext().build_decode_indices(*self.index_build)
 
 
 class DecodeStatic:
     """Fixed-address device buffers for decode batches of up to max_bs requests, shared by
-    every captured decode graph (replays are ordered on one stream). Host staging is pinned
-    so the three per-step host->device copies are asynchronous; a staging buffer is reused
-    only after the event of its previous copy has completed."""
+    every captured decode graph (replays are ordered on one stream). All per-step inputs
+    live in one pinned host block and one device block, so a step is one asynchronous
+    host->device copy; the host block is reused only after the event of its previous copy
+    has completed."""
 
     def __init__(self, max_bs: int, kv_capacity: int, device):
         self.max_bs = max_bs
-        self.i64 = torch.zeros(7, max_bs, dtype=torch.int64, device=device)
-        self.i32 = torch.zeros(2 * max_bs + 1, dtype=torch.int32, device=device)
-        self.f32 = torch.zeros(2, max_bs, dtype=torch.float32, device=device)
+        n64, n32, nf = 7 * max_bs, 2 * max_bs + 1, 2 * max_bs
+        o32 = 8 * n64
+        of = o32 + 4 * (n32 + (n32 & 1))  # keep the fp32 block 8-byte aligned
+        nbytes = of + 4 * nf
+        self.host = torch.zeros(nbytes, dtype=torch.uint8, pin_memory=True)
+        self.dev = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+        def views(buf):
+            return (buf[:o32].view(torch.int64).view(7, max_bs),
+                    buf[o32:o32 + 4 * n32].view(torch.int32),
+                    buf[of:].view(torch.float32).view(2, max_bs))
+
+        self.i64, self.i32, self.f32 = views(self.dev)
+        self.h64, self.h32, self.hf32 = (v.numpy() for v in views(self.host))
         self.kv_indices = torch.zeros(kv_capacity, dtype=torch.int32, device=device)
-        self.h64 = torch.zeros(7, max_bs, dtype=torch.int64, pin_memory=True)
-        self.h32 = torch.zeros(2 * max_bs + 1, dtype=torch.int32, pin_memory=True)
-        self.hf32 = torch.zeros(2, max_bs, dtype=torch.float32, pin_memory=True)
         self.copied = torch.cuda.Event()
         self.copied.record()
 
 
 def _sampling_host(reqs, repeat: int = 1):
-    temps = np.repeat(np.array([r.params.temperature for r in reqs], dtype=np.float32), repeat)
-    top_ps = np.repeat(np.array([r.params.top_p for r in reqs], dtype=np.float32), repeat)
-    top_ks = np.repeat(np.array([r.params.top_k if r.params.top_k > 0 else -1 for r in reqs],
-                                dtype=np.int64), repeat)
-    seeds = np.repeat(np.array([r.params.seed for r in reqs], dtype=np.int64), repeat)
-    return temps, top_ks, top_ps, seeds
+    f = np.array([r.samp_f for r in reqs], dtype=np.float32).reshape(-1, 2)
+    i = np.array([r.samp_i for r in reqs], dtype=np.int64).reshape(-1, 2)
+    if repeat != 1:
+        f = np.repeat(f, repeat, axis=0)
+        i = np.repeat(i, repeat, axis=0)
+    return f[:, 0], i[:, 0], f[:, 1], i[:, 1]
 
 
 def _to_device(arrays: list, dtype, device) -> list:
@@ -145,9 +166,12 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
     table row -1, KV slot -1, greedy), whose attention output is zero and whose tokens the
     caller ignores; real rows' results do not depend on them."""
     bs = len(reqs)
-    pos = np.fromiter((r.prompt_len + r.num_output - 1 for r in reqs), dtype=np.int64, count=bs)
-    for r, p in zip(reqs, pos.tolist()):
-        assert p == r.kv_len, f"req {r.rid}: decode position {p} != kv_len {r.kv_len}"
+    if not all(r.output_ids for r in reqs):
+        bad = next(r for r in reqs if not r.output_ids)
+        raise AssertionError(f"req {bad.rid}: decode step before any output token")
+    # position of the fed token = kv_len = prompt_len + num_output - 1 (request.py)
+    pos = np.fromiter((len(r.prompt_ids) + len(r.output_ids) - 1 for r in reqs),
+                      dtype=np.int64, count=bs)
     ids = np.fromiter((r.output_ids[-1] for r in reqs), dtype=np.int64, count=bs)
     rows = np.fromiter((r.req_row for r in reqs), dtype=np.int64, count=bs)
     new_slots = kv.alloc(bs).numpy()
@@ -158,41 +182,43 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
     np.cumsum(seq_lens, out=indptr[1:])
     temps, top_ks, top_ps, seeds = _sampling_host(reqs)
     total = int(indptr[-1])
+    index_build = None
     if static is None:
         d_ids, d_pos, d_rows, d_slots, d_spos, d_topk, d_seed = _to_device(
             [ids, pos, rows, new_slots, pos + 1, top_ks, seeds], np.int64, device)
         d_indptr, d_lens = _to_device([indptr, seq_lens], np.int32, device)
         d_temps, d_topp = _to_device([temps, top_ps], np.float32, device)
         kv_indices = torch.empty(total, dtype=torch.int32, device=device)
+        load_ext().build_decode_indices(kv.req_to_token_gpu, d_rows, d_slots, d_indptr, kv_indices)
     else:
         n = bs if pad_to is None else pad_to
         assert bs <= n <= static.max_bs and total <= static.kv_indices.numel()
         mb = static.max_bs
         static.copied.synchronize()
-        h64 = static.h64.numpy()
+        h64 = static.h64
         pad64 = (DUMMY_TOKEN_ID, 0, -1, -1, 1, -1, 0)  # ids, pos, rows, slots, spos, top_k, seed
-        for i, a in enumerate((ids, pos, rows, new_slots, pos + 1, top_ks, seeds)):
+        for i, a in enumerate((ids, pos, rows, new_slots, seq_lens, top_ks, seeds)):
             h64[i, :bs] = a
             h64[i, bs:n] = pad64[i]
-        h32 = static.h32.numpy()
+        h32 = static.h32
         h32[:bs + 1] = indptr
         h32[bs + 1:n + 1] = indptr[-1]
         h32[mb + 1:mb + 1 + bs] = seq_lens
         h32[mb + 1 + bs:mb + 1 + n] = 0
-        hf = static.hf32.numpy()
+        hf = static.hf32
         hf[0, :bs] = temps
         hf[1, :bs] = top_ps
         hf[0, bs:n] = 0.0
         hf[1, bs:n] = 1.0
-        static.i64.copy_(static.h64, non_blocking=True)
-        static.i32.copy_(static.h32, non_blocking=True)
-        static.f32.copy_(static.hf32, non_blocking=True)
+        static.dev.copy_(static.host, non_blocking=True)
         static.copied.record()
         d_ids, d_pos, d_rows, d_slots, d_spos, d_topk, d_seed = (static.i64[i, :n] for i in range(7))
         d_indptr, d_lens = static.i32[:n + 1], static.i32[mb + 1:mb + 1 + n]
         d_temps, d_topp = static.f32[0, :n], static.f32[1, :n]
         kv_indices = static.kv_indices[:total]
-    load_ext().build_decode_indices(kv.req_to_token_gpu, d_rows, d_slots, d_indptr, kv_indices)
+        # Every argument lives at a fixed address, so the index build is part of the
+        # forward (and of its captured graph): ModelRunner runs it first.
+        index_build = (kv.req_to_token_gpu, d_rows, d_slots, d_indptr, kv_indices)
     return ForwardBatch(
         mode=ForwardMode.DECODE, input_ids=d_ids, positions=d_pos, out_slots=d_slots,
         kv_indptr=d_indptr, kv_indices=kv_indices, seq_lens=d_lens,
@@ -202,4 +228,5 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         temperatures=d_temps, top_ks=d_topk, top_ps=d_topp, seeds=d_seed,
         invariant=invariant, all_greedy=bool((temps == 0).all()),
         real_rows=bs if d_ids.shape[0] != bs else None,
+        index_build=index_build, new_slots_host=new_slots,
     )

@@ -87,6 +87,7 @@ class ModelRunner:
         return out if fb.real_rows is None else out[:fb.real_rows]
 
     def _forward_eager(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
+        fb.build_indices()
         return self.model.forward(fb, self.kv_cache, self.decode_attn,
                                   decode_backend=self.cfg.decode_backend, greedy=greedy)
 

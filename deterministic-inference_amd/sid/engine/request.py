@@ -31,6 +31,9 @@ class Request:
         if params.stop_token_ids:
             self.eos_token_ids.update(params.stop_token_ids)
         self.output_ids: list = []
+        # host rows of the per-step sampling arrays (params do not change after admission)
+        self.samp_f = (float(params.temperature), float(params.top_p))
+        self.samp_i = (int(params.top_k) if params.top_k > 0 else -1, int(params.seed))
         self.state = RequestState.WAITING
         self.finished_reason: Optional[str] = None
         self.req_row = -1
