@@ -237,20 +237,21 @@ __device__ __forceinline__ void run_tiles(RowState& st, const Ctx& c, int t_begi
 
 // part_* layout: [split][total_q][HQ]; part_a holds the unnormalised accumulator
 // (128 dims), part_ml = (m, l). Lane holds dims 16*db + 4*g .. +3 of its row.
+template <bool FANOUT>
 __global__ void __launch_bounds__(256) extend_attention_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ qo_indptr,
     const int32_t* __restrict__ kv_indptr, const int32_t* __restrict__ kv_indices,
     int num_q_heads, int num_kv_heads, int64_t num_slots, float sm_scale, int mtiles,
     int64_t total_q, bf16_t* __restrict__ o, float* __restrict__ part_a,
-    float* __restrict__ part_ml) {
+    float* __restrict__ part_ml, int32_t* __restrict__ part_n) {
   __shared__ __align__(16) bf16_t sK[BN * KS_STRIDE];
   __shared__ __align__(16) bf16_t sVt[D * VT_STRIDE];
   __shared__ int32_t s_idx[KSPLIT];
 
   const int b = blockIdx.x;
   const int h_kv = blockIdx.y;
-  const bool fanout = part_a != nullptr;
+  constexpr bool fanout = FANOUT;
   const int mtile = fanout ? static_cast<int>(blockIdx.z) % mtiles : static_cast<int>(blockIdx.z);
   const int split = fanout ? static_cast<int>(blockIdx.z) / mtiles : 0;
 
@@ -298,11 +299,11 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   }
 
   const int64_t prow = static_cast<int64_t>(q_start + (c.row_ok ? qr : 0)) * num_q_heads + hq;
-  if (fanout) {
+  if constexpr (FANOUT) {
     RowState st;
     fresh(st);
-    run_tiles(st, c, split * KSPLIT, min(visible_end, (split + 1) * KSPLIT), qf, sm_scale, sK, sVt,
-              s_idx);
+    run_tiles(st, c, split * KSPLIT, min(visible_end, (split + 1) * KSPLIT), qf, sm_scale, sK,
+              sVt, s_idx);
     if (!c.row_ok) return;
     const int64_t pr = static_cast<int64_t>(split) * total_q * num_q_heads + prow;
     float* pa = part_a + pr * D;
@@ -312,10 +313,10 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
     if (c.g == 0) {
       part_ml[2 * pr] = st.m;
       part_ml[2 * pr + 1] = st.l;
+      if (split == 0) part_n[prow] = nsplits;
     }
     return;
-  }
-
+  } else {
   RowState run;
   fresh(run);
   for (int sp = 0; sp < nsplits; ++sp) {
@@ -334,67 +335,59 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
     u.y = pack_bf16x2(run.acc[db][2] / run.l, run.acc[db][3] / run.l);
     *reinterpret_cast<uint2*>(op + 16 * db + 4 * c.g) = u;
   }
+  }
 }
 
-// Fold the fanned-out split states of every (query row, head) in split order. Grid:
-// x = request, y = groups of 4 (row, head) items of that request; one 64-lane wave per
-// item. The wave first copies up to MERGE_CHUNK splits' states into LDS with one round of
-// independent loads, then folds them from LDS. Every lane reproduces the per-lane layout
-// of the attention kernel (dims 16*db + 4*g + i), so fold() runs on exactly the same
-// operands in the same order as the sequential path.
+// Fold the fanned-out split states of every (query row, head) item in split order. One
+// 64-lane wave per item (global item = row * HQ + head), 4 per workgroup. The item's split
+// count (written by the attention kernel's split-0 workgroup) and the states of up to
+// MERGE_CHUNK splits are loaded together, in one round of independent loads (states past
+// the item's count are loaded but not used), copied to LDS and folded from there. Every
+// lane reproduces the per-lane layout of the attention kernel (dims 16*db + 4*g + i), so
+// fold() runs on exactly the same operands in the same order as the sequential path.
 constexpr int MERGE_CHUNK = 16;
 
 __global__ void __launch_bounds__(256) extend_merge_kernel(
-    const int32_t* __restrict__ qo_indptr, const int32_t* __restrict__ kv_indptr,
-    int num_q_heads, int64_t total_q, const float* __restrict__ part_a,
-    const float* __restrict__ part_ml, bf16_t* __restrict__ o) {
+    int64_t items, int splits, const float* __restrict__ part_a,
+    const float* __restrict__ part_ml, const int32_t* __restrict__ part_n,
+    bf16_t* __restrict__ o) {
   __shared__ __align__(16) float s_a[4][MERGE_CHUNK][D];
   __shared__ float s_ml[4][MERGE_CHUNK][2];
-  const int b = blockIdx.x;
   const int wave = threadIdx.x >> 6;
-  const int local = blockIdx.y * 4 + wave;  // (row, head) within the request
   const int lane = threadIdx.x & 63;
-  const int q_start = qo_indptr[b];
-  const int extend_len = qo_indptr[b + 1] - q_start;
-  const int kv_len = kv_indptr[b + 1] - kv_indptr[b];
-  const bool valid = local < extend_len * num_q_heads;
-  const int64_t item = static_cast<int64_t>(q_start) * num_q_heads + local;
-  const int prefix = kv_len - extend_len;
-  const int qr = local / num_q_heads;
-  const int mtile = qr / BQ;
-  const int last_row = min(extend_len, (mtile + 1) * BQ) - 1;
-  const int visible_end = min(kv_len, prefix + last_row + 1);
-  const int nsplits = valid ? ceil_div(visible_end, KSPLIT) : 0;
-  const int64_t sp_stride = total_q * num_q_heads;
   const int g = lane >> 4;  // lane layout of the attention kernel
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const bool valid = item < items;
+  const int64_t it = valid ? item : items - 1;  // tail waves load a real item, write nothing
+  const int nsplits = part_n[it];
 
   RowState run;
   fresh(run);
-  // Uniform over the block: every wave takes part in every barrier.
-  int max_splits = nsplits;
-  {
-    __shared__ int s_n[4];
-    if (lane == 0) s_n[wave] = nsplits;
-    __syncthreads();
-    max_splits = max(max(s_n[0], s_n[1]), max(s_n[2], s_n[3]));
-  }
-  for (int c0 = 0; c0 < max_splits; c0 += MERGE_CHUNK) {
-    const int n = min(MERGE_CHUNK, nsplits - c0);  // this wave's splits in the chunk
+  for (int c0 = 0; c0 < splits; c0 += MERGE_CHUNK) {  // splits is uniform: a kernel argument
+    const int n = min(MERGE_CHUNK, splits - c0);
+    float ml = 0.0f;
+    if (lane < 2 * n) ml = part_ml[2 * (static_cast<int64_t>(c0 + (lane >> 1)) * items + it) + (lane & 1)];
+    // every load of the chunk issued before the first LDS store (one round trip)
+    constexpr int kPerLane = MERGE_CHUNK * (D / 4) / 64;
+    f32x4_v buf[kPerLane];
+#pragma unroll
+    for (int u = 0; u < kPerLane; ++u) {
+      const int e = lane + 64 * u;  // split e / 32, 16-byte piece e % 32
+      if (e < n * (D / 4)) {
+        const int64_t pr = static_cast<int64_t>(c0 + (e >> 5)) * items + it;
+        buf[u] = *reinterpret_cast<const f32x4_v*>(part_a + pr * D + 4 * (e & 31));
+      }
+    }
     __syncthreads();  // previous chunk folded
-    for (int e = lane; e < n * (D / 4); e += 64) {
-      const int sp = e / (D / 4);
-      const int j = e % (D / 4);
-      const int64_t pr = static_cast<int64_t>(c0 + sp) * sp_stride + item;
-      *reinterpret_cast<f32x4_v*>(&s_a[wave][sp][4 * j]) =
-          *reinterpret_cast<const f32x4_v*>(part_a + pr * D + 4 * j);
+#pragma unroll
+    for (int u = 0; u < kPerLane; ++u) {
+      const int e = lane + 64 * u;
+      if (e < n * (D / 4)) *reinterpret_cast<f32x4_v*>(&s_a[wave][e >> 5][4 * (e & 31)]) = buf[u];
     }
-    if (lane < 2 * max(n, 0)) {
-      const int sp = lane >> 1;
-      const int64_t pr = static_cast<int64_t>(c0 + sp) * sp_stride + item;
-      s_ml[wave][sp][lane & 1] = part_ml[2 * pr + (lane & 1)];
-    }
+    if (lane < 2 * n) s_ml[wave][lane >> 1][lane & 1] = ml;
     __syncthreads();
-    for (int sp = 0; sp < n; ++sp) {
+    const int use = min(n, nsplits - c0);
+    for (int sp = 0; sp < use; ++sp) {
       f32x4_v a[8];
 #pragma unroll
       for (int db = 0; db < 8; ++db)
@@ -428,7 +421,8 @@ extern "C" int64_t sid_extend_attention_workspace_bytes(int batch, int64_t total
   const int64_t mtiles = ceil_div(max_extend_len, BQ);
   if (static_cast<int64_t>(batch) * num_kv_heads * mtiles >= kFanoutBelowWg) return 0;
   const int64_t splits = ceil_div(max_kv_len, KSPLIT);
-  return splits * total_q * num_q_heads * (D + 2) * static_cast<int64_t>(sizeof(float));
+  // per (split, row, head): 128 accumulator floats + (m, l); per (row, head): split count
+  return (splits * (D + 2) + 1) * total_q * num_q_heads * static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int sid_extend_attention_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -457,24 +451,27 @@ extern "C" int sid_extend_attention_fwd(const void* q, const void* k_cache, cons
   if (fanout) {
     const int splits = ceil_div(max_kv_len, KSPLIT);
     SID_REQUIRE(static_cast<int64_t>(mtiles) * splits <= 65535, "extend_attention: grid too large");
+    const int64_t items = total_q * num_q_heads;
     float* pa = static_cast<float*>(workspace);
-    float* pml = pa + static_cast<int64_t>(splits) * total_q * num_q_heads * D;
-    hipLaunchKernelGGL(extend_attention_kernel, dim3(batch, num_kv_heads, mtiles * splits),
+    float* pml = pa + static_cast<int64_t>(splits) * items * D;
+    int32_t* pn = reinterpret_cast<int32_t*>(pml + static_cast<int64_t>(splits) * items * 2);
+    hipLaunchKernelGGL(extend_attention_kernel<true>, dim3(batch, num_kv_heads, mtiles * splits),
                        dim3(256), 0, s, (const bf16_t*)q, (const bf16_t*)k_cache,
                        (const bf16_t*)v_cache, qo_indptr, kv_indptr, kv_indices, num_q_heads,
-                       num_kv_heads, num_slots, sm_scale, mtiles, total_q, (bf16_t*)o, pa, pml);
+                       num_kv_heads, num_slots, sm_scale, mtiles, total_q, (bf16_t*)o, pa, pml,
+                       pn);
     int rc = check_launch("extend_attention");
     if (rc != SID_OK) return rc;
-    const int64_t groups = (static_cast<int64_t>(max_extend_len) * num_q_heads + 3) / 4;
-    SID_REQUIRE(groups <= 65535, "extend_attention: too many rows per request for the merge");
-    hipLaunchKernelGGL(extend_merge_kernel, dim3(batch, (unsigned)groups), dim3(256), 0, s,
-                       qo_indptr, kv_indptr, num_q_heads, total_q, pa, pml, (bf16_t*)o);
+    const int64_t groups = (items + 3) / 4;
+    SID_REQUIRE(groups < (1ll << 31), "extend_attention: too many rows for the merge");
+    hipLaunchKernelGGL(extend_merge_kernel, dim3((unsigned)groups), dim3(256), 0, s, items,
+                       splits, pa, pml, pn, (bf16_t*)o);
     return check_launch("extend_attention merge");
   }
   SID_REQUIRE(mtiles <= 65535, "extend_attention: grid too large");
-  hipLaunchKernelGGL(extend_attention_kernel, dim3(batch, num_kv_heads, mtiles), dim3(256), 0, s,
+  hipLaunchKernelGGL(extend_attention_kernel<false>, dim3(batch, num_kv_heads, mtiles), dim3(256), 0, s,
                      (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, qo_indptr,
                      kv_indptr, kv_indices, num_q_heads, num_kv_heads, num_slots, sm_scale, mtiles,
-                     total_q, (bf16_t*)o, nullptr, nullptr);
+                     total_q, (bf16_t*)o, nullptr, nullptr, nullptr);
   return check_launch("extend_attention");
 }
