@@ -42,11 +42,39 @@ constexpr int BN = 64;          // keys per tile
 constexpr int BQ = 32;          // query positions per workgroup (x 2 heads = 64 rows)
 constexpr int KSPLIT = 256;     // keys per split (4 tiles), anchored at position 0
 constexpr int KS_STRIDE = D + 8;    // bf16 elements per K row in LDS (272 bytes)
-constexpr int VT_STRIDE = BN + 8;   // bf16 elements per transposed V row in LDS (144 bytes)
+constexpr int VS_STRIDE = D + 16;   // bf16 elements per V row in LDS (288 bytes)
 constexpr float NEG_BIG = -1e30f;
 
-__device__ __forceinline__ float xor16(float v) { return lane_xor(v, 16); }
-__device__ __forceinline__ float xor32(float v) { return lane_xor(v, 32); }
+// Reductions over lanes l and l ^ 16 (l ^ 32): v_permlane16/32_swap hand each lane the
+// values of both lanes of its pair as (lower lane's, upper lane's), so both lanes compute
+// the same expression on the same operands (identical bits) without an LDS round trip.
+__device__ __forceinline__ float pair16_max(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float pair32_max(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float pair16_sum(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float pair32_sum(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+typedef short s16x4_v __attribute__((ext_vector_type(4)));
+typedef short s16x8_v __attribute__((ext_vector_type(8)));
+
+// 4 bf16 of a V^T fragment through the LDS transpose read: within each 16-lane group,
+// lane L receives element L % 4 of the 8-byte values addressed by lanes L / 4 + 4j
+// (j = 0..3) of its group.
+__device__ __forceinline__ s16x4_v ld_tr16(const bf16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_v*)(p));
+}
 
 // Per-lane softmax state of one query row (the lane's 32 output dims).
 struct RowState {
@@ -115,31 +143,22 @@ __device__ __forceinline__ void load_tile(TileRegs& r, const Ctx& c, const int32
     const int64_t slot = s_idx[k0 + (v >> 4)];
     r.k[i] = reinterpret_cast<const u32x4_v*>(c.k_cache + slot * c.row_stride + c.h_kv * D)[v & 15];
   }
-  // V: lane -> key, wave w -> 16-byte chunks 4w .. 4w+3.
-  const int64_t slot = s_idx[k0 + c.lane];
-  const u32x4_v* vp =
-      reinterpret_cast<const u32x4_v*>(c.v_cache + slot * c.row_stride + c.h_kv * D);
+  // V: the same key / chunk assignment (rows stored as they are; transposed on read).
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r.v[i] = vp[4 * c.wave + i];
+  for (int i = 0; i < 4; ++i) {
+    const int v = c.tid + 256 * i;
+    const int64_t slot = s_idx[k0 + (v >> 4)];
+    r.v[i] = reinterpret_cast<const u32x4_v*>(c.v_cache + slot * c.row_stride + c.h_kv * D)[v & 15];
+  }
 }
 
 __device__ __forceinline__ void store_tile(const TileRegs& r, const Ctx& c, bf16_t* sK,
-                                           bf16_t* sVt) {
+                                           bf16_t* sV) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int v = c.tid + 256 * i;
     *reinterpret_cast<u32x4_v*>(&sK[(v >> 4) * KS_STRIDE + (v & 15) * 8]) = r.k[i];
-  }
-  const int key = c.lane;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ch = 4 * c.wave + i;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t w = r.v[i][e];
-      sVt[(ch * 8 + 2 * e) * VT_STRIDE + key] = static_cast<bf16_t>(w & 0xffffu);
-      sVt[(ch * 8 + 2 * e + 1) * VT_STRIDE + key] = static_cast<bf16_t>(w >> 16);
-    }
+    *reinterpret_cast<u32x4_v*>(&sV[(v >> 4) * VS_STRIDE + (v & 15) * 8]) = r.v[i];
   }
 }
 
@@ -147,7 +166,7 @@ __device__ __forceinline__ void store_tile(const TileRegs& r, const Ctx& c, bf16
 // softmax).
 __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
                                           const bf16x8_v (&qf)[4], float sm_scale,
-                                          const bf16_t* sK, const bf16_t* sVt) {
+                                          const bf16_t* sK, const bf16_t* sV) {
   // S^T blocks: lane holds logits of its query for keys 8g..8g+7 (s[0..7]) and
   // 32+8g..32+8g+7 (s[8..15]). MFMA row m of key block j holds key
   // 32*(j/2) + 8*(m/4) + 4*(j%2) + m%4.
@@ -175,8 +194,8 @@ __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
     s[i] = vis[i] ? s[i] * sm_scale : NEG_BIG;
     tmax = fmaxf(tmax, s[i]);
   }
-  tmax = fmaxf(tmax, xor16(tmax));
-  tmax = fmaxf(tmax, xor32(tmax));
+  tmax = pair16_max(tmax);
+  tmax = pair32_max(tmax);
   const float m_new = fmaxf(st.m, tmax);
   const float rescale = __expf(st.m - m_new);
   float psum = 0.0f;
@@ -185,8 +204,8 @@ __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
     s[i] = vis[i] ? __expf(s[i] - m_new) : 0.0f;
     psum += s[i];
   }
-  psum += xor16(psum);
-  psum += xor32(psum);
+  psum = pair16_sum(psum);
+  psum = pair32_sum(psum);
   st.l = st.l * rescale + psum;
   st.m = m_new;
 
@@ -208,8 +227,13 @@ __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
     st.acc[db][3] *= rescale;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const bf16x8_v vf = *reinterpret_cast<const bf16x8_v*>(
-          &sVt[(16 * db + c.r) * VT_STRIDE + 32 * kb + 8 * c.g]);
+      // A = V^T rows 16 db + r (dims), columns 32 kb + 8 g .. +7 (keys): lane s of a group
+      // addresses key 32 kb + 8 g + s / 4 (+ 4), dims 16 db + 4 (s % 4) .. +3.
+      const bf16_t* vb = &sV[(32 * kb + 8 * c.g + (c.r >> 2)) * VS_STRIDE + 16 * db + 4 * (c.r & 3)];
+      const s16x4_v lo = ld_tr16(vb);
+      const s16x4_v hi = ld_tr16(vb + 4 * VS_STRIDE);
+      const bf16x8_v vf = __builtin_bit_cast(
+          bf16x8_v, static_cast<s16x8_v>(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)));
       st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[kb], st.acc[db], 0, 0, 0);
     }
   }
@@ -219,7 +243,7 @@ __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
 // into `st` tile by tile, with the next tile's loads in flight during each tile's math.
 __device__ __forceinline__ void run_tiles(RowState& st, const Ctx& c, int t_begin, int t_end,
                                           const bf16x8_v (&qf)[4], float sm_scale, bf16_t* sK,
-                                          bf16_t* sVt, int32_t* s_idx) {
+                                          bf16_t* sV, int32_t* s_idx) {
   if (t_begin >= t_end) return;
   __syncthreads();  // previous split's tiles done with s_idx
   stage_slots(s_idx, c, t_begin);
@@ -228,10 +252,10 @@ __device__ __forceinline__ void run_tiles(RowState& st, const Ctx& c, int t_begi
   load_tile(r, c, s_idx, 0);
   for (int t0 = t_begin; t0 < t_end; t0 += BN) {
     __syncthreads();  // previous tile's math done with the LDS tiles
-    store_tile(r, c, sK, sVt);
+    store_tile(r, c, sK, sV);
     __syncthreads();
     if (t0 + BN < t_end) load_tile(r, c, s_idx, t0 + BN - t_begin);
-    tile_math(st, c, t0, qf, sm_scale, sK, sVt);
+    tile_math(st, c, t0, qf, sm_scale, sK, sV);
   }
 }
 
@@ -246,7 +270,7 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
     int64_t total_q, bf16_t* __restrict__ o, float* __restrict__ part_a,
     float* __restrict__ part_ml, int32_t* __restrict__ part_n) {
   __shared__ __align__(16) bf16_t sK[BN * KS_STRIDE];
-  __shared__ __align__(16) bf16_t sVt[D * VT_STRIDE];
+  __shared__ __align__(16) bf16_t sV[BN * VS_STRIDE];
   __shared__ int32_t s_idx[KSPLIT];
 
   const int b = blockIdx.x;
@@ -303,7 +327,7 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
     RowState st;
     fresh(st);
     run_tiles(st, c, split * KSPLIT, min(visible_end, (split + 1) * KSPLIT), qf, sm_scale, sK,
-              sVt, s_idx);
+              sV, s_idx);
     if (!c.row_ok) return;
     const int64_t pr = static_cast<int64_t>(split) * total_q * num_q_heads + prow;
     float* pa = part_a + pr * D;
@@ -322,7 +346,7 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   for (int sp = 0; sp < nsplits; ++sp) {
     RowState st;
     fresh(st);
-    run_tiles(st, c, sp * KSPLIT, min(visible_end, (sp + 1) * KSPLIT), qf, sm_scale, sK, sVt,
+    run_tiles(st, c, sp * KSPLIT, min(visible_end, (sp + 1) * KSPLIT), qf, sm_scale, sK, sV,
               s_idx);
     fold(run, st.m, st.l, st.acc);
   }
