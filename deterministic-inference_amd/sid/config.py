@@ -68,6 +68,12 @@ class EngineConfig:
 
     dvr_window_size: int = 32
     dvr_group_size: int = 4
+    # The reference prefills every is_deterministic request alone (a fixed shape, so its
+    # first token is reproducible). Every prefill kernel here is batch-invariant (GEMM rows
+    # reduce in an M-independent order, extend attention is bitwise independent of
+    # co-batched requests), so a deterministic prompt gets the same bits inside a shared
+    # prefill batch and is batched by default; True restores one-request groups.
+    dvr_isolated_prefill: bool = False
 
     max_kv_splits: int = 32
     invariant_split_size: int = 256

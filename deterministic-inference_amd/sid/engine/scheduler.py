@@ -1,9 +1,11 @@
 """FCFS continuous batching with full KV reservation at admission (sid/engine/scheduler.py).
 
 A request is admitted only when the pool covers every active request's worst case
-(prompt + max_new_tokens), so decode never runs out of slots. In dvr mode deterministic
-requests prefill alone (their token 0 is never re-verified, so its batch must be fixed);
-the rest share prefill batches under max_prefill_tokens.
+(prompt + max_new_tokens), so decode never runs out of slots. Requests share prefill
+batches under max_prefill_tokens. The reference prefills each dvr-mode deterministic
+request alone (its token 0 is never re-verified, so its result must not depend on the
+batch); every prefill kernel here is batch-invariant, so deterministic requests share
+batches too unless EngineConfig.dvr_isolated_prefill asks for one-request groups.
 """
 
 from __future__ import annotations
@@ -46,7 +48,8 @@ class Scheduler:
     def prefill_groups(self, new_reqs: list) -> list:
         groups, shared = [], []
         for r in new_reqs:
-            if self.cfg.mode == Mode.DVR and r.params.is_deterministic:
+            if (self.cfg.mode == Mode.DVR and r.params.is_deterministic
+                    and self.cfg.dvr_isolated_prefill):
                 groups.append([r])
             else:
                 shared.append(r)

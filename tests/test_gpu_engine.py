@@ -78,3 +78,21 @@ def test_engine_step_api_and_release():
     assert eng.kv.free_count == free0  # every slot returned
     with pytest.raises(ValueError):
         eng.add_request(prompt_ids=[1] * 10, params=SamplingParams(max_new_tokens=10 ** 6))
+
+
+def test_dvr_shared_prefill_equals_isolated_prefill():
+    """Deterministic requests prefilled inside shared batches produce exactly the tokens of
+    the reference's one-request prefill groups (the prefill kernels are batch-invariant)."""
+    prompts = _prompts(10, 300)
+    params = [SamplingParams(max_new_tokens=40, temperature=0.7, seed=50 + i,
+                             is_deterministic=i % 2 == 0, ignore_eos=True)
+              for i in range(len(prompts))]
+    outs = {}
+    for isolated in (True, False):
+        cfg = EngineConfig(mode=Mode.DVR, kv_pool_tokens=32768, max_reqs=64, max_seq_len=2048,
+                           max_decode_batch=64, num_layers=4, seed=7,
+                           dvr_isolated_prefill=isolated)
+        print(f"isolated={isolated}", flush=True)
+        outs[isolated] = [o.token_ids for o in Engine(cfg).generate(prompts, params)]
+    for i in range(0, len(prompts), 2):
+        assert outs[True][i] == outs[False][i], i
