@@ -67,7 +67,14 @@ class EngineConfig:
     max_decode_batch: int = 256
 
     dvr_window_size: int = 32
-    dvr_group_size: int = 4
+    # Sequences per verify pass. The reference pads every pass to exactly G = 4 sequences
+    # (a fixed shape keeps its kernels' reduction orders fixed). Every verify-path kernel
+    # here is batch-invariant, so with dvr_verify_buckets a pass takes up to G ready
+    # sequences and is padded only to the next power of two (one graph per size): same
+    # tokens, fewer and fuller passes. dvr_verify_buckets=False, dvr_group_size=4 is the
+    # reference's schedule.
+    dvr_group_size: int = 16
+    dvr_verify_buckets: bool = True
     # The reference prefills every is_deterministic request alone (a fixed shape, so its
     # first token is reproducible). Every prefill kernel here is batch-invariant (GEMM rows
     # reduce in an M-independent order, extend attention is bitwise independent of

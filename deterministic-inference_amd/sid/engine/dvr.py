@@ -1,9 +1,10 @@
 """Decode-verify-rollback (LLM-42 style), as sid/engine/dvr.py.
 
-Every verify pass has the same shape: G sequences x W extend tokens, padded with dummy
-sequences. Fixed shape means the same kernels and reduction orders every time, and the
-extend kernel makes each row depend only on its own sequence, so the verifier's tokens
-are a function of the request's history alone.
+A verify pass is S sequences x W extend tokens, padded with dummy sequences: S = G (the
+reference's fixed shape) or, with EngineConfig.dvr_verify_buckets, the next power of two
+>= the ready sequences (at most G). Every kernel of the pass makes each row depend only on
+its own sequence (batch-invariant GEMMs and extend attention), so the verifier's tokens are
+a function of the request's history alone, whatever S is.
 
 For a real request with prompt length P, verified_len v >= 1 and u = min(unverified, W)
 window tokens t[0..u-1] = output_ids[v:v+u]:
@@ -35,6 +36,13 @@ def _bucket(n: int) -> int:
     while b < n:
         b *= 2
     return b
+
+
+def _pow2_at_least(n: int, cap: int) -> int:
+    b = 1
+    while b < n:
+        b *= 2
+    return min(b, cap)
 
 
 class DummyPool:
@@ -121,7 +129,11 @@ class Verifier:
             top_ps.extend([r.params.top_p] * W)
             seeds.extend([r.params.seed] * W)
 
-        for d in range(len(reqs), G):
+        # Sequences in this pass: G (the reference's fixed shape) or, with bucketed shapes,
+        # the next power of two >= len(reqs); dummy sequences fill the rest.
+        n_pad = _pow2_at_least(len(reqs), G) if self.cfg.dvr_verify_buckets else G
+        rows = n_pad * W
+        for d in range(len(reqs), n_pad):
             dummy = self.pool.dummy_slots[d * W:(d + 1) * W]
             ids.extend([DUMMY_TOKEN_ID] * W)
             positions.extend(range(W))
@@ -134,29 +146,33 @@ class Verifier:
             top_ps.extend([1.0] * W)
             seeds.extend([0] * W)
 
-        buf["input_ids"].copy_(torch.tensor(ids, dtype=torch.int64))
-        buf["positions"].copy_(torch.tensor(positions, dtype=torch.int64))
-        buf["out_slots"].copy_(torch.cat(out_slots).to(torch.int64))
-        buf["sample_positions"].copy_(torch.tensor(spos, dtype=torch.int64))
-        buf["temperatures"].copy_(torch.tensor(temps, dtype=torch.float32))
-        buf["top_ks"].copy_(torch.tensor(top_ks, dtype=torch.int64))
-        buf["top_ps"].copy_(torch.tensor(top_ps, dtype=torch.float32))
-        buf["seeds"].copy_(torch.tensor(seeds, dtype=torch.int64))
+        v = {k: t[:rows] for k, t in buf.items()
+             if k in ("input_ids", "positions", "out_slots", "sample_positions", "temperatures",
+                      "top_ks", "top_ps", "seeds")}
+        v["input_ids"].copy_(torch.tensor(ids, dtype=torch.int64))
+        v["positions"].copy_(torch.tensor(positions, dtype=torch.int64))
+        v["out_slots"].copy_(torch.cat(out_slots).to(torch.int64))
+        v["sample_positions"].copy_(torch.tensor(spos, dtype=torch.int64))
+        v["temperatures"].copy_(torch.tensor(temps, dtype=torch.float32))
+        v["top_ks"].copy_(torch.tensor(top_ks, dtype=torch.int64))
+        v["top_ps"].copy_(torch.tensor(top_ps, dtype=torch.float32))
+        v["seeds"].copy_(torch.tensor(seeds, dtype=torch.int64))
         total_kv = sum(kv_lens)
         buf["kv_indices"][:total_kv].copy_(torch.cat(kv_chunks))
-        indptr = torch.zeros(G + 1, dtype=torch.int64)
+        indptr = torch.zeros(n_pad + 1, dtype=torch.int64)
         indptr[1:] = torch.cumsum(torch.tensor(kv_lens, dtype=torch.int64), dim=0)
-        buf["kv_indptr"].copy_(indptr.to(torch.int32))
+        kv_indptr = buf["kv_indptr"][:n_pad + 1]
+        kv_indptr.copy_(indptr.to(torch.int32))
 
         fb = ForwardBatch(
             mode=ForwardMode.VERIFY,
-            input_ids=buf["input_ids"], positions=buf["positions"], out_slots=buf["out_slots"],
-            qo_indptr=buf["qo_indptr"], kv_indptr=buf["kv_indptr"],
+            input_ids=v["input_ids"], positions=v["positions"], out_slots=v["out_slots"],
+            qo_indptr=buf["qo_indptr"][:n_pad + 1], kv_indptr=kv_indptr,
             kv_indices=buf["kv_indices"][:total_kv], max_extend_len=W,
             max_kv_len=_bucket(max(kv_lens)),
-            sample_indices=self._sample_indices, sample_positions=buf["sample_positions"],
-            temperatures=buf["temperatures"], top_ks=buf["top_ks"], top_ps=buf["top_ps"],
-            seeds=buf["seeds"], invariant=True, all_greedy=all(t == 0 for t in temps),
+            sample_indices=self._sample_indices[:rows], sample_positions=v["sample_positions"],
+            temperatures=v["temperatures"], top_ks=v["top_ks"], top_ps=v["top_ps"],
+            seeds=v["seeds"], invariant=True, all_greedy=all(t == 0 for t in temps),
         )
         return fb, VerifyMeta(reqs=list(reqs), window_lens=window_lens, windows=windows)
 

@@ -115,7 +115,7 @@ class ModelRunner:
     def tag_verify(self, fb: ForwardBatch) -> ForwardBatch:
         """Verify batches always live in the persistent verify buffers: graph them."""
         if self.graphs is not None:
-            fb.graph_key = ("verify", fb.max_kv_len)
+            fb.graph_key = ("verify", fb.input_ids.shape[0], fb.max_kv_len)
         return fb
 
     def sample(self, fb: ForwardBatch, logits: torch.Tensor) -> torch.Tensor:

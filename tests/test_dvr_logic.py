@@ -45,7 +45,9 @@ class FakeRunner:
 
 
 def setup():
-    cfg = EngineConfig(mode=Mode.DVR, dvr_window_size=W, dvr_group_size=G, device="cpu")
+    # the reference's fixed verify shape (every pass padded to G sequences)
+    cfg = EngineConfig(mode=Mode.DVR, dvr_window_size=W, dvr_group_size=G, device="cpu",
+                       dvr_verify_buckets=False)
     kv = FakeKV()
     runner = FakeRunner(cfg)
     return cfg, kv, runner, Verifier(cfg, runner, kv)
@@ -226,3 +228,26 @@ def test_collect_ready_groups_by_rid():
     groups = ver.collect_ready(reqs)
     # rid 7 has 2 unverified and is not finished -> not ready; the rest sorted by rid, G=2
     assert [[r.rid for r in g] for g in groups] == [[1, 2], [5]]
+
+
+def test_bucketed_verify_shapes():
+    """With dvr_verify_buckets a pass holds the next power of two >= its ready sequences
+    (at most G): no dummy sequence for one request, one for three with G = 4."""
+    cfg = EngineConfig(mode=Mode.DVR, dvr_window_size=W, dvr_group_size=4, device="cpu",
+                       dvr_verify_buckets=True)
+    kv = FakeKV()
+    runner = FakeRunner(cfg)
+    ver = Verifier(cfg, runner, kv)
+    p, v = 5, 1
+    req = make_request(kv, 0, p, list(range(50, 59)), v, row=3)
+    fb, _ = ver.build_verify_batch([req])
+    assert fb.input_ids.numel() == W and fb.qo_indptr.tolist() == [0, W]
+    assert fb.kv_indptr.tolist() == [0, p + v - 1 + W]
+    assert fb.kv_indices.numel() == p + v - 1 + W
+    assert fb.sample_indices.numel() == W
+    reqs = [make_request(kv, i, p, list(range(50, 59)), v, row=4 + i) for i in range(3)]
+    fb, meta = ver.build_verify_batch(reqs)
+    assert fb.input_ids.numel() == 4 * W and fb.qo_indptr.tolist() == [0, W, 2 * W, 3 * W, 4 * W]
+    assert fb.input_ids[3 * W:].tolist() == [DUMMY_TOKEN_ID] * W
+    assert fb.kv_indices.numel() == 3 * (p + v - 1 + W) + W
+    assert meta.window_lens == [W] * 3
