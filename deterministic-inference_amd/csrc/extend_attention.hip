@@ -91,16 +91,28 @@ __device__ __forceinline__ void fresh(RowState& s) {
 }
 
 // run <- fold(run, part): the one merge used by every path.
+// The fold's per-row scalars and its elementwise step, shared by every path that folds.
+struct FoldScale {
+  float mn, alpha, beta;
+};
+__device__ __forceinline__ FoldScale fold_scale(float run_m, float m) {
+  const float mn = fmaxf(run_m, m);
+  return {mn, __expf(run_m - mn), __expf(m - mn)};
+}
+// Written as one explicit fma over a separately rounded product, so the compiler has no
+// contraction choice to make differently in different kernels.
+__device__ __forceinline__ float fold_elem(float run, float part, const FoldScale& f) {
+  return __builtin_fmaf(run, f.alpha, part * f.beta);
+}
+
 __device__ __forceinline__ void fold(RowState& run, float m, float l, const f32x4_v (&a)[8]) {
-  const float mn = fmaxf(run.m, m);
-  const float alpha = __expf(run.m - mn);
-  const float beta = __expf(m - mn);
-  run.l = run.l * alpha + l * beta;
+  const FoldScale f = fold_scale(run.m, m);
+  run.l = fold_elem(run.l, l, f);
 #pragma unroll
   for (int db = 0; db < 8; ++db)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) run.acc[db][i] = run.acc[db][i] * alpha + a[db][i] * beta;
-  run.m = mn;
+    for (int i = 0; i < 4; ++i) run.acc[db][i] = fold_elem(run.acc[db][i], a[db][i], f);
+  run.m = f.mn;
 }
 
 struct Ctx {
@@ -362,72 +374,50 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   }
 }
 
-// Fold the fanned-out split states of every (query row, head) item in split order. One
-// 64-lane wave per item (global item = row * HQ + head), 4 per workgroup. The item's split
-// count (written by the attention kernel's split-0 workgroup) and the states of up to
-// MERGE_CHUNK splits are loaded together, in one round of independent loads (states past
-// the item's count are loaded but not used), copied to LDS and folded from there. Every
-// lane reproduces the per-lane layout of the attention kernel (dims 16*db + 4*g + i), so
-// fold() runs on exactly the same operands in the same order as the sequential path.
+// Fold the fanned-out split states of every (query row, head) item in split order: one
+// wave per item (global item = row * HQ + head), lane l owning dims 2l and 2l + 1. fold()
+// is elementwise with per-row scalars, so any assignment of dims to lanes computes the
+// same bits as the attention kernel's own layout. The item's split count (written by the
+// attention kernel's split-0 workgroup) and up to MERGE_CHUNK splits' states are loaded
+// together, then folded.
 constexpr int MERGE_CHUNK = 16;
 
 __global__ void __launch_bounds__(256) extend_merge_kernel(
     int64_t items, int splits, const float* __restrict__ part_a,
     const float* __restrict__ part_ml, const int32_t* __restrict__ part_n,
     bf16_t* __restrict__ o) {
-  __shared__ __align__(16) float s_a[4][MERGE_CHUNK][D];
-  __shared__ float s_ml[4][MERGE_CHUNK][2];
-  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int g = lane >> 4;  // lane layout of the attention kernel
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-  const bool valid = item < items;
-  const int64_t it = valid ? item : items - 1;  // tail waves load a real item, write nothing
-  const int nsplits = part_n[it];
-
-  RowState run;
-  fresh(run);
-  for (int c0 = 0; c0 < splits; c0 += MERGE_CHUNK) {  // splits is uniform: a kernel argument
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= items) return;  // whole waves: no barrier below
+  const int nsplits = part_n[item];
+  float m = NEG_BIG, l = 0.0f;
+  float2 acc = make_float2(0.0f, 0.0f);
+  for (int c0 = 0; c0 < splits; c0 += MERGE_CHUNK) {
     const int n = min(MERGE_CHUNK, splits - c0);
-    float ml = 0.0f;
-    if (lane < 2 * n) ml = part_ml[2 * (static_cast<int64_t>(c0 + (lane >> 1)) * items + it) + (lane & 1)];
-    // every load of the chunk issued before the first LDS store (one round trip)
-    constexpr int kPerLane = MERGE_CHUNK * (D / 4) / 64;
-    f32x4_v buf[kPerLane];
+    float2 a[MERGE_CHUNK];
+    float sm[MERGE_CHUNK], sl[MERGE_CHUNK];
 #pragma unroll
-    for (int u = 0; u < kPerLane; ++u) {
-      const int e = lane + 64 * u;  // split e / 32, 16-byte piece e % 32
-      if (e < n * (D / 4)) {
-        const int64_t pr = static_cast<int64_t>(c0 + (e >> 5)) * items + it;
-        buf[u] = *reinterpret_cast<const f32x4_v*>(part_a + pr * D + 4 * (e & 31));
+    for (int sp = 0; sp < MERGE_CHUNK; ++sp) {
+      if (sp < n) {
+        const int64_t pr = static_cast<int64_t>(c0 + sp) * items + item;
+        a[sp] = reinterpret_cast<const float2*>(part_a + pr * D)[lane];
+        sm[sp] = part_ml[2 * pr];
+        sl[sp] = part_ml[2 * pr + 1];
       }
     }
-    __syncthreads();  // previous chunk folded
-#pragma unroll
-    for (int u = 0; u < kPerLane; ++u) {
-      const int e = lane + 64 * u;
-      if (e < n * (D / 4)) *reinterpret_cast<f32x4_v*>(&s_a[wave][e >> 5][4 * (e & 31)]) = buf[u];
-    }
-    if (lane < 2 * n) s_ml[wave][lane >> 1][lane & 1] = ml;
-    __syncthreads();
     const int use = min(n, nsplits - c0);
-    for (int sp = 0; sp < use; ++sp) {
-      f32x4_v a[8];
 #pragma unroll
-      for (int db = 0; db < 8; ++db)
-        a[db] = *reinterpret_cast<const f32x4_v*>(&s_a[wave][sp][16 * db + 4 * g]);
-      fold(run, s_ml[wave][sp][0], s_ml[wave][sp][1], a);
+    for (int sp = 0; sp < MERGE_CHUNK; ++sp) {
+      if (sp < use) {  // fold() on two dims
+        const FoldScale f = fold_scale(m, sm[sp]);
+        l = fold_elem(l, sl[sp], f);
+        acc.x = fold_elem(acc.x, a[sp].x, f);
+        acc.y = fold_elem(acc.y, a[sp].y, f);
+        m = f.mn;
+      }
     }
   }
-  if (!valid || (lane & 15) != 0) return;  // 4 lanes (g = 0..3) write the 128 dims
-  bf16_t* op = o + item * D;
-#pragma unroll
-  for (int db = 0; db < 8; ++db) {
-    uint2 u;
-    u.x = pack_bf16x2(run.acc[db][0] / run.l, run.acc[db][1] / run.l);
-    u.y = pack_bf16x2(run.acc[db][2] / run.l, run.acc[db][3] / run.l);
-    *reinterpret_cast<uint2*>(op + 16 * db + 4 * g) = u;
-  }
+  reinterpret_cast<uint32_t*>(o + item * D)[lane] = pack_bf16x2(acc.x / l, acc.y / l);
 }
 
 // Fan the splits out when the grid would leave most CUs idle.
