@@ -75,6 +75,12 @@ class EngineConfig:
     # reference's schedule.
     dvr_group_size: int = 16
     dvr_verify_buckets: bool = True
+    # A verify pass costs about the same for 1 and for 16 sequences (weight reads and
+    # per-layer launches dominate), so passes wait until this many windows are ready, unless
+    # a ready request has finished decoding or holds 2 W unverified tokens (it keeps
+    # decoding meanwhile). Committed tokens do not depend on when a window is verified.
+    # 1 = the reference's schedule (verify whatever is ready, every step).
+    dvr_min_verify: int = 8
     # The reference prefills every is_deterministic request alone (a fixed shape, so its
     # first token is reproducible). Every prefill kernel here is batch-invariant (GEMM rows
     # reduce in an M-independent order, extend attention is bitwise independent of

@@ -82,7 +82,13 @@ class Verifier:
         return req.unverified() >= window_size or req.finished_reason is not None
 
     def collect_ready(self, reqs: list) -> list:
+        """Ready requests in rid order, in groups of at most G; nothing while fewer than
+        dvr_min_verify are ready, unless one of them must be verified now (it finished
+        decoding, so only verification can release it, or it holds 2 W unverified tokens)."""
         ready = sorted((r for r in reqs if self.ready(r, self.W)), key=lambda r: r.rid)
+        if len(ready) < self.cfg.dvr_min_verify and not any(
+                r.finished_reason is not None or r.unverified() >= 2 * self.W for r in ready):
+            return []
         return [ready[i:i + self.G] for i in range(0, len(ready), self.G)]
 
     def build_verify_batch(self, reqs: list) -> tuple:

@@ -47,7 +47,7 @@ class FakeRunner:
 def setup():
     # the reference's fixed verify shape (every pass padded to G sequences)
     cfg = EngineConfig(mode=Mode.DVR, dvr_window_size=W, dvr_group_size=G, device="cpu",
-                       dvr_verify_buckets=False)
+                       dvr_verify_buckets=False, dvr_min_verify=1)
     kv = FakeKV()
     runner = FakeRunner(cfg)
     return cfg, kv, runner, Verifier(cfg, runner, kv)
@@ -251,3 +251,21 @@ def test_bucketed_verify_shapes():
     assert fb.input_ids[3 * W:].tolist() == [DUMMY_TOKEN_ID] * W
     assert fb.kv_indices.numel() == 3 * (p + v - 1 + W) + W
     assert meta.window_lens == [W] * 3
+
+
+def test_collect_ready_waits_for_a_full_pass():
+    """With dvr_min_verify = 3, two ready windows wait; a finished request or a 2 W backlog
+    is verified at once, together with every other ready request."""
+    cfg = EngineConfig(mode=Mode.DVR, dvr_window_size=W, dvr_group_size=4, device="cpu",
+                       dvr_min_verify=3)
+    kv = FakeKV()
+    ver = Verifier(cfg, FakeRunner(cfg), kv)
+    a = make_request(kv, 1, 3, list(range(50, 59)), 1, row=1)    # W unverified
+    b = make_request(kv, 2, 3, list(range(50, 59)), 1, row=2)
+    assert ver.collect_ready([a, b]) == []
+    c = make_request(kv, 3, 3, list(range(50, 50 + 2 * W + 1)), 1, row=3)  # 2 W unverified
+    assert [[r.rid for r in g] for g in ver.collect_ready([a, b, c])] == [[1, 2, 3]]
+    d = make_request(kv, 4, 3, [50, 51, EOS], 1, row=4)          # finished, 2 unverified
+    assert [[r.rid for r in g] for g in ver.collect_ready([a, d])] == [[1, 4]]
+    e = make_request(kv, 5, 3, list(range(50, 59)), 1, row=5)
+    assert [[r.rid for r in g] for g in ver.collect_ready([a, b, e])] == [[1, 2, 5]]

@@ -80,19 +80,24 @@ def test_engine_step_api_and_release():
         eng.add_request(prompt_ids=[1] * 10, params=SamplingParams(max_new_tokens=10 ** 6))
 
 
-def test_dvr_shared_prefill_equals_isolated_prefill():
-    """Deterministic requests prefilled inside shared batches produce exactly the tokens of
-    the reference's one-request prefill groups (the prefill kernels are batch-invariant)."""
+def test_dvr_schedule_does_not_change_tokens():
+    """This engine's DVR schedule (deterministic prompts in shared prefill batches, verify
+    passes of up to 16 sequences padded to a power of two, passes deferred until 8 windows
+    are ready) commits exactly the tokens of the reference's schedule (one-request prefill
+    groups, every pass padded to G = 4, verify whatever is ready every step)."""
     prompts = _prompts(10, 300)
-    params = [SamplingParams(max_new_tokens=40, temperature=0.7, seed=50 + i,
+    params = [SamplingParams(max_new_tokens=70, temperature=0.7, seed=50 + i,
                              is_deterministic=i % 2 == 0, ignore_eos=True)
               for i in range(len(prompts))]
+    reference = dict(dvr_isolated_prefill=True, dvr_group_size=4, dvr_verify_buckets=False,
+                     dvr_min_verify=1)
     outs = {}
-    for isolated in (True, False):
+    for name, extra in (("reference", reference), ("default", {})):
         cfg = EngineConfig(mode=Mode.DVR, kv_pool_tokens=32768, max_reqs=64, max_seq_len=2048,
-                           max_decode_batch=64, num_layers=4, seed=7,
-                           dvr_isolated_prefill=isolated)
-        print(f"isolated={isolated}", flush=True)
-        outs[isolated] = [o.token_ids for o in Engine(cfg).generate(prompts, params)]
+                           max_decode_batch=64, num_layers=4, seed=7, **extra)
+        print(f"schedule={name}", flush=True)
+        res = Engine(cfg).generate(prompts, params)
+        outs[name] = [o.token_ids for o in res]
+        assert all(o.num_windows > 0 for o, p in zip(res, params) if p.is_deterministic)
     for i in range(0, len(prompts), 2):
-        assert outs[True][i] == outs[False][i], i
+        assert outs["reference"][i] == outs["default"][i], i
