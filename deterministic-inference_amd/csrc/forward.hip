@@ -12,6 +12,9 @@ namespace sid {
 namespace {
 
 constexpr int64_t kAlign = 256;
+// Greedy rows up to this count take the lm_head with the fused argmax (one streaming pass
+// over the weights, no logits); more rows go through fp32 logits (tiled GEMM) + argmax.
+constexpr int64_t kFusedArgmaxMaxRows = 64;
 
 struct Carver {
   char* base;
@@ -107,7 +110,8 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
   const int64_t t = b->num_tokens;
   const int64_t r = b->sample_indices ? b->num_samples : t;
   SID_REQUIRE(r > 0, "qwen3_extend_forward: no sampled rows");
-  SID_REQUIRE(logits || r <= 256, "qwen3_extend_forward: greedy over %lld rows needs a logits buffer",
+  SID_REQUIRE(logits || r <= kFusedArgmaxMaxRows,
+              "qwen3_extend_forward: greedy over %lld rows needs a logits buffer",
               (long long)r);
   const Layout l = plan(m, b, workspace);
   SID_REQUIRE(workspace && workspace_bytes >= l.total,
@@ -177,7 +181,7 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
     SID_TRY(sid_gather_rows(l.x, b->sample_indices, l.rows, r, h, t, stream));
     rows = l.rows;
   }
-  if (greedy_tokens && r <= 256) {
+  if (greedy_tokens && r <= kFusedArgmaxMaxRows) {
     return sid_linear_argmax(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, l.argmax_ws,
                              l.argmax_ws_bytes, greedy_tokens, stream);
   }

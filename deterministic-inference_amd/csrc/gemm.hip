@@ -758,12 +758,15 @@ extern "C" int sid_linear(const void* x, int64_t ldx, const void* w, const void*
   int rc = check_shapes(x, ldx, w, m, n, k, "linear");
   if (rc != SID_OK) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (stream_shape_ok(m, n, k) && n >= kStreamMinN) {
+  // The streaming kernel reads the weights once per 64-row group; past one group the tiled
+  // kernel (each weight row reused by 128 rows) is faster: M = 128 151936 x 1024 fp32
+  // logits 165 -> 101 us, M = 256 327 -> 179 us (identical bits).
+  if (m <= MROWS && stream_shape_ok(m, n, k) && n >= kStreamMinN) {
     launch_stream<false>(x, ldx, w, bias, y, static_cast<int>(m), static_cast<int>(n), out_fp32,
                          nullptr, nullptr, s);
     return check_launch("linear");
   }
-  if (m >= kTiledMinM) {
+  if (m >= kTiledMinM || (m > MROWS && n >= kStreamMinN)) {
     SID_REQUIRE((m + 63) / 64 <= 65535, "linear: too many rows");
     const int64_t wide_tiles = ((m + 127) / 128) * ((n + 127) / 128);
     if (wide_tiles >= kTiledWideMinTiles) {

@@ -66,6 +66,12 @@ def linear_argmax_supported(m: int, k: int) -> bool:
     return 1 <= m <= 256 and k == 1024
 
 
+def linear_argmax_preferred(m: int, k: int) -> bool:
+    """Where the fused kernel is the faster choice: one 64-row group (it streams the weights
+    once per group; more rows go through the tiled GEMM's logits + argmax_rows)."""
+    return 1 <= m <= 64 and k == 1024
+
+
 def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
                   logits: Optional[torch.Tensor] = None,
                   workspace: Optional[torch.Tensor] = None,

@@ -16,6 +16,9 @@ from sid.kernels.jit import load_ext
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 
+FUSED_ARGMAX_MAX_ROWS = 64  # csrc/forward.hip kFusedArgmaxMaxRows
+
+
 class Layer(ctypes.Structure):
     _fields_ = [("input_ln", _vp), ("qkv", _vp), ("q_norm", _vp), ("k_norm", _vp), ("o", _vp),
                 ("post_ln", _vp), ("gate_up", _vp), ("down", _vp), ("k_cache", _vp),
@@ -92,7 +95,7 @@ class NativeQwen3:
         tokens: Optional[torch.Tensor] = None
         if greedy:
             tokens = torch.empty(r, dtype=torch.int64, device=dev)
-            if r > 256:
+            if r > FUSED_ARGMAX_MAX_ROWS:  # the library needs a logits buffer past that
                 logits = torch.empty(r, self.vocab, dtype=torch.float32, device=dev)
         else:
             logits = torch.empty(r, self.vocab, dtype=torch.float32, device=dev)

@@ -15,7 +15,7 @@ import torch
 from sid.config import ModelConfig
 from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.kernels.extend_attention import extend_attention_fwd
-from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_supported,
+from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_preferred,
                                             linear_partials)
 from sid.kernels.ops import (argmax_rows, embedding, fused_add_rmsnorm_partials, gather_rows, qkv_post,
                              silu_mul, silu_mul_partials)
@@ -108,7 +108,7 @@ class Qwen3Model:
                 x, residual = fused_add_rmsnorm(linear(act, lw["down"]), residual, next_w, eps)
         rows = x if fb.sample_indices is None else gather_rows(x, fb.sample_indices)
         if greedy:
-            if linear_argmax_supported(rows.shape[0], rows.shape[1]):
+            if linear_argmax_preferred(rows.shape[0], rows.shape[1]):
                 return linear_argmax(rows, self.w["lm_head"])
             return argmax_rows(linear(rows, self.w["lm_head"], out_fp32=True))
         return linear(rows, self.w["lm_head"], out_fp32=True)

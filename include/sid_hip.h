@@ -34,7 +34,7 @@ extern "C" {
 /* Message describing the last non-SID_OK return on this thread ("" if none). */
 const char* sid_last_error(void);
 
-/* ABI version of this library (bumped on any signature change). */
+/* ABI version of this library (bumped on any signature or precondition change). */
 int sid_abi_version(void);
 
 /*
@@ -268,7 +268,7 @@ int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bia
  * has no counterpart of its own in the reference, whose forward is Python.
  * Projections of <= split_k_max_tokens tokens use the split-K path. Outputs:
  * logits fp32 [R, vocab] and/or greedy_tokens int64 [R] (R = num_samples, or
- * num_tokens without sample_indices; greedy without logits needs R <= 256).
+ * num_tokens without sample_indices; greedy without logits needs R <= 64).
  */
 typedef struct {
   const void* input_ln;
