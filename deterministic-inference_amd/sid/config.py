@@ -81,6 +81,9 @@ class EngineConfig:
     # decoding meanwhile). Committed tokens do not depend on when a window is verified.
     # 1 = the reference's schedule (verify whatever is ready, every step).
     dvr_min_verify: int = 8
+    # Run a step's verify passes on a side stream beside its decode step (graphs only; the
+    # verify windows are then taken before the decode appends). False: decode, then verify.
+    dvr_overlap_verify: bool = True
     # The reference prefills every is_deterministic request alone (a fixed shape, so its
     # first token is reproducible). Every prefill kernel here is batch-invariant (GEMM rows
     # reduce in an M-independent order, extend attention is bitwise independent of

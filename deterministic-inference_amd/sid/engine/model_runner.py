@@ -148,7 +148,10 @@ class GraphCache:
         self.runner = runner
         self.max_graphs = max_graphs
         self.graphs: OrderedDict = OrderedDict()
-        self.pool = torch.cuda.graph_pool_handle()
+        # Graphs of one kind replay in order on one stream and share a memory pool; decode
+        # and verify graphs may replay concurrently on two streams, so each kind has its own.
+        self.pools = {"decode": torch.cuda.graph_pool_handle(),
+                      "verify": torch.cuda.graph_pool_handle()}
         self.decode_static = DecodeStatic(cfg.max_decode_batch,
                                           cfg.max_decode_batch * cfg.max_seq_len, runner.device)
 
@@ -173,6 +176,6 @@ class GraphCache:
         runner._forward_eager(fb, greedy)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, pool=self.pool):
+        with torch.cuda.graph(graph, pool=self.pools[fb.graph_key[0]]):
             out = runner._forward_eager(fb, greedy)
         return graph, out

@@ -83,14 +83,15 @@ def test_engine_step_api_and_release():
 def test_dvr_schedule_does_not_change_tokens():
     """This engine's DVR schedule (deterministic prompts in shared prefill batches, verify
     passes of up to 16 sequences padded to a power of two, passes deferred until 8 windows
-    are ready) commits exactly the tokens of the reference's schedule (one-request prefill
-    groups, every pass padded to G = 4, verify whatever is ready every step)."""
+    are ready, run on a side stream beside the step's decode) commits exactly the tokens of
+    the reference's schedule (one-request prefill groups, every pass padded to G = 4,
+    verify whatever is ready after every decode step)."""
     prompts = _prompts(10, 300)
     params = [SamplingParams(max_new_tokens=70, temperature=0.7, seed=50 + i,
                              is_deterministic=i % 2 == 0, ignore_eos=True)
               for i in range(len(prompts))]
     reference = dict(dvr_isolated_prefill=True, dvr_group_size=4, dvr_verify_buckets=False,
-                     dvr_min_verify=1)
+                     dvr_min_verify=1, dvr_overlap_verify=False)
     outs = {}
     for name, extra in (("reference", reference), ("default", {})):
         cfg = EngineConfig(mode=Mode.DVR, kv_pool_tokens=32768, max_reqs=64, max_seq_len=2048,
