@@ -152,6 +152,7 @@ class GraphCache:
         # and verify graphs may replay concurrently on two streams, so each kind has its own.
         self.pools = {"decode": torch.cuda.graph_pool_handle(),
                       "verify": torch.cuda.graph_pool_handle()}
+        self._warm: set = set()
         self.decode_static = DecodeStatic(cfg.max_decode_batch,
                                           cfg.max_decode_batch * cfg.max_seq_len, runner.device)
 
@@ -171,9 +172,14 @@ class GraphCache:
 
     def _capture(self, fb: ForwardBatch, greedy: bool):
         runner = self.runner
-        # One eager pass first (lazy initialisation inside torch ops happens outside the
-        # capture); it computes exactly what the replay will recompute.
-        runner._forward_eager(fb, greedy)
+        kind = fb.graph_key[0]
+        if kind not in self._warm:
+            # One eager pass before the first capture of a kind, so lazy initialisation
+            # (library load, descriptors, torch's first-use work) happens outside a capture;
+            # it computes exactly what the replay recomputes. Later captures of the kind run
+            # the same host code and skip it.
+            runner._forward_eager(fb, greedy)
+            self._warm.add(kind)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self.pools[fb.graph_key[0]]):
