@@ -26,14 +26,28 @@ HQ, HKV, D = 16, 8, 128
 HBM_PEAK_GBS = 8000.0
 
 
-def _time_us(fn, reps=50, warm=5):
+def _time_us(fn, reps=50, warm=5, graph=True):
+    """Average device time per call: reps back-to-back calls captured in one HIP graph and
+    replayed between two events (host launch cost is not in the number); graph=False times
+    eager launches instead."""
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
+    g = None
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(reps):
-        fn()
+    if g is not None:
+        g.replay()
+    else:
+        for _ in range(reps):
+            fn()
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / reps * 1e3
@@ -168,7 +182,7 @@ def config4(args):
 
     def one():
         runner.step(fb)
-    us = _time_us(one, reps=20, warm=3)
+    us = _time_us(one, reps=20, warm=3, graph=False)  # runner.step replays its own graph
     return {"metric": "DVR verify pass (G=4 x W=32 over 2048-token prefixes) (config 4)",
             "value": round(us / 1e3, 3), "unit": "ms/pass", "higher_is_better": False,
             "verify_tokens_per_s": round(128 / (us * 1e-6), 1),

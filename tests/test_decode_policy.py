@@ -39,9 +39,12 @@ def test_heuristic_splits_matches_reference_formula_cases():
 
 
 def test_segment_size_prefers_long_segments_when_grid_is_full():
-    assert segment_size(64, 2049, 256) == 256
+    # largest segment with >= 1.5 workgroups per CU (384 on 256 CUs)
+    assert segment_size(64, 2049, 256) == 256   # 64 x 9 = 576
+    assert segment_size(32, 2049, 256) == 128   # 32 x 9 = 288 < 384; 32 x 17 = 544
     assert segment_size(8, 2049, 256) == 64
-    assert segment_size(4, 8192, 256) == 128
+    assert segment_size(4, 8192, 256) == 64     # 4 x 64 = 256 < 384 at 128
+    assert segment_size(48, 1025, 256) == 128   # 48 x 5 = 240; 48 x 9 = 432
     assert segment_size(1, 10, 256) == SEGMENT_SIZES[-1]
 
 
