@@ -288,7 +288,10 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   const int b = blockIdx.x;
   const int h_kv = blockIdx.y;
   constexpr bool fanout = FANOUT;
-  const int mtile = fanout ? static_cast<int>(blockIdx.z) % mtiles : static_cast<int>(blockIdx.z);
+  // Without fan-out a workgroup walks every split up to its tile's causal limit, so late
+  // query tiles take longest: dispatch them first (blockIdx.z = 0 is the last tile).
+  const int mtile = fanout ? static_cast<int>(blockIdx.z) % mtiles
+                           : mtiles - 1 - static_cast<int>(blockIdx.z);
   const int split = fanout ? static_cast<int>(blockIdx.z) / mtiles : 0;
 
   Ctx c;
