@@ -47,6 +47,14 @@ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_to_f32(f32_to_bf16(f));
 }
 
+// SwiGLU element on bf16-rounded inputs: bf16(silu(g)) * u (torch's F.silu(gate) * up,
+// before the caller's final rounding). Shared by silu_mul_kernel and the GEMM epilogue that
+// fuses it, so both give the same bits.
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+  const float s = round_bf16(g / (1.0f + __expf(-g)));
+  return s * u;
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }

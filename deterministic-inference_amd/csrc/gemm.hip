@@ -745,6 +745,83 @@ void launch_stream(const void* x, int64_t ldx, const void* w, const void* bias, 
   }
 }
 
+// ---- gate_up projection with the SwiGLU epilogue (decode-sized M) -----------------------
+//
+// out[m, j] = bf16(bf16(silu(g)) * u), g = bf16(x w[j]^T), u = bf16(x w[I + j]^T), each a
+// canonical chunk fold: the same bits as sid_linear_partials + sid_silu_mul_partials, with
+// neither the fp32 partials' round trip through memory nor the second launch. A workgroup
+// has one wave per 256-wide chunk (NCH waves, K = 256 NCH) and owns 8 output columns of a
+// 64-row group: MFMA column lanes 0-7 are gate rows j0..j0+7 and lanes 8-15 up rows
+// I+j0..I+j0+7 of w. Wave c accumulates chunk c from zero with x and w fragments loaded
+// straight from global memory (each wave reads a different chunk, so nothing is shared
+// through LDS); the chunk sums meet in LDS and are folded c0 + c1 + ... in order.
+template <int NCH, int MBS>
+__global__ void __launch_bounds__(NCH * 64) linear_silu_kernel(const bf16_t* __restrict__ x,
+                                                               const bf16_t* __restrict__ w,
+                                                               int64_t M, int64_t inter,
+                                                               bf16_t* __restrict__ out) {
+  constexpr int64_t K = static_cast<int64_t>(NCH) * KC;
+  constexpr int SS = 17;  // LDS row stride of a chunk sum tile (floats)
+  __shared__ float sacc[NCH][MROWS * SS];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int64_t j0 = static_cast<int64_t>(blockIdx.x) * 8;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * MROWS;
+  const int mrows = static_cast<int>(min<int64_t>(MROWS, M - m0));
+  const int64_t k0 = static_cast<int64_t>(wave) * KC;
+  const int64_t wr = r < 8 ? j0 + r : inter + j0 + (r - 8);
+
+  bf16x8_v wf[NSTEP];
+  load_w(wf, w + wr * K + 8 * g, k0);
+  bf16x8_v xf[MBS][NSTEP];
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) {
+    const int64_t row = min<int64_t>(m0 + 16 * mb + r, M - 1);  // clamped rows are dropped
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) xf[mb][s] = ld_frag(x + row * K + k0 + KSTEP * s + 8 * g);
+  }
+  // Every load is issued before the first MFMA (one memory latency per workgroup; left to
+  // itself the compiler interleaves loads and MFMAs and waits on each group).
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4_v acc[MBS];
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) acc[mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb)
+      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[mb][s], wf[s], acc[mb], 0, 0, 0);
+  }
+  // Lane holds rows 16 mb + 4 g + i of column r.
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sacc[wave][(16 * mb + 4 * g + i) * SS + r] = acc[mb][i];
+  }
+  __syncthreads();
+  // 64 rows x 8 outputs, two adjacent outputs per thread.
+  for (int o = threadIdx.x; o < MBS * 16 * 4; o += NCH * 64) {
+    const int row = o >> 2;
+    const int col = 2 * (o & 3);
+    if (row >= mrows) continue;
+    float y[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float gs = sacc[0][row * SS + col + e];
+      float us = sacc[0][row * SS + 8 + col + e];
+#pragma unroll
+      for (int c = 1; c < NCH; ++c) {
+        gs += sacc[c][row * SS + col + e];
+        us += sacc[c][row * SS + 8 + col + e];
+      }
+      y[e] = silu_mul1(round_bf16(gs), round_bf16(us));
+    }
+    *reinterpret_cast<uint32_t*>(out + (m0 + row) * inter + j0 + col) = pack_bf16x2(y[0], y[1]);
+  }
+}
+
 }  // namespace
 }  // namespace sid
 
@@ -838,4 +915,33 @@ extern "C" int sid_linear_argmax(const void* x, int64_t ldx, const void* w, cons
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(256), 0, s, bv, bi, waves,
                      static_cast<int>(m), out_idx);
   return check_launch("linear_argmax finalize");
+}
+
+extern "C" int sid_linear_silu_mul(const void* x, const void* w, void* out, int64_t m, int64_t k,
+                                   int64_t inter, void* stream) {
+  SID_REQUIRE(m >= 0 && k >= 0 && inter >= 0, "linear_silu_mul: negative size");
+  if (m == 0 || inter == 0) return SID_OK;
+  SID_REQUIRE(x && w && out, "linear_silu_mul: null pointer");
+  SID_REQUIRE(k == 4 * KC, "linear_silu_mul: K must be %d, got %lld", 4 * KC, (long long)k);
+  SID_REQUIRE(inter % 8 == 0, "linear_silu_mul: intermediate size %lld not a multiple of 8",
+              (long long)inter);
+  SID_REQUIRE(inter / 8 <= 0x7fffffff && (m + MROWS - 1) / MROWS <= 65535,
+              "linear_silu_mul: too large");
+  SID_REQUIRE((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(out) % 4 == 0,
+              "linear_silu_mul: misaligned operand");
+  const dim3 grid((unsigned)(inter / 8), (unsigned)((m + MROWS - 1) / MROWS));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int mbs = m >= MROWS ? 4 : static_cast<int>((m + 15) / 16);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(4 * 64), 0, s, (const bf16_t*)x, (const bf16_t*)w, m,
+                       inter, (bf16_t*)out);
+  };
+  switch (mbs) {
+    case 1: go(linear_silu_kernel<4, 1>); break;
+    case 2: go(linear_silu_kernel<4, 2>); break;
+    case 3: go(linear_silu_kernel<4, 3>); break;
+    default: go(linear_silu_kernel<4, 4>); break;
+  }
+  return check_launch("linear_silu_mul");
 }

@@ -129,11 +129,6 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
   o2 = fmaf(x2, c, x1 * s);
 }
 
-__device__ __forceinline__ float silu_mul1(float g, float u) {
-  const float s = round_bf16(g / (1.0f + __expf(-g)));
-  return s * u;
-}
-
 // ---- RMSNorm ----------------------------------------------------------------------------
 
 constexpr int MAXV = 16;  // vectors per lane kept in registers between the two passes

@@ -33,6 +33,7 @@ _SIGNATURES = {
     "sid_qkv_post": [_vp, _vp, _i32, _i64, _i32, _i32, _i32, _vp, _vp, _f32, _vp, _vp, _i64, _vp,
                      _vp, _vp, _vp, _i64, _vp],
     "sid_silu_mul": [_vp, _vp, _i64, _i64, _vp],
+    "sid_linear_silu_mul": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
     "sid_build_decode_indices": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
@@ -45,7 +46,7 @@ _SIGNATURES = {
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
             "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes",
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward", *_SIGNATURES)
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -303,6 +304,16 @@ class NativeLib:
                    q_norm.data_ptr(), k_norm.data_ptr(), float(eps), positions.data_ptr(),
                    cos_sin.data_ptr(), cos_sin.shape[0], slots.data_ptr(), q_out.data_ptr(),
                    k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0], _stream(q_out))
+
+    def linear_silu_mul(self, x, w, out) -> None:
+        _gpu(x, "x", torch.bfloat16)
+        _gpu(w, "weight", torch.bfloat16)
+        _gpu(out, "out", torch.bfloat16)
+        _check(x.dim() == 2 and w.dim() == 2 and w.shape[1] == x.shape[1], "x / weight shapes")
+        _check(w.shape[0] % 2 == 0 and tuple(out.shape) == (x.shape[0], w.shape[0] // 2),
+               "linear_silu_mul: out must be [M, N/2]")
+        self._call("sid_linear_silu_mul", x.data_ptr(), w.data_ptr(), out.data_ptr(), x.shape[0],
+                   x.shape[1], w.shape[0] // 2, _stream(out))
 
     def silu_mul(self, gate_up, out) -> None:
         _gpu(gate_up, "gate_up", torch.bfloat16)

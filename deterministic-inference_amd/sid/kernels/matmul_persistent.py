@@ -61,6 +61,27 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor,
     return out
 
 
+# Rows up to which the fused gate_up + SwiGLU kernel replaces linear_partials +
+# silu_mul_partials. Every workgroup reads its rows' whole x (K = 1024) for 8 output
+# columns, 4x the x traffic of the split-K kernel, so the saved launch and partial round trip
+# win only for small batches (MI355X, gate_up 6144 x 1024, weights from HBM, graph-timed:
+# M=1 7.95 -> 5.54 us, M=32 9.94 -> 8.78, M=64 12.56 -> 12.29; M=128 16.1 -> 17.0 slower).
+LINEAR_SILU_MAX_ROWS = 64
+
+
+def linear_silu_mul_preferred(m: int, k: int) -> bool:
+    """Shapes where linear_silu_mul is used for the MLP's first half (K = 1024)."""
+    return 1 <= m <= LINEAR_SILU_MAX_ROWS and k == 1024
+
+
+def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """F.silu(gate) * up of (gate, up) = (x @ weight^T).chunk(2, -1), as one launch: the same
+    bits as silu_mul_partials(linear_partials(x, weight)). x [M, 1024] bf16 -> [M, N/2]."""
+    out = torch.empty(x.shape[0], weight.shape[0] // 2, dtype=torch.bfloat16, device=x.device)
+    load_ext().linear_silu_mul(x, weight, out)
+    return out
+
+
 def linear_argmax_supported(m: int, k: int) -> bool:
     """Shapes the fused lm_head + greedy argmax kernel takes (M <= 256, K = 1024)."""
     return 1 <= m <= 256 and k == 1024

@@ -16,7 +16,8 @@ from sid.config import ModelConfig
 from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.kernels.extend_attention import extend_attention_fwd
 from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_preferred,
-                                            linear_partials)
+                                            linear_partials, linear_silu_mul,
+                                            linear_silu_mul_preferred)
 from sid.kernels.ops import (argmax_rows, embedding, fused_add_rmsnorm_partials, gather_rows, qkv_post,
                              silu_mul, silu_mul_partials)
 from sid.kernels.rmsnorm import fused_add_rmsnorm, rmsnorm
@@ -96,7 +97,10 @@ class Qwen3Model:
             if split:
                 x, residual = fused_add_rmsnorm_partials(linear_partials(o, lw["o"]), residual,
                                                          lw["post_ln"], eps)
-                act = silu_mul_partials(linear_partials(x, lw["gate_up"]))
+                if linear_silu_mul_preferred(t, x.shape[1]):
+                    act = linear_silu_mul(x, lw["gate_up"])
+                else:
+                    act = silu_mul_partials(linear_partials(x, lw["gate_up"]))
             else:
                 x, residual = fused_add_rmsnorm(linear(o, lw["o"]), residual, lw["post_ln"], eps)
                 act = silu_mul(linear(x, lw["gate_up"]))

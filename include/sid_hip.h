@@ -200,6 +200,19 @@ int sid_silu_mul_partials(const float* partials, int nchunks, void* out, int64_t
                           int64_t inter, void* stream);
 
 /*
+ * The gate_up projection and SwiGLU in one launch: out[t, j] =
+ * bf16(bf16(silu(g)) * u) with g = row j and u = row I + j of
+ * x @ w^T (x bf16 [M, K] contiguous, w bf16 [2I, K]), both in sid_linear's
+ * reduction order and rounding. Bit-identical to sid_linear_partials followed
+ * by sid_silu_mul_partials. K must be 1024; I a multiple of 8; x and w
+ * 16-byte aligned. out bf16 [M, I].
+ * Replaces sid/model/qwen3.py:84-85 (gate_up = F.linear(...);
+ * F.silu(gate) * up) for decode-sized batches.
+ */
+int sid_linear_silu_mul(const void* x, const void* w, void* out, int64_t m, int64_t k,
+                        int64_t inter, void* stream);
+
+/*
  * Fused QKV epilogue of Qwen3 attention (sid/model/qwen3.py:49-61): row t of
  * the projection is [q (HQ*D) | k (HKV*D) | v (HKV*D)], given either as bf16
  * qkv [T, (HQ+2*HKV)*D] or as sid_linear_partials output (exactly one of qkv

@@ -2,7 +2,8 @@
   qkv_post  == split + contiguous + qk_head_rmsnorm(q), (k) + RoPE + reshape_and_cache
                (sid/model/qwen3.py:49-61), fed by linear or by linear_partials;
   fused_add_rmsnorm_partials == linear + fused_add_rmsnorm;
-  silu_mul_partials          == linear + silu_mul."""
+  silu_mul_partials          == linear + silu_mul;
+  linear_silu_mul            == linear_partials + silu_mul_partials."""
 
 from __future__ import annotations
 
@@ -79,3 +80,23 @@ def test_silu_mul_partials_matches_unfused(t):
     x = torch.randn(t, 1024, device="cuda", dtype=torch.bfloat16)
     w = (torch.randn(6144, 1024, device="cuda") * 0.05).to(torch.bfloat16)
     assert torch.equal(silu_mul_partials(linear_partials(x, w)), silu_mul(linear(x, w)))
+
+
+@pytest.mark.parametrize("t", [1, 5, 16, 33, 64, 65, 128, 200, 256])
+@pytest.mark.parametrize("inter", [3072, 96])
+def test_linear_silu_mul_matches_unfused(t, inter):
+    """gate_up projection + SwiGLU in one launch == linear_partials + silu_mul_partials (and
+    == linear + silu_mul), bit for bit, on full and ragged 64-row groups."""
+    from sid.kernels.matmul_persistent import linear, linear_partials, linear_silu_mul
+    from sid.kernels.ops import silu_mul, silu_mul_partials
+    print(f"linear_silu_mul t={t} inter={inter}", flush=True)
+    torch.manual_seed(1000 * t + inter)
+    x = torch.randn(t, 1024, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(2 * inter, 1024, device="cuda") * 0.05).to(torch.bfloat16)
+    fused = linear_silu_mul(x, w)
+    assert torch.equal(fused, silu_mul_partials(linear_partials(x, w)))
+    assert torch.equal(fused, silu_mul(linear(x, w)))
+    # torch fp32 reference of the same op (bf16 tolerance)
+    gu = (x.float() @ w.float().t())
+    ref = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]
+    assert (fused.float() - ref).abs().max().item() <= 2e-2 * max(1.0, ref.abs().max().item())
