@@ -11,6 +11,10 @@
 namespace sid {
 namespace {
 
+// Rows up to which the gate_up projection and SwiGLU run as sid_linear_silu_mul (the same
+// bits as the split-K pair; faster up to here on MI355X, slower beyond).
+constexpr int64_t kLinearSiluMaxRows = 128;
+
 constexpr int64_t kAlign = 256;
 // Greedy rows up to this count take the lm_head with the fused argmax (one streaming pass
 // over the weights, no logits); more rows go through fp32 logits (tiled GEMM) + argmax.
@@ -157,8 +161,10 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
       SID_TRY(sid_linear(l.attn, ao, lw.o, nullptr, l.x, t, h, ao, 0, stream));
       SID_TRY(sid_fused_add_rmsnorm(l.x, l.resid, lw.post_ln, t, h, eps, stream));
     }
-    // act = silu(gate) * up
-    if (split) {
+    // act = silu(gate) * up (one launch for up to kLinearSiluMaxRows rows)
+    if (t <= kLinearSiluMaxRows && h == 1024) {
+      SID_TRY(sid_linear_silu_mul(l.x, lw.gate_up, l.act, t, h, inter, stream));
+    } else if (split) {
       SID_TRY(sid_linear_partials(l.x, h, lw.gate_up, part, t, 2 * inter, h, stream));
       SID_TRY(sid_silu_mul_partials(part, h / 256, l.act, t, inter, stream));
     } else {

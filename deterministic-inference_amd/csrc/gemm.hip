@@ -750,31 +750,35 @@ void launch_stream(const void* x, int64_t ldx, const void* w, const void* bias, 
 // out[m, j] = bf16(bf16(silu(g)) * u), g = bf16(x w[j]^T), u = bf16(x w[I + j]^T), each a
 // canonical chunk fold: the same bits as sid_linear_partials + sid_silu_mul_partials, with
 // neither the fp32 partials' round trip through memory nor the second launch. A workgroup
-// has one wave per 256-wide chunk (NCH waves, K = 256 NCH) and owns 8 output columns of a
-// 64-row group: MFMA column lanes 0-7 are gate rows j0..j0+7 and lanes 8-15 up rows
-// I+j0..I+j0+7 of w. Wave c accumulates chunk c from zero with x and w fragments loaded
-// straight from global memory (each wave reads a different chunk, so nothing is shared
-// through LDS); the chunk sums meet in LDS and are folded c0 + c1 + ... in order.
-template <int NCH, int MBS>
+// has one wave per 256-wide chunk (NCH waves, K = 256 NCH) and owns 8 NB output columns of
+// a 64-row group; in MFMA column block nb, lanes 0-7 are gate rows j0+8nb.. and lanes 8-15
+// the matching up rows I+j0+8nb.. of w. Wave c accumulates chunk c from zero with x and w
+// fragments loaded straight from global memory (each wave reads a different chunk, so
+// nothing is shared through LDS; the NB column blocks share the wave's x fragments); the
+// chunk sums meet in LDS and are folded c0 + c1 + ... in order.
+template <int NCH, int MBS, int NB>
 __global__ void __launch_bounds__(NCH * 64) linear_silu_kernel(const bf16_t* __restrict__ x,
                                                                const bf16_t* __restrict__ w,
                                                                int64_t M, int64_t inter,
                                                                bf16_t* __restrict__ out) {
   constexpr int64_t K = static_cast<int64_t>(NCH) * KC;
-  constexpr int SS = 17;  // LDS row stride of a chunk sum tile (floats)
+  constexpr int SS = 16 * NB + 1;  // LDS row stride of a chunk sum tile (floats)
   __shared__ float sacc[NCH][MROWS * SS];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int64_t j0 = static_cast<int64_t>(blockIdx.x) * 8;
+  const int64_t j0 = static_cast<int64_t>(blockIdx.x) * (8 * NB);
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * MROWS;
   const int mrows = static_cast<int>(min<int64_t>(MROWS, M - m0));
   const int64_t k0 = static_cast<int64_t>(wave) * KC;
-  const int64_t wr = r < 8 ? j0 + r : inter + j0 + (r - 8);
 
-  bf16x8_v wf[NSTEP];
-  load_w(wf, w + wr * K + 8 * g, k0);
+  bf16x8_v wf[NB][NSTEP];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t wr = r < 8 ? j0 + 8 * nb + r : inter + j0 + 8 * nb + (r - 8);
+    load_w(wf[nb], w + wr * K + 8 * g, k0);
+  }
   bf16x8_v xf[MBS][NSTEP];
 #pragma unroll
   for (int mb = 0; mb < MBS; ++mb) {
@@ -785,40 +789,55 @@ __global__ void __launch_bounds__(NCH * 64) linear_silu_kernel(const bf16_t* __r
   // Every load is issued before the first MFMA (one memory latency per workgroup; left to
   // itself the compiler interleaves loads and MFMAs and waits on each group).
   __builtin_amdgcn_sched_barrier(0);
-  f32x4_v acc[MBS];
+  f32x4_v acc[NB][MBS];
 #pragma unroll
-  for (int mb = 0; mb < MBS; ++mb) acc[mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb) acc[nb][mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) {
 #pragma unroll
-    for (int mb = 0; mb < MBS; ++mb)
-      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[mb][s], wf[s], acc[mb], 0, 0, 0);
+    for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+      for (int mb = 0; mb < MBS; ++mb)
+        acc[nb][mb] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[mb][s], wf[nb][s], acc[nb][mb], 0, 0, 0);
+    }
   }
-  // Lane holds rows 16 mb + 4 g + i of column r.
+  // Lane holds rows 16 mb + 4 g + i of column block nb, column r.
 #pragma unroll
-  for (int mb = 0; mb < MBS; ++mb) {
+  for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sacc[wave][(16 * mb + 4 * g + i) * SS + r] = acc[mb][i];
+    for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sacc[wave][(16 * mb + 4 * g + i) * SS + 16 * nb + r] = acc[nb][mb][i];
+    }
   }
   __syncthreads();
-  // 64 rows x 8 outputs, two adjacent outputs per thread.
-  for (int o = threadIdx.x; o < MBS * 16 * 4; o += NCH * 64) {
-    const int row = o >> 2;
-    const int col = 2 * (o & 3);
+  // 64 rows x 8 NB outputs, two adjacent outputs per thread per pass.
+  for (int o = threadIdx.x; o < MBS * 16 * 4 * NB; o += NCH * 64) {
+    const int row = o / (4 * NB);
+    const int q = o % (4 * NB);
+    const int nb = q >> 2;
+    const int col = 2 * (q & 3);  // within the block's 8 gate columns
     if (row >= mrows) continue;
+    const int base = row * SS + 16 * nb + col;
     float y[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      float gs = sacc[0][row * SS + col + e];
-      float us = sacc[0][row * SS + 8 + col + e];
+      float gs = sacc[0][base + e];
+      float us = sacc[0][base + 8 + e];
 #pragma unroll
       for (int c = 1; c < NCH; ++c) {
-        gs += sacc[c][row * SS + col + e];
-        us += sacc[c][row * SS + 8 + col + e];
+        gs += sacc[c][base + e];
+        us += sacc[c][base + 8 + e];
       }
       y[e] = silu_mul1(round_bf16(gs), round_bf16(us));
     }
-    *reinterpret_cast<uint32_t*>(out + (m0 + row) * inter + j0 + col) = pack_bf16x2(y[0], y[1]);
+    *reinterpret_cast<uint32_t*>(out + (m0 + row) * inter + j0 + 8 * nb + col) =
+        pack_bf16x2(y[0], y[1]);
   }
 }
 
@@ -930,18 +949,30 @@ extern "C" int sid_linear_silu_mul(const void* x, const void* w, void* out, int6
   SID_REQUIRE((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(out) % 4 == 0,
               "linear_silu_mul: misaligned operand");
-  const dim3 grid((unsigned)(inter / 8), (unsigned)((m + MROWS - 1) / MROWS));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int mbs = m >= MROWS ? 4 : static_cast<int>((m + 15) / 16);
+  // Two column blocks per wave halve the x read per output (M = 64, I = 3072, weights from
+  // HBM: 12.3 -> 9.3 us); an I that is not a multiple of 16 takes one block per wave.
+  const int nb = inter % 16 == 0 ? 2 : 1;
+  const dim3 grid((unsigned)(inter / (8 * nb)), (unsigned)((m + MROWS - 1) / MROWS));
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(4 * 64), 0, s, (const bf16_t*)x, (const bf16_t*)w, m,
                        inter, (bf16_t*)out);
   };
-  switch (mbs) {
-    case 1: go(linear_silu_kernel<4, 1>); break;
-    case 2: go(linear_silu_kernel<4, 2>); break;
-    case 3: go(linear_silu_kernel<4, 3>); break;
-    default: go(linear_silu_kernel<4, 4>); break;
+  if (nb == 2) {
+    switch (mbs) {
+      case 1: go(linear_silu_kernel<4, 1, 2>); break;
+      case 2: go(linear_silu_kernel<4, 2, 2>); break;
+      case 3: go(linear_silu_kernel<4, 3, 2>); break;
+      default: go(linear_silu_kernel<4, 4, 2>); break;
+    }
+  } else {
+    switch (mbs) {
+      case 1: go(linear_silu_kernel<4, 1, 1>); break;
+      case 2: go(linear_silu_kernel<4, 2, 1>); break;
+      case 3: go(linear_silu_kernel<4, 3, 1>); break;
+      default: go(linear_silu_kernel<4, 4, 1>); break;
+    }
   }
   return check_launch("linear_silu_mul");
 }

@@ -62,11 +62,12 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor,
 
 
 # Rows up to which the fused gate_up + SwiGLU kernel replaces linear_partials +
-# silu_mul_partials. Every workgroup reads its rows' whole x (K = 1024) for 8 output
-# columns, 4x the x traffic of the split-K kernel, so the saved launch and partial round trip
-# win only for small batches (MI355X, gate_up 6144 x 1024, weights from HBM, graph-timed:
-# M=1 7.95 -> 5.54 us, M=32 9.94 -> 8.78, M=64 12.56 -> 12.29; M=128 16.1 -> 17.0 slower).
-LINEAR_SILU_MAX_ROWS = 64
+# silu_mul_partials. Every workgroup reads its rows' whole x (K = 1024) for 16 output
+# columns, twice the x traffic of the split-K kernel per weight byte, against which it saves
+# a launch and the fp32 partials' round trip (MI355X, gate_up 6144 x 1024, weights from HBM,
+# graph-timed pair -> fused: M=1 8.0 -> 5.2 us, M=32 9.9 -> 6.8, M=64 12.5 -> 9.3,
+# M=128 16.0 -> 14.6, M=192 19.3 -> 19.8).
+LINEAR_SILU_MAX_ROWS = 128
 
 
 def linear_silu_mul_preferred(m: int, k: int) -> bool:
