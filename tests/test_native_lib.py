@@ -62,6 +62,14 @@ def test_validation_errors_without_device_work(ext):
     assert rc == 1 and b"multiple of 64" in lib.sid_last_error()
     rc = lib.sid_reshape_and_cache(1, 1, 1, 1, 1, 4, 1, 3, 10, None)
     assert rc == 1 and b"16-byte" in lib.sid_last_error()
+    # gate_up + SwiGLU: K fixed at 1024, I a multiple of 8, 16-byte aligned operands
+    rc = lib.sid_linear_silu_mul(16, 16, 16, 4, 2048, 3072, None)
+    assert rc == 1 and b"K must be 1024" in lib.sid_last_error()
+    rc = lib.sid_linear_silu_mul(16, 16, 16, 4, 1024, 3074, None)
+    assert rc == 1 and b"multiple of 8" in lib.sid_last_error()
+    rc = lib.sid_linear_silu_mul(8, 16, 16, 4, 1024, 3072, None)
+    assert rc == 1 and b"misaligned" in lib.sid_last_error()
+    assert lib.sid_linear_silu_mul(None, None, None, 0, 1024, 3072, None) == 0
     # empty work is a successful no-op
     assert lib.sid_reshape_and_cache(None, None, None, None, None, 0, 8, 128, 10, None) == 0
     assert lib.sid_flash_decode_fwd(None, None, None, None, None, None, 0, 16, 8, 128, 10, 1, 0, f,
