@@ -220,8 +220,12 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
       }
       l[h] = l[h] * rs + psum;
       m[h] = mn;
+      // x * 1.0f == x: once the running maxima settle, no lane of the wave rescales, and the
+      // 16 multiplies are skipped with identical bits.
+      if (__builtin_amdgcn_ballot_w64(rs != 1.0f) != 0) {
 #pragma unroll
-      for (int d = 0; d < 16; ++d) acc[h][d] *= rs;
+        for (int d = 0; d < 16; ++d) acc[h][d] *= rs;
+      }
 #pragma unroll
       for (int t = 0; t < TPL; ++t) {
         float vf[16];
