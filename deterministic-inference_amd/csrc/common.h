@@ -55,6 +55,15 @@ __device__ __forceinline__ float silu_mul1(float g, float u) {
   return s * u;
 }
 
+// Two finite fp32 values to packed bf16 (round to nearest even) with the hardware
+// conversion (v_cvt_pk_bf16_f32): no NaN test, so no branch; for finite inputs the bits are
+// pack_bf16x2's.
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2_finite(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_hw{lo, hi}), bf16x2_hw));
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
