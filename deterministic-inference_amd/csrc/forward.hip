@@ -15,6 +15,18 @@ namespace {
 // bits as the split-K pair; faster up to here on MI355X, slower beyond).
 constexpr int64_t kLinearSiluMaxRows = 128;
 
+// Whether a projection of t rows and n output columns takes the split-K path (the same bits
+// either way). Narrow outputs (n <= 2048: o, down) have few output tiles, so split-K keeps
+// the chip busy up to 4x `wide_max` rows; n <= 4096 (qkv) up to `wide_max`; wider ones
+// (gate_up) below `wide_max`, where the tiled direct GEMM takes over. (MI355X, fused consumers included: down at 512 rows 21.2 us
+// split vs 34.9 direct, o 18.6 vs 24.8; qkv at 384 rows 13.7 vs 13.2; gate_up at 256 rows
+// 21.6 vs 17.2.)
+bool split_for(int64_t t, int64_t n, int64_t wide_max) {
+  if (n <= 2048) return t <= 4 * wide_max;
+  if (n <= 4096) return t <= wide_max;
+  return t < wide_max;
+}
+
 constexpr int64_t kAlign = 256;
 // Greedy rows up to this count take the lm_head with the fused argmax (one streaming pass
 // over the weights, no logits); more rows go through fp32 logits (tiled GEMM) + argmax.
@@ -53,17 +65,19 @@ Layout plan(const sid_qwen3_model* m, const sid_extend_batch* b, void* ws) {
   const int64_t wq = static_cast<int64_t>(m->num_q_heads + 2 * m->num_kv_heads) * m->head_dim;
   const int64_t ao = static_cast<int64_t>(m->num_q_heads) * m->head_dim;
   const int64_t inter = m->intermediate;
-  const bool split = t <= m->split_k_max_tokens;
   const int64_t r = b->sample_indices ? b->num_samples : t;
   Carver c{static_cast<char*>(ws), 0, 0};
   Layout l{};
   l.resid = c.take(t * h * 2);
   l.x = c.take(t * h * 2);
+  // One buffer for the largest projection output: fp32 chunk partials [K/256][t][n] on the
+  // split-K path, bf16 [t][n] on the direct one (o and down write straight into x).
   int64_t proj = 0;
-  if (split) {
-    proj = std::max({h / 256 * wq, ao / 256 * h, h / 256 * 2 * inter, inter / 256 * h}) * t * 4;
-  } else {
-    proj = std::max(wq, 2 * inter) * t * 2;
+  const int64_t shapes[4][2] = {{wq, h}, {h, ao}, {2 * inter, h}, {h, inter}};  // {n, k}
+  for (const auto& nk : shapes) {
+    const int64_t need = split_for(t, nk[0], m->split_k_max_tokens) ? nk[1] / 256 * nk[0] * t * 4
+                                                                      : nk[0] * t * 2;
+    proj = std::max(proj, need);
   }
   l.proj = c.take(proj);
   l.q = c.take(t * ao * 2);
@@ -127,7 +141,11 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
   const int64_t ao = static_cast<int64_t>(hq) * d;
   const int64_t inter = m->intermediate;
   const float eps = m->rms_eps;
-  const bool split = t <= m->split_k_max_tokens;
+  const int64_t smax = m->split_k_max_tokens;
+  const bool split_qkv = split_for(t, wq, smax);
+  const bool split_o = split_for(t, h, smax);
+  const bool split_gu = split_for(t, 2 * inter, smax);
+  const bool split_down = split_for(t, h, smax);
   float* part = static_cast<float*>(l.proj);
   const int kvmax = static_cast<int>(b->max_kv_len > 0 ? b->max_kv_len : b->num_kv_indices);
 
@@ -137,7 +155,7 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
   for (int i = 0; i < m->num_layers; ++i) {
     const sid_qwen3_layer& lw = m->layers[i];
     // qkv projection -> q/k-norm, RoPE, KV-cache write
-    if (split) {
+    if (split_qkv) {
       SID_TRY(sid_linear_partials(l.x, h, lw.qkv, part, t, wq, h, stream));
       SID_TRY(sid_qkv_post(nullptr, part, h / 256, t, hq, hkv, d, lw.q_norm, lw.k_norm, eps,
                            b->positions, m->cos_sin, m->max_positions, b->out_slots, l.q,
@@ -153,7 +171,7 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
                                      std::max(b->max_extend_len, 1), kvmax, m->sm_scale,
                                      l.ext_ws, l.ext_ws_bytes, l.attn, stream));
     // o projection; residual += o; x = rmsnorm(residual, post_ln)
-    if (split) {
+    if (split_o) {
       SID_TRY(sid_linear_partials(l.attn, ao, lw.o, part, t, h, ao, stream));
       SID_TRY(sid_fused_add_rmsnorm_partials(part, static_cast<int>(ao / 256), l.resid,
                                              lw.post_ln, l.x, t, h, eps, stream));
@@ -164,7 +182,7 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
     // act = silu(gate) * up (one launch for up to kLinearSiluMaxRows rows)
     if (t <= kLinearSiluMaxRows && h == 1024) {
       SID_TRY(sid_linear_silu_mul(l.x, lw.gate_up, l.act, t, h, inter, stream));
-    } else if (split) {
+    } else if (split_gu) {
       SID_TRY(sid_linear_partials(l.x, h, lw.gate_up, part, t, 2 * inter, h, stream));
       SID_TRY(sid_silu_mul_partials(part, h / 256, l.act, t, inter, stream));
     } else {
@@ -173,7 +191,7 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
     }
     // down projection; residual += down; x = rmsnorm(residual, next input_ln / final norm)
     const void* next_w = i + 1 < m->num_layers ? m->layers[i + 1].input_ln : m->final_norm;
-    if (split) {
+    if (split_down) {
       SID_TRY(sid_linear_partials(l.act, inter, lw.down, part, t, h, inter, stream));
       SID_TRY(sid_fused_add_rmsnorm_partials(part, static_cast<int>(inter / 256), l.resid,
                                              next_w, l.x, t, h, eps, stream));

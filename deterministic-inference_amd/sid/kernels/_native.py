@@ -46,7 +46,7 @@ _SIGNATURES = {
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
             "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes",
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward", *_SIGNATURES)
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 def _check(cond: bool, msg: str) -> None:

@@ -24,10 +24,23 @@ from sid.kernels.rmsnorm import fused_add_rmsnorm, rmsnorm
 from sid.kernels.rope import RotaryEmbedding
 
 
-# Token counts up to this (decode batches, the 4 x 32 DVR verify pass) use split-K
-# projections whose chunk partials are folded by the consuming fused kernel; larger ones
-# (prefill) use direct GEMMs. Both give identical bits.
+# Split-K projections (chunk partials folded by the consuming fused kernel) or direct GEMMs:
+# both give identical bits, so this is a speed choice per projection shape. Outputs of
+# N <= 2048 columns (o, down: few output tiles) split up to 4 x SPLIT_K_MAX_TOKENS rows,
+# N <= 4096 (qkv) up to SPLIT_K_MAX_TOKENS, wider ones (gate_up) below it (at and above it
+# the tiled direct GEMM is faster). The native executor applies the same rule
+# (sid_qwen3_model.split_k_max_tokens). MI355X, consumers included: down at 512 rows 21.2 us
+# split vs 34.9 direct, o 18.6 vs 24.8; qkv at 384 rows 13.7 vs 13.2; gate_up at 256 rows
+# 21.6 vs 17.2.
 SPLIT_K_MAX_TOKENS = 256
+
+
+def split_k_preferred(rows: int, n: int, wide_max: int = SPLIT_K_MAX_TOKENS) -> bool:
+    if n <= 2048:
+        return rows <= 4 * wide_max
+    if n <= 4096:
+        return rows <= wide_max
+    return rows < wide_max
 
 
 class Qwen3Model:
@@ -87,25 +100,30 @@ class Qwen3Model:
         eps = cfg.rms_norm_eps
         layers = self.w["layers"]
         t = fb.input_ids.shape[0]
-        split = t <= SPLIT_K_MAX_TOKENS
+        h = cfg.hidden_size
+        split_qkv = split_k_preferred(t, cfg.q_size + 2 * cfg.kv_size)
+        split_o = split_k_preferred(t, h)
+        split_gu = split_k_preferred(t, 2 * cfg.intermediate_size)
+        split_down = split_k_preferred(t, h)
         decode_attn.reset_plan()
         residual = embedding(fb.input_ids, self.w["embed"])
         x = rmsnorm(residual, layers[0]["input_ln"], eps)
         for i in range(cfg.num_layers):
             lw = layers[i]
-            o = self._attention(i, x, fb, kv_cache, decode_attn, decode_backend, split)
-            if split:
+            o = self._attention(i, x, fb, kv_cache, decode_attn, decode_backend, split_qkv)
+            if split_o:
                 x, residual = fused_add_rmsnorm_partials(linear_partials(o, lw["o"]), residual,
                                                          lw["post_ln"], eps)
-                if linear_silu_mul_preferred(t, x.shape[1]):
-                    act = linear_silu_mul(x, lw["gate_up"])
-                else:
-                    act = silu_mul_partials(linear_partials(x, lw["gate_up"]))
             else:
                 x, residual = fused_add_rmsnorm(linear(o, lw["o"]), residual, lw["post_ln"], eps)
+            if linear_silu_mul_preferred(t, x.shape[1]):
+                act = linear_silu_mul(x, lw["gate_up"])
+            elif split_gu:
+                act = silu_mul_partials(linear_partials(x, lw["gate_up"]))
+            else:
                 act = silu_mul(linear(x, lw["gate_up"]))
             next_w = layers[i + 1]["input_ln"] if i + 1 < cfg.num_layers else self.w["norm"]
-            if split:
+            if split_down:
                 x, residual = fused_add_rmsnorm_partials(linear_partials(act, lw["down"]),
                                                          residual, next_w, eps)
             else:

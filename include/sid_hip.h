@@ -279,7 +279,9 @@ int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bia
  * down projection + residual add + RMSNorm; then the sampled rows' lm_head).
  * Results are bit-identical to issuing the same entry points one by one. It
  * has no counterpart of its own in the reference, whose forward is Python.
- * Projections of <= split_k_max_tokens tokens use the split-K path. Outputs:
+ * A projection with N <= 2048 output columns uses the split-K path up to
+ * 4 * split_k_max_tokens tokens, N <= 4096 up to split_k_max_tokens, wider ones
+ * below split_k_max_tokens (the results are the same either way). Outputs:
  * logits fp32 [R, vocab] and/or greedy_tokens int64 [R] (R = num_samples, or
  * num_tokens without sample_indices; greedy without logits needs R <= 64).
  */

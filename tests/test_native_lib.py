@@ -40,7 +40,7 @@ def test_python_binding_matches_header(ext):
 
 
 def test_abi_version(ext):
-    assert ext.lib.sid_abi_version() == 10
+    assert ext.lib.sid_abi_version() == 11
 
 
 def test_validation_errors_without_device_work(ext):
