@@ -13,6 +13,7 @@ from the request->token table by one kernel.
 from __future__ import annotations
 
 import enum
+import itertools
 from dataclasses import dataclass
 from typing import Optional
 
@@ -95,8 +96,13 @@ class DecodeStatic:
 
 
 def _sampling_host(reqs, repeat: int = 1):
-    f = np.array([r.samp_f for r in reqs], dtype=np.float32).reshape(-1, 2)
-    i = np.array([r.samp_i for r in reqs], dtype=np.int64).reshape(-1, 2)
+    """(temperatures, top_ks, top_ps, seeds) of the requests, each repeated `repeat` times.
+    (One flat fromiter per dtype: half the host time of building arrays from the tuples.)"""
+    n = len(reqs)
+    f = np.fromiter(itertools.chain.from_iterable(r.samp_f for r in reqs), dtype=np.float32,
+                    count=2 * n).reshape(-1, 2)
+    i = np.fromiter(itertools.chain.from_iterable(r.samp_i for r in reqs), dtype=np.int64,
+                    count=2 * n).reshape(-1, 2)
     if repeat != 1:
         f = np.repeat(f, repeat, axis=0)
         i = np.repeat(i, repeat, axis=0)
