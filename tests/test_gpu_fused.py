@@ -57,7 +57,8 @@ def test_qkv_post_matches_unfused(t, use_partials):
     assert torch.equal(kc1, kc0) and torch.equal(vc1, vc0)
 
 
-@pytest.mark.parametrize("t,k", [(1, 2048), (64, 2048), (33, 3072)])
+@pytest.mark.parametrize("t,k", [(1, 2048), (64, 2048), (33, 3072), (300, 3072), (1024, 2048),
+                                 (1024, 3072)])
 def test_fused_add_rmsnorm_partials_matches_unfused(t, k):
     from sid.kernels.matmul_persistent import linear, linear_partials
     from sid.kernels.ops import fused_add_rmsnorm_partials

@@ -62,7 +62,8 @@ def test_strided_input_rows():
 
 @pytest.mark.parametrize("m,n,k", [(64, 4096, 1024), (64, 1024, 2048), (64, 6144, 1024),
                                    (64, 1024, 3072), (5, 1024, 3072), (1, 4096, 1024),
-                                   (100, 1024, 2048)])
+                                   (100, 1024, 2048), (512, 1024, 2048), (1024, 1024, 3072),
+                                   (300, 4096, 1024)])
 def test_partials_fold_equals_linear(m, n, k):
     """Chunk partials folded in increasing chunk order and rounded to bf16 equal sid_linear
     bit for bit (the contract the *_partials consumers rely on)."""
