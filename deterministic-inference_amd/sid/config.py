@@ -96,6 +96,11 @@ class EngineConfig:
 
     decode_backend: str = "hip"  # "hip" split-KV kernel | "extend" (extend kernel, debugging)
     use_graphs: bool = True  # replay decode / verify forwards as HIP graphs
+    # nondet / batch_invariant with graphs: launch decode step N+1 before step N's tokens are
+    # read back (N+1 takes them on the device), so the host's per-step work overlaps the GPU.
+    # A request that stops on EOS at step N has its row of N+1 discarded. Tokens do not
+    # change (batch_invariant: bit for bit); False: one synchronous step at a time.
+    overlap_decode: bool = True
 
     device: str = "cuda"
     seed: int = 0  # random-init weight seed

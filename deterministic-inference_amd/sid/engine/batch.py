@@ -76,7 +76,7 @@ class DecodeStatic:
 
     def __init__(self, max_bs: int, kv_capacity: int, device):
         self.max_bs = max_bs
-        n64, n32, nf = 7 * max_bs, 2 * max_bs + 1, 2 * max_bs
+        n64, n32, nf = 8 * max_bs, 2 * max_bs + 1, 2 * max_bs
         o32 = 8 * n64
         of = o32 + 4 * (n32 + (n32 & 1))  # keep the fp32 block 8-byte aligned
         nbytes = of + 4 * nf
@@ -84,7 +84,7 @@ class DecodeStatic:
         self.dev = torch.zeros(nbytes, dtype=torch.uint8, device=device)
 
         def views(buf):
-            return (buf[:o32].view(torch.int64).view(7, max_bs),
+            return (buf[:o32].view(torch.int64).view(8, max_bs),
                     buf[o32:o32 + 4 * n32].view(torch.int32),
                     buf[of:].view(torch.float32).view(2, max_bs))
 
@@ -150,6 +150,13 @@ def build_prefill_batch(reqs: list, kv, device: str, invariant: bool) -> Forward
     )
 
 
+def gather_prev_tokens(static: DecodeStatic, bs: int, prev_tokens: torch.Tensor) -> None:
+    """Input ids of a batch built with prev_rows: ids[i] = prev_tokens[prev_rows[i]], on the
+    stream, after the batch's host->device copy (so the in-flight step that produces
+    prev_tokens has finished when it runs)."""
+    torch.index_select(prev_tokens, 0, static.i64[7, :bs], out=static.i64[0, :bs])
+
+
 def batch_bucket(bs: int, max_bs: int) -> int:
     """Padded decode batch size of a graph: 1, 2, 4, 8, then steps of 8 up to 64, of 16 up
     to 128, of 32 beyond (at most max_bs). Padding rows are empty requests."""
@@ -165,20 +172,31 @@ def batch_bucket(bs: int, max_bs: int) -> int:
 
 def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
                        static: Optional[DecodeStatic] = None,
-                       pad_to: Optional[int] = None) -> ForwardBatch:
+                       pad_to: Optional[int] = None,
+                       prev_rows: Optional[np.ndarray] = None) -> ForwardBatch:
     """One new token per request; attention covers the full sequence including the
     position being written now. With `static`, the batch lives in its fixed buffers and
     may be padded to `pad_to` rows: padding rows are empty requests (sequence length 0,
     table row -1, KV slot -1, greedy), whose attention output is zero and whose tokens the
-    caller ignores; real rows' results do not depend on them."""
+    caller ignores; real rows' results do not depend on them.
+
+    prev_rows (static only): every request has one more token than its output_ids hold,
+    sampled by a step still in flight, at that step's row prev_rows[i]; the batch feeds it
+    (positions one further on) and the caller gathers the token ids on the device
+    (`gather_prev_tokens`) after this returns."""
     bs = len(reqs)
     if not all(r.output_ids for r in reqs):
         bad = next(r for r in reqs if not r.output_ids)
         raise AssertionError(f"req {bad.rid}: decode step before any output token")
+    pending = 0 if prev_rows is None else 1
     # position of the fed token = kv_len = prompt_len + num_output - 1 (request.py)
-    pos = np.fromiter((len(r.prompt_ids) + len(r.output_ids) - 1 for r in reqs),
+    pos = np.fromiter((len(r.prompt_ids) + len(r.output_ids) - 1 + pending for r in reqs),
                       dtype=np.int64, count=bs)
-    ids = np.fromiter((r.output_ids[-1] for r in reqs), dtype=np.int64, count=bs)
+    if pending:
+        assert static is not None, "a pending token needs the graph-static buffers"
+        ids = np.full(bs, DUMMY_TOKEN_ID, dtype=np.int64)  # replaced on the device
+    else:
+        ids = np.fromiter((r.output_ids[-1] for r in reqs), dtype=np.int64, count=bs)
     rows = np.fromiter((r.req_row for r in reqs), dtype=np.int64, count=bs)
     new_slots = kv.alloc(bs).numpy()
     kv.req_to_token[torch.from_numpy(rows), torch.from_numpy(pos)] = \
@@ -206,6 +224,8 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         for i, a in enumerate((ids, pos, rows, new_slots, seq_lens, top_ks, seeds)):
             h64[i, :bs] = a
             h64[i, bs:n] = pad64[i]
+        if pending:
+            h64[7, :bs] = prev_rows
         h32 = static.h32
         h32[:bs + 1] = indptr
         h32[bs + 1:n + 1] = indptr[-1]

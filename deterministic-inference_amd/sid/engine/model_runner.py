@@ -14,7 +14,7 @@ import torch
 
 from sid.config import EngineConfig, Mode, ModelConfig
 from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_bucket,
-                              build_decode_batch)
+                              build_decode_batch, gather_prev_tokens)
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
 from sid.kernels.decode_attention import DecodeAttention
@@ -98,13 +98,20 @@ class ModelRunner:
             return self.forward(fb, greedy=True)
         return self.sample(fb, self.forward(fb))
 
-    def prepare_decode(self, reqs: list, invariant: bool) -> ForwardBatch:
-        """build_decode_batch, into the graph-static buffers when graphs are enabled."""
+    def prepare_decode(self, reqs: list, invariant: bool, prev_rows=None,
+                       prev_tokens: torch.Tensor | None = None) -> ForwardBatch:
+        """build_decode_batch, into the graph-static buffers when graphs are enabled. With
+        prev_rows / prev_tokens (graphs only), each request's newest token is still in
+        flight: row prev_rows[i] of prev_tokens, gathered on the device."""
         if self.graphs is None:
+            assert prev_rows is None, "a pending token needs graphs"
             return build_decode_batch(reqs, self.kv_cache, self.device, invariant)
-        pad = batch_bucket(len(reqs), self.graphs.decode_static.max_bs)
+        static = self.graphs.decode_static
+        pad = batch_bucket(len(reqs), static.max_bs)
         fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant,
-                                static=self.graphs.decode_static, pad_to=pad)
+                                static=static, pad_to=pad, prev_rows=prev_rows)
+        if prev_rows is not None:
+            gather_prev_tokens(static, len(reqs), prev_tokens)
         # The attention grid depends on the longest request (fixed-256 splits, or the
         # segment count of the heuristic splits): bucket it so a graph serves a range.
         bucket = seq_bucket(fb.max_seq_len)

@@ -1,0 +1,72 @@
+"""Overlapped decode (EngineConfig.overlap_decode): step N+1 is launched before step N's
+tokens are read back, taking them on the device. In batch_invariant mode the tokens must
+equal the synchronous engine's bit for bit, including requests that stop on a stop token
+mid-stream (their row of the step already in flight is discarded), under a decode batch
+limit that forces admissions (which drain the pipeline), with greedy and seeded sampling;
+every KV slot must come back. nondet mode: same lengths and slot accounting."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from sid.config import EngineConfig, Mode, SamplingParams
+from sid.engine.engine import Engine
+
+pytestmark = pytest.mark.gpu
+
+
+def _engine(mode, overlap, max_batch=6):
+    cfg = EngineConfig(mode=mode, kv_pool_tokens=32768, max_reqs=32, max_seq_len=2048,
+                       max_decode_batch=max_batch, num_layers=4, seed=7,
+                       overlap_decode=overlap)
+    return Engine(cfg)
+
+
+def _prompts(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randint(0, 151936, (int(torch.randint(8, 90, (1,), generator=g)),),
+                          generator=g).tolist() for _ in range(n)]
+
+
+def _params(n, temperature, stops=None, ignore_eos=True):
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(5, 40, (n,), generator=g).tolist()
+    return [SamplingParams(max_new_tokens=lens[i], temperature=temperature, seed=100 + i,
+                           ignore_eos=ignore_eos,
+                           stop_token_ids=[] if stops is None else [stops[i]])
+            for i in range(n)]
+
+
+def _run(mode, overlap, prompts, params, max_batch=6):
+    eng = _engine(mode, overlap, max_batch)
+    free0 = eng.kv.free_count
+    outs = eng.generate(prompts, params)
+    assert eng._inflight is None
+    assert eng.kv.free_count == free0, "KV slots leaked"
+    return [o.token_ids for o in outs], [o.finish_reason for o in outs]
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.7])
+def test_overlap_matches_synchronous_batch_invariant(temperature):
+    prompts = _prompts(14, 11)
+    print(f"overlap batch_invariant T={temperature}", flush=True)
+    base, _ = _run(Mode.BATCH_INVARIANT, False, prompts, _params(14, temperature))
+    # stop tokens that occur mid-stream: each request's 4th token (or none for short ones)
+    stops = [t[3] if len(t) > 6 else 151935 for t in base]
+    params = _params(14, temperature, stops, ignore_eos=False)
+    a, ra = _run(Mode.BATCH_INVARIANT, False, prompts, params)
+    b, rb = _run(Mode.BATCH_INVARIANT, True, prompts, params)
+    assert a == b and ra == rb
+    assert "stop" in ra and "length" in ra  # both finish kinds exercised
+    c, _ = _run(Mode.BATCH_INVARIANT, True, prompts, _params(14, temperature))
+    assert c == base
+
+
+def test_overlap_nondet_lengths_and_slots():
+    prompts = _prompts(10, 12)
+    print("overlap nondet", flush=True)
+    params = _params(10, 0.7)
+    toks, reasons = _run(Mode.NONDET, True, prompts, params, max_batch=4)
+    assert [len(t) for t in toks] == [p.max_new_tokens for p in params]
+    assert set(reasons) == {"length"}
