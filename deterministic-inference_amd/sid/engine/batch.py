@@ -150,11 +150,18 @@ def build_prefill_batch(reqs: list, kv, device: str, invariant: bool) -> Forward
     )
 
 
-def gather_prev_tokens(static: DecodeStatic, bs: int, prev_tokens: torch.Tensor) -> None:
-    """Input ids of a batch built with prev_rows: ids[i] = prev_tokens[prev_rows[i]], on the
-    stream, after the batch's host->device copy (so the in-flight step that produces
-    prev_tokens has finished when it runs)."""
-    torch.index_select(prev_tokens, 0, static.i64[7, :bs], out=static.i64[0, :bs])
+def gather_prev_tokens(static: DecodeStatic, prev_rows: np.ndarray,
+                       prev_tokens: torch.Tensor) -> None:
+    """Input ids of a batch built with prev_rows: ids[i] = prev_tokens[prev_rows[i]] where
+    prev_rows[i] >= 0, on the stream after the batch's host->device copy (so the in-flight
+    step that produces prev_tokens has finished when it runs)."""
+    bs = len(prev_rows)
+    rows, ids = static.i64[7, :bs], static.i64[0, :bs]
+    if (prev_rows >= 0).all():
+        torch.index_select(prev_tokens, 0, rows, out=ids)
+    else:
+        got = torch.index_select(prev_tokens, 0, rows.clamp(min=0))
+        ids.copy_(torch.where(rows >= 0, got, ids))
 
 
 def batch_bucket(bs: int, max_bs: int) -> int:
@@ -180,23 +187,24 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
     table row -1, KV slot -1, greedy), whose attention output is zero and whose tokens the
     caller ignores; real rows' results do not depend on them.
 
-    prev_rows (static only): every request has one more token than its output_ids hold,
-    sampled by a step still in flight, at that step's row prev_rows[i]; the batch feeds it
-    (positions one further on) and the caller gathers the token ids on the device
-    (`gather_prev_tokens`) after this returns."""
+    prev_rows (static only): prev_rows[i] >= 0 means request i has one more token than its
+    output_ids hold, sampled by a step still in flight at that step's row prev_rows[i]; the
+    batch feeds it (position one further on) and the caller gathers it on the device
+    (`gather_prev_tokens`) after this returns. prev_rows[i] < 0: the newest token is in
+    output_ids, as without prev_rows."""
     bs = len(reqs)
     if not all(r.output_ids for r in reqs):
         bad = next(r for r in reqs if not r.output_ids)
         raise AssertionError(f"req {bad.rid}: decode step before any output token")
-    pending = 0 if prev_rows is None else 1
     # position of the fed token = kv_len = prompt_len + num_output - 1 (request.py)
-    pos = np.fromiter((len(r.prompt_ids) + len(r.output_ids) - 1 + pending for r in reqs),
+    pos = np.fromiter((len(r.prompt_ids) + len(r.output_ids) - 1 for r in reqs),
                       dtype=np.int64, count=bs)
-    if pending:
+    ids = np.fromiter((r.output_ids[-1] for r in reqs), dtype=np.int64, count=bs)
+    if prev_rows is not None:
         assert static is not None, "a pending token needs the graph-static buffers"
-        ids = np.full(bs, DUMMY_TOKEN_ID, dtype=np.int64)  # replaced on the device
-    else:
-        ids = np.fromiter((r.output_ids[-1] for r in reqs), dtype=np.int64, count=bs)
+        pending = prev_rows >= 0
+        pos += pending  # the in-flight token sits one position further on
+        ids[pending] = DUMMY_TOKEN_ID  # replaced on the device
     rows = np.fromiter((r.req_row for r in reqs), dtype=np.int64, count=bs)
     new_slots = kv.alloc(bs).numpy()
     kv.req_to_token[torch.from_numpy(rows), torch.from_numpy(pos)] = \
@@ -224,7 +232,7 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         for i, a in enumerate((ids, pos, rows, new_slots, seq_lens, top_ks, seeds)):
             h64[i, :bs] = a
             h64[i, bs:n] = pad64[i]
-        if pending:
+        if prev_rows is not None:
             h64[7, :bs] = prev_rows
         h32 = static.h32
         h32[:bs + 1] = indptr

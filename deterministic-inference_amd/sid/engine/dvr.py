@@ -197,6 +197,7 @@ class Verifier:
                 r.output_ids = r.output_ids[:v + j] + [got[j]]
                 r.verified_len = v + j + 1
                 r.num_rollbacks += 1
+                r.epoch += 1
                 r.tokens_rolled_back += old_len - (v + j)
                 start = r.prompt_len + r.verified_len - 1
                 end = r.prompt_len + old_len - 1

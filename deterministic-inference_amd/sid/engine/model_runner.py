@@ -104,14 +104,14 @@ class ModelRunner:
         prev_rows / prev_tokens (graphs only), each request's newest token is still in
         flight: row prev_rows[i] of prev_tokens, gathered on the device."""
         if self.graphs is None:
-            assert prev_rows is None, "a pending token needs graphs"
+            assert prev_rows is None or not (prev_rows >= 0).any(), "a pending token needs graphs"
             return build_decode_batch(reqs, self.kv_cache, self.device, invariant)
         static = self.graphs.decode_static
         pad = batch_bucket(len(reqs), static.max_bs)
         fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant,
                                 static=static, pad_to=pad, prev_rows=prev_rows)
-        if prev_rows is not None:
-            gather_prev_tokens(static, len(reqs), prev_tokens)
+        if prev_rows is not None and (prev_rows >= 0).any():
+            gather_prev_tokens(static, prev_rows, prev_tokens)
         # The attention grid depends on the longest request (fixed-256 splits, or the
         # segment count of the heuristic splits): bucket it so a graph serves a range.
         bucket = seq_bucket(fb.max_seq_len)

@@ -42,6 +42,9 @@ class Request:
         self.num_rollbacks = 0
         self.tokens_rolled_back = 0
         self.stream_offset = 0
+        # bumped whenever a rollback rewrites output_ids: a decode row launched before the
+        # bump (overlapped decode) is stale and is discarded
+        self.epoch = 0
 
     @property
     def prompt_len(self) -> int:

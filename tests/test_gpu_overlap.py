@@ -70,3 +70,31 @@ def test_overlap_nondet_lengths_and_slots():
     toks, reasons = _run(Mode.NONDET, True, prompts, params, max_batch=4)
     assert [len(t) for t in toks] == [p.max_new_tokens for p in params]
     assert set(reasons) == {"length"}
+
+
+def test_overlap_dvr_deterministic_tokens_unchanged():
+    """dvr: verify passes run beside the overlapped decode; rollbacks arrive while the next
+    step is in flight (its rows for rolled-back requests are discarded). The deterministic
+    requests' tokens equal the synchronous engine's; every slot comes back."""
+    prompts = _prompts(16, 13)
+    print("overlap dvr", flush=True)
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(20, 90, (16,), generator=g).tolist()
+    params = [SamplingParams(max_new_tokens=lens[i], temperature=0.7 if i % 3 else 0.0,
+                             seed=7 + i, is_deterministic=i % 2 == 0, ignore_eos=True)
+              for i in range(16)]
+
+    def run(overlap):
+        eng = _engine(Mode.DVR, overlap, max_batch=8)
+        free0 = eng.kv.free_count
+        outs = eng.generate(prompts, params)
+        assert eng._inflight is None
+        assert eng.kv.free_count == free0, "KV slots leaked"
+        return outs
+
+    a, b = run(False), run(True)
+    for i, (x, y) in enumerate(zip(a, b)):
+        assert len(y.token_ids) == params[i].max_new_tokens
+        if params[i].is_deterministic:
+            assert x.token_ids == y.token_ids, f"request {i}"
+    assert sum(o.num_rollbacks for o in b) > 0  # the rollback path ran
