@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--attn-reps", type=int, default=4)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (launch every kernel)")
+    ap.add_argument("--sync-steps", action="store_true",
+                    help="time one synchronous step at a time (no overlapped launch)")
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5],
                     help="BASELINE config: 3 (default) = full decode step; 1 = decode attention op; "
                          "2 = cache write + decode attention at B=32; 4 = DVR verify pass; "
@@ -104,14 +106,53 @@ class DecodeWorkload:
         return toks
 
 
-def time_steps(wl, steps, warmup):
+def time_steps(wl, steps, warmup, pipelined=True):
+    """Seconds per decode step. pipelined: step k+1 is launched before step k's tokens are
+    read back and its slots released, as the engine's overlapped decode runs
+    (EngineConfig.overlap_decode); every step still feeds the same positions, so each does
+    identical work. Otherwise one synchronous step at a time."""
     torch = wl.torch
-    for _ in range(warmup):
-        wl.step()
+    if not pipelined:
+        for _ in range(warmup):
+            wl.step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            wl.step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+    host = [torch.empty(len(wl.reqs), dtype=torch.int64, pin_memory=True) for _ in range(2)]
+    turn = [0]
+
+    def launch():
+        fb = wl.build()
+        tok = wl.runner.step(fb)
+        h = host[turn[0]]
+        turn[0] ^= 1
+        h.copy_(tok, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        return fb, h, ev
+
+    def finish(step):
+        fb, h, ev = step
+        ev.synchronize()
+        toks = h.tolist()
+        wl.kv.free(torch.from_numpy(fb.new_slots_host))  # roll back: same positions next time
+        return toks
+
+    def run(n):
+        prev = launch()
+        for _ in range(n - 1):
+            nxt = launch()
+            finish(prev)
+            prev = nxt
+        finish(prev)
+
+    run(max(warmup, 1))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        wl.step()
+    run(steps)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / steps
 
@@ -290,7 +331,7 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    sec = time_steps(wl, args.steps, args.warmup)
+    sec = time_steps(wl, args.steps, args.warmup, pipelined=not (args.sync_steps or args.eager))
     roof = attention_roofline(wl, args.attn_reps)
     gemms = gemm_report(wl)
     base = None if args.no_cpu_baseline else cpu_baseline(wl)
@@ -303,7 +344,8 @@ def main():
         "data": "synthetic: random-init weights ~N(0,0.02), random token ids, N(0,1) KV prefixes",
         "config": {"workload": f"Qwen3-0.6B-shape decode step, batch {b}, context "
                                f"{args.context}+1, greedy, {args.mode} split policy, "
-                               f"{'eager launches' if args.eager else 'HIP graph replay'}",
+                               f"{'eager launches' if args.eager else 'HIP graph replay'}"
+                               f"{'' if (args.sync_steps or args.eager) else ', next step launched before the readback (overlapped decode)'}",
                    "batch": b, "context": args.context, "layers": wl.runner.mcfg.num_layers,
                    "mode": args.mode},
         "roofline": roof,
