@@ -70,7 +70,7 @@ def test_engine_step_api_and_release():
     rid = eng.add_request(prompt_ids=_prompts(1, 5)[0],
                           params=SamplingParams(max_new_tokens=40, is_deterministic=True,
                                                 ignore_eos=True))
-    while eng.scheduler.has_work():
+    while eng.has_work():
         eng.step()
     out = eng.get_output(rid)
     assert out is not None and len(out.token_ids) == 40 and out.finish_reason == "length"

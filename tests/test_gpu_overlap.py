@@ -98,3 +98,22 @@ def test_overlap_dvr_deterministic_tokens_unchanged():
         if params[i].is_deterministic:
             assert x.token_ids == y.token_ids, f"request {i}"
     assert sum(o.num_rollbacks for o in b) > 0  # the rollback path ran
+
+
+def test_overlap_manual_step_loop_returns_every_slot():
+    """Driving step() by hand until Engine.has_work() is False applies the last launched
+    step too (its rows may belong only to requests that already stopped on EOS)."""
+    prompts = _prompts(8, 14)
+    print("overlap manual step loop", flush=True)
+    base, _ = _run(Mode.BATCH_INVARIANT, False, prompts, _params(8, 0.0))
+    stops = [t[2] if len(t) > 4 else 151935 for t in base]
+    params = _params(8, 0.0, stops, ignore_eos=False)
+    want, _ = _run(Mode.BATCH_INVARIANT, False, prompts, params)
+    eng = _engine(Mode.BATCH_INVARIANT, True)
+    free0 = eng.kv.free_count
+    rids = [eng.add_request(prompt_ids=p, params=sp) for p, sp in zip(prompts, params)]
+    while eng.has_work():
+        eng.step()
+    got = [eng.get_output(r).token_ids for r in rids]
+    assert got == want
+    assert eng.kv.free_count == free0
