@@ -10,8 +10,13 @@ lm_head on the sampled rows, bf16 logits returned as fp32.
 
 Every intermediate that the GPU path stores as bf16 is rounded to bf16 here too, so the
 only differences left are accumulation orders (checked by tolerance and argmax agreement).
-Pinned by: each op's own oracle (tests/test_oracle.py) and the decode/extend identity —
-a decode step over L keys equals the last row of a one-token extend over the same keys.
+Pinned by (tests/test_oracle_qwen3.py): transformers' own Qwen3ForCausalLM, built from a
+Qwen3Config with the real head geometry and seeded weights (tests/golden/qwen3_hf_logits.pt,
+written by tests/golden/make_qwen3_fixtures.py): every prefill and decode row within the bf16
+noise of that model and with the same argmax, while swapped gate/up halves or swapped q/k-norm
+weights miss it by 10-100x; a decode step equals, bit for bit, a one-token extend over the
+same keys; the last prefill row equals a decode over the cached prefix. Each op is also
+pinned by its own oracle (tests/test_oracle.py).
 """
 
 from __future__ import annotations
