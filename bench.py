@@ -77,11 +77,8 @@ class DecodeWorkload:
         g = torch.Generator(device="cuda").manual_seed(seed + 1)
         for pool_t in kv.k_pools + kv.v_pools:
             pool_t.copy_(torch.randn(pool_t.shape, generator=g, device="cuda").to(pool_t.dtype))
-        # page-shuffled slot assignment (page size 16)
-        slots = kv.alloc(batch * context)
-        pages = slots.view(-1, 16)[torch.randperm(batch * context // 16,
-                                                  generator=torch.Generator().manual_seed(seed))]
-        slots = pages.reshape(batch, context)
+        # pages scattered over the pool (page size 16), as after a long run of requests
+        kv.scatter_free_pages(seed)
         vocab = self.runner.mcfg.vocab_size
         gen = torch.Generator().manual_seed(seed + 2)
         self.reqs = []
@@ -89,10 +86,12 @@ class DecodeWorkload:
             r = Request(i, torch.randint(0, vocab, (context,), generator=gen).tolist(),
                         SamplingParams(max_new_tokens=1 << 20, ignore_eos=True),
                         self.runner.mcfg.eos_token_ids)
-            r.req_row = kv.alloc_row()
-            kv.write_row(r.req_row, 0, slots[i])
+            r.req_row = kv.open_row()
+            kv.grow(r.req_row, context)
             r.output_ids.append(int(torch.randint(0, vocab, (1,), generator=gen)))
             self.reqs.append(r)
+        kv.sync_rows([r.req_row for r in self.reqs])
+        self.context = context
         self.invariant = self.cfg.mode == Mode.BATCH_INVARIANT
 
     def build(self):
@@ -101,9 +100,14 @@ class DecodeWorkload:
     def step(self):
         fb = self.build()
         toks = self.runner.step(fb).tolist()
-        # roll the state back: release this step's slots (LIFO: the next step reuses them)
-        self.kv.free(self.torch.from_numpy(fb.new_slots_host))
+        self.rollback()
         return toks
+
+    def rollback(self):
+        """Back to `context` positions per request: the page this step opened goes back to
+        the top of the free stack, so the next step takes the same one (identical work)."""
+        for r in self.reqs:
+            self.kv.shrink(r.req_row, self.context)
 
 
 def time_steps(wl, steps, warmup, pipelined=True):
@@ -138,7 +142,7 @@ def time_steps(wl, steps, warmup, pipelined=True):
         fb, h, ev = step
         ev.synchronize()
         toks = h.tolist()
-        wl.kv.free(torch.from_numpy(fb.new_slots_host))  # roll back: same positions next time
+        wl.rollback()  # same positions next time
         return toks
 
     def run(n):
@@ -192,7 +196,7 @@ def attention_roofline(wl, reps):
     bytes_launch = (rows * mcfg.num_kv_heads * mcfg.head_dim * 2 * 2   # K + V rows
                     + rows * 4                                           # kv_indices
                     + 2 * b * mcfg.num_q_heads * mcfg.head_dim * 2)      # q in, o out
-    wl.kv.free(torch.from_numpy(fb.new_slots_host))
+    wl.rollback()
     achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
@@ -244,7 +248,7 @@ def cpu_baseline(wl, min_seconds=10.0, max_reps=12):
              "out_slots": (indptr[1:] - 1).long(), "kv_indptr": indptr,
              "kv_indices": torch.arange(rows, dtype=torch.int32),
              "sample_indices": torch.arange(len(wl.reqs))}
-    wl.kv.free(torch.from_numpy(fb.new_slots_host))
+    wl.rollback()
 
     forward_ref(wc, mcfg, kp, vp, batch, layers=1)  # warm
     times = []

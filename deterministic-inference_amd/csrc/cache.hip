@@ -46,26 +46,35 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(
 }
 
 
-// Decode-batch construction on the device: request b owns row rows[b] of the
-// request->token table and has kv_indptr[b+1]-kv_indptr[b] = L positions, the
-// last of which is the token being decoded now. Writes that token's new slot
-// into the table and copies the row's first L slots into kv_indices.
-__global__ void __launch_bounds__(256) build_decode_indices_kernel(
-    int32_t* __restrict__ req_to_token, int64_t row_stride, int64_t num_rows,
+// Decode-batch construction on the device, over page tables. Request b owns
+// row rows[b] of the block table [num_rows, max_pages] (int32 page ids; a page
+// holds `page_size` = 1 << page_shift consecutive pool slots) and has
+// L = kv_indptr[b+1] - kv_indptr[b] positions, the last of which is the token
+// decoded now; its slot new_slots[b] was chosen on the host. Position i < L-1
+// lives in slot table[i >> shift] * page_size + (i & mask). When the new token
+// opens a page (position L-1 is a page's first), its page id enters the table
+// for later steps; no thread of this launch reads that entry (every earlier
+// position lies in an earlier page), so there is no intra-launch dependency.
+// Consecutive threads take consecutive positions: a wave reads one or a few
+// table entries (broadcast) and writes 256 contiguous bytes of kv_indices.
+__global__ void __launch_bounds__(256) build_paged_decode_indices_kernel(
+    int32_t* __restrict__ tables, int64_t max_pages, int64_t num_rows, int page_shift,
     const int64_t* __restrict__ rows, const int64_t* __restrict__ new_slots,
     const int32_t* __restrict__ kv_indptr, int32_t* __restrict__ kv_indices) {
   const int b = blockIdx.x;
   const int64_t row = rows[b];
   const int start = kv_indptr[b];
   const int len = kv_indptr[b + 1] - start;
-  if (row < 0 || row >= num_rows || len <= 0 || len > row_stride) return;
-  int32_t* table = req_to_token + row * row_stride;
-  const int32_t fresh = new_slots != nullptr ? static_cast<int32_t>(new_slots[b]) : table[len - 1];
-  const int body = len - 1;
-  for (int i = threadIdx.x; i < body; i += blockDim.x) kv_indices[start + i] = table[i];
+  if (row < 0 || row >= num_rows || len <= 0 || ((len - 1) >> page_shift) >= max_pages) return;
+  int32_t* table = tables + row * max_pages;
+  const int32_t mask = (1 << page_shift) - 1;
+  const int last = len - 1;
+  for (int i = threadIdx.x; i < last; i += blockDim.x)
+    kv_indices[start + i] = (table[i >> page_shift] << page_shift) | (i & mask);
   if (threadIdx.x == 0) {
-    kv_indices[start + body] = fresh;
-    if (new_slots != nullptr) table[body] = fresh;
+    const int32_t slot = static_cast<int32_t>(new_slots[b]);
+    kv_indices[start + last] = slot;
+    if ((last & mask) == 0) table[last >> page_shift] = slot >> page_shift;
   }
 }
 
@@ -118,17 +127,22 @@ extern "C" int sid_gather_rows(const void* table, const int64_t* idx, void* out,
   return check_launch("gather_rows");
 }
 
-extern "C" int sid_build_decode_indices(int32_t* req_to_token, int64_t row_stride, int64_t num_rows,
-                                        const int64_t* rows, const int64_t* new_slots,
-                                        const int32_t* kv_indptr, int32_t* kv_indices, int batch,
-                                        void* stream) {
-  SID_REQUIRE(batch >= 0, "build_decode_indices: negative batch");
+extern "C" int sid_build_paged_decode_indices(int32_t* block_tables, int64_t max_pages,
+                                              int64_t num_rows, int page_size,
+                                              const int64_t* rows, const int64_t* new_slots,
+                                              const int32_t* kv_indptr, int32_t* kv_indices,
+                                              int batch, void* stream) {
+  SID_REQUIRE(batch >= 0, "build_paged_decode_indices: negative batch");
   if (batch == 0) return SID_OK;
-  SID_REQUIRE(req_to_token && rows && kv_indptr && kv_indices,
-              "build_decode_indices: null pointer");
-  SID_REQUIRE(row_stride > 0 && num_rows > 0, "build_decode_indices: empty table");
-  hipLaunchKernelGGL(build_decode_indices_kernel, dim3(batch), dim3(256), 0,
-                     (hipStream_t)stream, req_to_token, row_stride, num_rows, rows, new_slots,
-                     kv_indptr, kv_indices);
-  return check_launch("build_decode_indices");
+  SID_REQUIRE(block_tables && rows && new_slots && kv_indptr && kv_indices,
+              "build_paged_decode_indices: null pointer");
+  SID_REQUIRE(max_pages > 0 && num_rows > 0, "build_paged_decode_indices: empty table");
+  SID_REQUIRE(page_size > 0 && (page_size & (page_size - 1)) == 0 && page_size <= (1 << 20),
+              "build_paged_decode_indices: page_size %d is not a power of two", page_size);
+  int shift = 0;
+  while ((1 << shift) < page_size) ++shift;
+  hipLaunchKernelGGL(build_paged_decode_indices_kernel, dim3(batch), dim3(256), 0,
+                     (hipStream_t)stream, block_tables, max_pages, num_rows, shift, rows,
+                     new_slots, kv_indptr, kv_indices);
+  return check_launch("build_paged_decode_indices");
 }

@@ -59,6 +59,10 @@ class EngineConfig:
     dtype: str = "bfloat16"
 
     kv_pool_tokens: int = 256 * 1024
+    # KV pages: a request holds whole pages of this many consecutive pool slots (a power of
+    # two; 1 = the reference's token-granular pool). Slot numbering, and so every kernel's
+    # view of the pool, is the same for any page size.
+    kv_page_size: int = 16
     max_reqs: int = 256
     max_seq_len: int = 32768
     max_prompt_len: int = 16384

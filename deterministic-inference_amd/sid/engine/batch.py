@@ -7,7 +7,7 @@ generates P+v+j. (A mismatch here would make every verify window fail at index 0
 
 Host work per decode step is O(B) Python plus one host->device copy (graph-static
 buffers; three without them); the kv_indices of the whole batch are built on the device
-from the request->token table by one kernel.
+from the requests' block tables by one kernel.
 """
 
 from __future__ import annotations
@@ -54,17 +54,17 @@ class ForwardBatch:
     all_greedy: Optional[bool] = None  # host-known: every row has temperature 0
     graph_key: Optional[tuple] = None  # set when the inputs live in graph-static buffers
     real_rows: Optional[int] = None    # rows of real requests when padded (decode graphs)
-    # decode batches in the graph-static buffers: build_decode_indices arguments, run at the
+    # decode batches in the graph-static buffers: build_paged_decode_indices arguments, run at the
     # start of the forward (inside the graph) instead of by the builder
     index_build: Optional[tuple] = None
-    new_slots_host: Optional[np.ndarray] = None  # decode: the KV slots taken by this step
+    new_slots_host: Optional[np.ndarray] = None  # decode: the KV slot each row writes
 
     def build_indices(self) -> None:
         """Enqueue the deferred kv_indices build (a no-op when the builder already ran it).
         The forward calls this first; a caller that reads kv_indices without a forward
         calls it itself."""
         if self.index_build is not None:
-            load_ext().build_decode_indices(*self.index_build)
+            load_ext().build_paged_decode_indices(*self.index_build)
 
 
 class DecodeStatic:
@@ -122,16 +122,17 @@ def _to_device(arrays: list, dtype, device) -> list:
 
 
 def build_prefill_batch(reqs: list, kv, device: str, invariant: bool) -> ForwardBatch:
-    """Allocates prompt slots; extend attention with prefix 0."""
+    """Takes pages for every prompt (block tables copied to the device); extend attention
+    with prefix 0."""
     ids, pos, slots, qo = [], [], [], [0]
     for r in reqs:
         p = r.prompt_len
-        s = kv.alloc(p)
-        kv.write_row(r.req_row, 0, s)
+        kv.grow(r.req_row, p)
         ids.append(np.asarray(r.prompt_ids, dtype=np.int64))
         pos.append(np.arange(p, dtype=np.int64))
-        slots.append(s.numpy())
+        slots.append(kv.slot_range(r.req_row, 0, p))
         qo.append(qo[-1] + p)
+    kv.sync_rows([r.req_row for r in reqs])
     temps, top_ks, top_ps, seeds = _sampling_host(reqs)
     qo_np = np.asarray(qo, dtype=np.int64)
     i64 = _to_device([np.concatenate(ids), np.concatenate(pos), np.concatenate(slots),
@@ -206,9 +207,7 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         pos += pending  # the in-flight token sits one position further on
         ids[pending] = DUMMY_TOKEN_ID  # replaced on the device
     rows = np.fromiter((r.req_row for r in reqs), dtype=np.int64, count=bs)
-    new_slots = kv.alloc(bs).numpy()
-    kv.req_to_token[torch.from_numpy(rows), torch.from_numpy(pos)] = \
-        torch.from_numpy(new_slots.astype(np.int32))
+    new_slots = kv.decode_slots(rows, pos)
     seq_lens = pos + 1
     indptr = np.zeros(bs + 1, dtype=np.int64)
     np.cumsum(seq_lens, out=indptr[1:])
@@ -221,7 +220,8 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         d_indptr, d_lens = _to_device([indptr, seq_lens], np.int32, device)
         d_temps, d_topp = _to_device([temps, top_ps], np.float32, device)
         kv_indices = torch.empty(total, dtype=torch.int32, device=device)
-        load_ext().build_decode_indices(kv.req_to_token_gpu, d_rows, d_slots, d_indptr, kv_indices)
+        load_ext().build_paged_decode_indices(kv.block_tables_gpu, kv.page_size, d_rows, d_slots,
+                                              d_indptr, kv_indices)
     else:
         n = bs if pad_to is None else pad_to
         assert bs <= n <= static.max_bs and total <= static.kv_indices.numel()
@@ -252,7 +252,7 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         kv_indices = static.kv_indices[:total]
         # Every argument lives at a fixed address, so the index build is part of the
         # forward (and of its captured graph): ModelRunner runs it first.
-        index_build = (kv.req_to_token_gpu, d_rows, d_slots, d_indptr, kv_indices)
+        index_build = (kv.block_tables_gpu, kv.page_size, d_rows, d_slots, d_indptr, kv_indices)
     return ForwardBatch(
         mode=ForwardMode.DECODE, input_ids=d_ids, positions=d_pos, out_slots=d_slots,
         kv_indptr=d_indptr, kv_indices=kv_indices, seq_lens=d_lens,

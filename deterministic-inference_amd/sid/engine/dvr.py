@@ -1,27 +1,38 @@
-"""Decode-verify-rollback (LLM-42 style), as sid/engine/dvr.py.
+"""Decode-verify-rollback: the verify pass and its commit rule (the role of sid/engine/dvr.py).
 
-A verify pass is S sequences x W extend tokens, padded with dummy sequences: S = G (the
-reference's fixed shape) or, with EngineConfig.dvr_verify_buckets, the next power of two
->= the ready sequences (at most G). Every kernel of the pass makes each row depend only on
-its own sequence (batch-invariant GEMMs and extend attention), so the verifier's tokens are
-a function of the request's history alone, whatever S is.
+A deterministic request decodes on the fast (batch-dependent) path; every W tokens, or
+when it finishes, its unverified tokens are recomputed by a verify pass whose result is a
+function of the request's history alone, and the tokens are committed up to the first
+disagreement.
 
-For a real request with prompt length P, verified_len v >= 1 and u = min(unverified, W)
-window tokens t[0..u-1] = output_ids[v:v+u]:
-  input row  = [output_ids[v-1], t[0], ..., t[u-2]] + [DUMMY] * (W - u)
-  positions  = P+v-1 .. P+v+u-2, padding rows repeat the last real position
-  prefix     = KV positions 0 .. P+v-2
-  out_slots  = the slots decode already wrote for P+v-1 .. P+v+u-2 (overwritten in
-               place), then scratch slots for the padding rows
-  prediction j is compared with t[j]; its sample position is P+v+j.
-At the first mismatch j the request keeps v+j tokens plus the verifier's token (at least
-one token of progress per pass) and frees the KV of everything after it.
+A pass is an extend batch of S sequences x W rows. For a real sequence with prompt length
+P, verified_len v >= 1 and a window of u = min(unverified, W) tokens output_ids[v:v+u]:
+  rows 0 .. u-1   feed output_ids[v-1 .. v+u-2] at positions P+v-1 .. P+v+u-2, and write
+                  their K/V over the slots decode wrote for those positions;
+  rows u .. W-1   padding: the DUMMY token at the last real position, K/V to scratch slots;
+  keys            positions 0 .. P+v-2 (its block table) followed by the W rows' slots;
+  row j predicts the token at position P+v+j (its sample position), compared with
+  output_ids[v+j].
+Dummy sequences (prefix 0, W DUMMY rows at positions 0 .. W-1, all on scratch slots) pad
+the pass to S sequences: S = G, the reference's fixed shape, or with
+EngineConfig.dvr_verify_buckets the next power of two >= the real sequences (at most G).
+Every kernel of the pass makes a row depend only on its own sequence (M-invariant GEMM rows,
+extend attention independent of the other sequences), so the verifier's tokens do not
+depend on S or on the other sequences.
+
+Commit rule, at the first index j where the verifier disagrees: keep v + j tokens, append
+the verifier's token (so a pass always commits at least one token) and give back the KV
+pages that only the discarded tokens used; with no disagreement, all u tokens are verified.
+
+The pass is built as arrays (numpy, one row per sequence or per verify row) and copied into
+the runner's persistent verify buffers, so its graph replays read fixed addresses.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from sid.config import DUMMY_TOKEN_ID, EngineConfig
@@ -29,36 +40,23 @@ from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.engine.request import Request
 
 
-def _bucket(n: int) -> int:
-    """Power-of-two bound (>= 512) of the longest verify sequence: the verify pass is
-    replayed as a graph per bucket, whose attention grid covers every sequence up to it."""
-    b = 512
-    while b < n:
-        b *= 2
-    return b
+def kv_bucket(n: int) -> int:
+    """Power-of-two bound (>= 512) of a pass's longest key list: one verify graph serves
+    every pass up to it (its attention grid covers that many keys)."""
+    return max(512, 1 << (int(n) - 1).bit_length())
 
 
-def _pow2_at_least(n: int, cap: int) -> int:
-    b = 1
-    while b < n:
-        b *= 2
-    return min(b, cap)
-
-
-class DummyPool:
-    """Scratch KV slots: G*W for dummy sequences, G*(W-1) for window padding."""
-
-    def __init__(self, kv, group_size: int, window_size: int):
-        self.dummy_slots = kv.alloc(group_size * window_size)
-        self.padding_slots = kv.alloc(group_size * (window_size - 1))
-        self.window_size = window_size
+def sequences_in_pass(ready: int, group: int, buckets: bool) -> int:
+    if not buckets:
+        return group
+    return min(group, 1 << (int(ready) - 1).bit_length())
 
 
 @dataclass
 class VerifyMeta:
     reqs: list
-    window_lens: list
-    windows: list
+    window_lens: list   # u per real sequence
+    windows: list       # the tokens each window checks: output_ids[v:v+u]
 
 
 class Verifier:
@@ -66,146 +64,138 @@ class Verifier:
         self.cfg = cfg
         self.runner = runner
         self.kv = kv
-        self.W = cfg.dvr_window_size
-        self.G = cfg.dvr_group_size
-        self.pool = DummyPool(kv, self.G, self.W)
+        self.W = W = cfg.dvr_window_size
+        self.G = G = cfg.dvr_group_size
+        # scratch K/V targets: row j >= 1 of real sequence i pads into pad[i, j - 1]; row j
+        # of dummy sequence d writes dummy[d, j]
+        scratch = kv.scratch_slots(G * W + G * (W - 1))
+        self.dummy_slots = scratch[:G * W].reshape(G, W)
+        self.pad_slots = scratch[G * W:].reshape(G, W - 1)
         buf = runner.verify_buffers
-        gw = self.G * self.W
         self.device = buf["qo_indptr"].device
-        buf["qo_indptr"].copy_(torch.arange(0, gw + 1, self.W, dtype=torch.int32))
-        self._sample_indices = torch.arange(gw, dtype=torch.int64, device=self.device)
+        buf["qo_indptr"].copy_(torch.arange(0, G * W + 1, W, dtype=torch.int32))
+        self._sample_rows = torch.arange(G * W, dtype=torch.int64, device=self.device)
 
-    @staticmethod
-    def ready(req: Request, window_size: int) -> bool:
-        if not req.params.is_deterministic or req.unverified() <= 0:
-            return False
-        return req.unverified() >= window_size or req.finished_reason is not None
+    # ---- which windows --------------------------------------------------------------------
+
+    def ready(self, req: Request) -> bool:
+        """A deterministic request has a window to verify: W unverified tokens, or any
+        once it has finished decoding."""
+        n = req.unverified()
+        return req.params.is_deterministic and n > 0 and (
+            n >= self.W or req.finished_reason is not None)
 
     def collect_ready(self, reqs: list) -> list:
-        """Ready requests in rid order, in groups of at most G; nothing while fewer than
-        dvr_min_verify are ready, unless one of them must be verified now (it finished
-        decoding, so only verification can release it, or it holds 2 W unverified tokens)."""
-        ready = sorted((r for r in reqs if self.ready(r, self.W)), key=lambda r: r.rid)
-        if len(ready) < self.cfg.dvr_min_verify and not any(
-                r.finished_reason is not None or r.unverified() >= 2 * self.W for r in ready):
+        """Ready requests in rid order, cut into passes of at most G. With
+        dvr_min_verify = m, nothing is returned while fewer than m are ready, unless one
+        of them cannot wait (it finished decoding, or it has 2 W unverified tokens)."""
+        ready = sorted((r for r in reqs if self.ready(r)), key=lambda r: r.rid)
+        urgent = any(r.finished_reason is not None or r.unverified() >= 2 * self.W
+                     for r in ready)
+        if len(ready) < self.cfg.dvr_min_verify and not urgent:
             return []
-        return [ready[i:i + self.G] for i in range(0, len(ready), self.G)]
+        return [ready[k:k + self.G] for k in range(0, len(ready), self.G)]
+
+    # ---- the pass ---------------------------------------------------------------------------
 
     def build_verify_batch(self, reqs: list) -> tuple:
-        assert 1 <= len(reqs) <= self.G
-        W, G, kv = self.W, self.G, self.kv
+        n, W = len(reqs), self.W
+        assert 1 <= n <= self.G, f"{n} sequences for a pass of at most {self.G}"
+        S = sequences_in_pass(n, self.G, self.cfg.dvr_verify_buckets)
+        j = np.arange(W, dtype=np.int64)
+
+        v = np.array([r.verified_len for r in reqs], dtype=np.int64)
+        assert (v >= 1).all(), "a request entered verify before its first token was committed"
+        u = np.minimum(np.array([r.unverified() for r in reqs], dtype=np.int64), W)
+        assert (u >= 1).all()
+        base = np.array([r.prompt_len for r in reqs], dtype=np.int64) + v - 1
+        kv_have = np.array([r.kv_len for r in reqs], dtype=np.int64)
+        assert (kv_have >= base + u).all(), "a window reaches past the KV decode wrote"
+
+        # per verify row [S, W]
+        tokens = np.full((S, W), DUMMY_TOKEN_ID, dtype=np.int64)
+        windows = []
+        for i, r in enumerate(reqs):
+            fed = r.output_ids[v[i] - 1:v[i] - 1 + u[i]]
+            tokens[i, :u[i]] = fed
+            windows.append(r.output_ids[v[i]:v[i] + u[i]])
+        positions = np.empty((S, W), dtype=np.int64)
+        positions[:n] = base[:, None] + np.minimum(j[None, :], u[:, None] - 1)
+        positions[n:] = j
+        sample_pos = np.empty((S, W), dtype=np.int64)
+        sample_pos[:n] = base[:, None] + 1 + j
+        sample_pos[n:] = j + 1
+        slots = np.empty((S, W), dtype=np.int64)
+        slots[:n, 1:] = self.pad_slots[:n]
+        for i, r in enumerate(reqs):
+            slots[i, :u[i]] = self.kv.slot_range(r.req_row, base[i], base[i] + u[i])
+        slots[n:] = self.dummy_slots[n:S]
+
+        # keys: each real sequence's prefix, then its W rows' slots; dummies: their rows
+        kv_lens = np.full(S, W, dtype=np.int64)
+        kv_lens[:n] += base
+        chunks = []
+        for i, r in enumerate(reqs):
+            chunks.append(self.kv.slot_range(r.req_row, 0, base[i]))
+            chunks.append(slots[i])
+        chunks.extend(slots[n:S])
+        kv_indices = np.concatenate(chunks)
+        kv_indptr = np.zeros(S + 1, dtype=np.int64)
+        np.cumsum(kv_lens, out=kv_indptr[1:])
+
+        # sampling parameters repeat per row; dummy rows are greedy
+        temps = np.zeros((S, W), dtype=np.float32)
+        top_p = np.ones((S, W), dtype=np.float32)
+        top_k = np.full((S, W), -1, dtype=np.int64)
+        seeds = np.zeros((S, W), dtype=np.int64)
+        for i, r in enumerate(reqs):
+            temps[i], top_p[i] = r.samp_f
+            top_k[i], seeds[i] = r.samp_i
+
+        rows = S * W
         buf = self.runner.verify_buffers
-        ids, positions, spos = [], [], []
-        out_slots, kv_lens, kv_chunks = [], [], []
-        temps, top_ks, top_ps, seeds = [], [], [], []
-        window_lens, windows = [], []
-        pad_used = 0
-
-        for r in reqs:
-            p, v = r.prompt_len, r.verified_len
-            assert v >= 1, f"req {r.rid} entered verify with verified_len 0"
-            u = min(r.unverified(), W)
-            assert u >= 1
-            window = r.output_ids[v:v + u]
-            window_lens.append(u)
-            windows.append(window)
-
-            ids.extend([r.output_ids[v - 1]] + window[:-1] + [DUMMY_TOKEN_ID] * (W - u))
-            positions.extend(range(p + v - 1, p + v - 1 + u))
-            positions.extend([p + v + u - 2] * (W - u))
-            spos.extend(range(p + v, p + v + W))
-
-            prefix_len = p + v - 1
-            end = prefix_len + u
-            assert r.kv_len >= end, (
-                f"req {r.rid}: window needs KV through position {end - 1}, only {r.kv_len} valid")
-            real = kv.req_to_token[r.req_row, prefix_len:end].to(torch.int64)
-            pad = W - u
-            if pad:
-                slots = torch.cat([real, self.pool.padding_slots[pad_used:pad_used + pad]])
-                pad_used += pad
-            else:
-                slots = real
-            out_slots.append(slots)
-            kv_lens.append(prefix_len + W)
-            kv_chunks.append(torch.cat([kv.req_to_token[r.req_row, :prefix_len].to(torch.int32),
-                                        slots.to(torch.int32)]))
-            temps.extend([r.params.temperature] * W)
-            top_ks.extend([r.params.top_k if r.params.top_k > 0 else -1] * W)
-            top_ps.extend([r.params.top_p] * W)
-            seeds.extend([r.params.seed] * W)
-
-        # Sequences in this pass: G (the reference's fixed shape) or, with bucketed shapes,
-        # the next power of two >= len(reqs); dummy sequences fill the rest.
-        n_pad = _pow2_at_least(len(reqs), G) if self.cfg.dvr_verify_buckets else G
-        rows = n_pad * W
-        for d in range(len(reqs), n_pad):
-            dummy = self.pool.dummy_slots[d * W:(d + 1) * W]
-            ids.extend([DUMMY_TOKEN_ID] * W)
-            positions.extend(range(W))
-            spos.extend(range(1, W + 1))
-            out_slots.append(dummy)
-            kv_lens.append(W)
-            kv_chunks.append(dummy.to(torch.int32))
-            temps.extend([0.0] * W)
-            top_ks.extend([-1] * W)
-            top_ps.extend([1.0] * W)
-            seeds.extend([0] * W)
-
-        v = {k: t[:rows] for k, t in buf.items()
-             if k in ("input_ids", "positions", "out_slots", "sample_positions", "temperatures",
-                      "top_ks", "top_ps", "seeds")}
-        v["input_ids"].copy_(torch.tensor(ids, dtype=torch.int64))
-        v["positions"].copy_(torch.tensor(positions, dtype=torch.int64))
-        v["out_slots"].copy_(torch.cat(out_slots).to(torch.int64))
-        v["sample_positions"].copy_(torch.tensor(spos, dtype=torch.int64))
-        v["temperatures"].copy_(torch.tensor(temps, dtype=torch.float32))
-        v["top_ks"].copy_(torch.tensor(top_ks, dtype=torch.int64))
-        v["top_ps"].copy_(torch.tensor(top_ps, dtype=torch.float32))
-        v["seeds"].copy_(torch.tensor(seeds, dtype=torch.int64))
-        total_kv = sum(kv_lens)
-        buf["kv_indices"][:total_kv].copy_(torch.cat(kv_chunks))
-        indptr = torch.zeros(n_pad + 1, dtype=torch.int64)
-        indptr[1:] = torch.cumsum(torch.tensor(kv_lens, dtype=torch.int64), dim=0)
-        kv_indptr = buf["kv_indptr"][:n_pad + 1]
-        kv_indptr.copy_(indptr.to(torch.int32))
+        dev = {}
+        for name, arr in (("input_ids", tokens), ("positions", positions), ("out_slots", slots),
+                          ("sample_positions", sample_pos), ("temperatures", temps),
+                          ("top_ks", top_k), ("top_ps", top_p), ("seeds", seeds)):
+            dst = buf[name][:rows]
+            dst.copy_(torch.from_numpy(arr.reshape(-1)).to(dst.dtype))
+            dev[name] = dst
+        total = int(kv_indptr[-1])
+        buf["kv_indices"][:total].copy_(torch.from_numpy(kv_indices.astype(np.int32)))
+        buf["kv_indptr"][:S + 1].copy_(torch.from_numpy(kv_indptr.astype(np.int32)))
 
         fb = ForwardBatch(
-            mode=ForwardMode.VERIFY,
-            input_ids=v["input_ids"], positions=v["positions"], out_slots=v["out_slots"],
-            qo_indptr=buf["qo_indptr"][:n_pad + 1], kv_indptr=kv_indptr,
-            kv_indices=buf["kv_indices"][:total_kv], max_extend_len=W,
-            max_kv_len=_bucket(max(kv_lens)),
-            sample_indices=self._sample_indices[:rows], sample_positions=v["sample_positions"],
-            temperatures=v["temperatures"], top_ks=v["top_ks"], top_ps=v["top_ps"],
-            seeds=v["seeds"], invariant=True, all_greedy=all(t == 0 for t in temps),
+            mode=ForwardMode.VERIFY, input_ids=dev["input_ids"], positions=dev["positions"],
+            out_slots=dev["out_slots"], qo_indptr=buf["qo_indptr"][:S + 1],
+            kv_indptr=buf["kv_indptr"][:S + 1], kv_indices=buf["kv_indices"][:total],
+            max_extend_len=W, max_kv_len=kv_bucket(int(kv_lens.max())),
+            sample_indices=self._sample_rows[:rows], sample_positions=dev["sample_positions"],
+            temperatures=dev["temperatures"], top_ks=dev["top_ks"], top_ps=dev["top_ps"],
+            seeds=dev["seeds"], invariant=True, all_greedy=bool((temps == 0).all()),
         )
-        return fb, VerifyMeta(reqs=list(reqs), window_lens=window_lens, windows=windows)
+        return fb, VerifyMeta(reqs=list(reqs), window_lens=u.tolist(), windows=windows)
+
+    # ---- commit ----------------------------------------------------------------------------
 
     def compare_and_rollback(self, meta: VerifyMeta, verify_tokens: torch.Tensor) -> None:
         W = self.W
-        tokens = verify_tokens.tolist()
+        got = verify_tokens.reshape(-1)[:len(meta.reqs) * W].view(-1, W).cpu().numpy()
         for i, r in enumerate(meta.reqs):
             u = meta.window_lens[i]
-            window = meta.windows[i]
-            got = tokens[i * W:i * W + u]
-            j = next((idx for idx in range(u) if got[idx] != window[idx]), u)
+            differ = np.flatnonzero(got[i, :u] != np.asarray(meta.windows[i], dtype=np.int64))
             r.num_windows += 1
-            v = r.verified_len
-            if j < u:
-                old_len = r.num_output
-                r.output_ids = r.output_ids[:v + j] + [got[j]]
-                r.verified_len = v + j + 1
+            if differ.size == 0:
+                r.verified_len += u
+            else:
+                keep = r.verified_len + int(differ[0])
+                r.tokens_rolled_back += r.num_output - keep
+                del r.output_ids[keep:]
+                r.output_ids.append(int(got[i, differ[0]]))
+                r.verified_len = keep + 1
                 r.num_rollbacks += 1
                 r.epoch += 1
-                r.tokens_rolled_back += old_len - (v + j)
-                start = r.prompt_len + r.verified_len - 1
-                end = r.prompt_len + old_len - 1
-                if end > start:
-                    self.kv.free(self.kv.req_to_token[r.req_row, start:end])
-                r.finished_reason = None
+                self.kv.shrink(r.req_row, r.kv_len)
                 r.check_finished()
-            else:
-                r.verified_len = v + u
             r.assert_invariants(dvr_mode=True)
             assert r.kv_len == r.prompt_len + r.num_output - 1

@@ -36,7 +36,7 @@ _SIGNATURES = {
     "sid_linear_silu_mul": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
-    "sid_build_decode_indices": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
+    "sid_build_paged_decode_indices": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _vp],
     "sid_flash_decode_segments_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
                                       _i32, _i32, _i32, _i32, _f32, _vp, _vp, _i32, _i32, _vp,
                                       _vp],
@@ -358,16 +358,17 @@ class NativeLib:
                    top_ks.data_ptr(), top_ps.data_ptr(), seeds.data_ptr(), positions.data_ptr(),
                    r, v, ws.data_ptr(), ws.numel(), out.data_ptr(), _stream(logits))
 
-    def build_decode_indices(self, req_to_token, rows, new_slots, kv_indptr, kv_indices) -> None:
-        _gpu(req_to_token, "req_to_token", torch.int32)
+    def build_paged_decode_indices(self, block_tables, page_size: int, rows, new_slots,
+                                   kv_indptr, kv_indices) -> None:
+        _gpu(block_tables, "block_tables", torch.int32)
+        _check(block_tables.dim() == 2, "block_tables must be [rows, max_pages]")
         _gpu(rows, "rows", torch.int64)
-        if new_slots is not None:
-            _gpu(new_slots, "new_slots", torch.int64)
-            _check(new_slots.numel() == rows.numel(), "new_slots must have B entries")
+        _gpu(new_slots, "new_slots", torch.int64)
+        _check(new_slots.numel() == rows.numel(), "new_slots must have B entries")
         _gpu(kv_indptr, "kv_indptr", torch.int32)
         _gpu(kv_indices, "kv_indices", torch.int32)
         _check(kv_indptr.numel() == rows.numel() + 1, "kv_indptr must have B+1 entries")
-        self._call("sid_build_decode_indices", req_to_token.data_ptr(), req_to_token.shape[1],
-                   req_to_token.shape[0], rows.data_ptr(),
-                   new_slots.data_ptr() if new_slots is not None else None,
-                   kv_indptr.data_ptr(), kv_indices.data_ptr(), rows.numel(), _stream(rows))
+        self._call("sid_build_paged_decode_indices", block_tables.data_ptr(),
+                   block_tables.shape[1], block_tables.shape[0], int(page_size), rows.data_ptr(),
+                   new_slots.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                   rows.numel(), _stream(rows))

@@ -349,18 +349,24 @@ int sid_argmax_rows(const float* logits, int64_t ld, int64_t* out, int64_t rows,
                     void* stream);
 
 /*
- * Device-side decode batch construction. For request b (row rows[b] of the
- * int32 request->token table [num_rows, row_stride], L_b = kv_indptr[b+1] -
- * kv_indptr[b] positions, the last one being decoded now): if new_slots
- * (int64 [B]) is non-NULL, table[row][L_b - 1] = new_slots[b]; then
- * kv_indices[kv_indptr[b] + i] = table[row][i] for i < L_b. Rows outside the
- * table or L_b > row_stride are skipped. Replaces the per-request host loop of
- * build_decode_batch, sid/engine/batch.py:120-133.
+ * Device-side decode batch construction over page tables. Request b sits on
+ * row rows[b] of the int32 block table [num_rows, max_pages] (page ids; page p
+ * holds pool slots p*page_size .. p*page_size + page_size - 1, page_size a
+ * power of two) and has L_b = kv_indptr[b+1] - kv_indptr[b] positions, the
+ * last one being decoded now into slot new_slots[b] (int64 [B], chosen by the
+ * host allocator). Writes kv_indices[kv_indptr[b] + i] =
+ * table[row][i / page_size] * page_size + i % page_size for i < L_b - 1, and
+ * new_slots[b] for i = L_b - 1; when that position opens a page
+ * ((L_b - 1) % page_size == 0), stores its page id into the table for later
+ * steps. Rows outside the table, L_b <= 0 or L_b beyond max_pages pages are
+ * skipped. Replaces the per-request host loop of build_decode_batch
+ * (sid/engine/batch.py:120-133) over the reference's token table
+ * (sid/engine/kv_cache.py:45-47), which is the page_size 1 case.
  */
-int sid_build_decode_indices(int32_t* req_to_token, int64_t row_stride, int64_t num_rows,
-                             const int64_t* rows, const int64_t* new_slots,
-                             const int32_t* kv_indptr, int32_t* kv_indices, int batch,
-                             void* stream);
+int sid_build_paged_decode_indices(int32_t* block_tables, int64_t max_pages, int64_t num_rows,
+                                   int page_size, const int64_t* rows, const int64_t* new_slots,
+                                   const int32_t* kv_indptr, int32_t* kv_indices, int batch,
+                                   void* stream);
 
 #ifdef __cplusplus
 }

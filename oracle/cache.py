@@ -10,7 +10,10 @@ block_table_to_indices  expands a page_size-16 block table into token slots,
                         page layout over the reference's token-granular pool,
                         sid/engine/kv_cache.py:1-12). Pinned by a brute-force loop.
 decode_indices_ref      restates build_decode_batch's kv_indptr / kv_indices construction,
-                        sid/engine/batch.py:110-154. Pinned by a brute-force loop.
+                        sid/engine/batch.py:110-154, over block tables: request b's keys are
+                        block_table_to_indices of its table row. page_size 1 is the
+                        reference's request -> token table (sid/engine/kv_cache.py:45-47).
+                        Pinned by a brute-force loop and by the page_size 1 special case.
 """
 
 from __future__ import annotations
@@ -33,10 +36,11 @@ def block_table_to_indices(block_table: np.ndarray, seq_len: int, page_size: int
     return (block_table[pos // page_size].astype(np.int64) * page_size + pos % page_size).astype(np.int32)
 
 
-def decode_indices_ref(req_to_token: np.ndarray, rows: list[int], seq_lens: list[int]):
-    """-> (kv_indptr int32 [B+1], kv_indices int32 [sum]) for requests on req_to_token rows."""
+def decode_indices_ref(block_tables: np.ndarray, rows: list[int], seq_lens: list[int],
+                       page_size: int = 1):
+    """-> (kv_indptr int32 [B+1], kv_indices int32 [sum]) for requests on block-table rows."""
     indptr = np.zeros(len(rows) + 1, dtype=np.int64)
     indptr[1:] = np.cumsum(seq_lens)
-    idx = np.concatenate([req_to_token[r, :L] for r, L in zip(rows, seq_lens)]) if rows else \
-        np.zeros(0, dtype=np.int32)
+    idx = np.concatenate([block_table_to_indices(block_tables[r], L, page_size)
+                          for r, L in zip(rows, seq_lens)]) if rows else np.zeros(0, np.int32)
     return indptr.astype(np.int32), idx.astype(np.int32)

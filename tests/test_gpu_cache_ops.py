@@ -86,23 +86,76 @@ def test_gather_rows_and_embedding():
     assert torch.equal(out[0], table[3]) and torch.count_nonzero(out[1:]) == 0
 
 
-def test_build_decode_indices_vs_oracle():
+@pytest.mark.parametrize("page_size", [1, 16])
+def test_build_paged_decode_indices_vs_oracle(page_size):
+    """Bit-exact vs the block-table expansion; a request whose new token opens a page gets
+    that page recorded in its table row, and no other table entry changes."""
     rng = np.random.default_rng(4)
-    r2t = rng.integers(1, 10 ** 6, size=(8, 300)).astype(np.int32)
-    rows = [3, 1, 6]
-    lens = [5, 300, 1]
-    new = [777, 888, 999]
-    r2t_after = r2t.copy()
-    for r, L, s in zip(rows, lens, new):
-        r2t_after[r, L - 1] = s
-    want_ptr, want_idx = decode_indices_ref(r2t_after, rows, lens)
-    dev = torch.from_numpy(r2t).cuda()
+    rows_n, max_pages = 8, 300 // page_size + 2
+    tables = rng.integers(1, 5000, size=(rows_n, max_pages)).astype(np.int32)
+    rows = [3, 1, 6, 2]
+    lens = [5, 300, 1, 2 * page_size + 1]
+    # new token slots: position L-1 of each request; a page-opening position gets a fresh page
+    after = tables.copy()
+    new = []
+    for r, L in zip(rows, lens):
+        pos = L - 1
+        if pos % page_size == 0:
+            page = 9000 + r
+            after[r, pos // page_size] = page
+        else:
+            page = tables[r, pos // page_size]
+        new.append(page * page_size + pos % page_size)
+    want_ptr, want_idx = decode_indices_ref(after, rows, lens, page_size)
+    dev = torch.from_numpy(tables).cuda()
     ptr = torch.from_numpy(want_ptr).cuda()
     out = torch.full((int(want_ptr[-1]),), -7, dtype=torch.int32, device="cuda")
-    _ext().build_decode_indices(dev, torch.tensor(rows, device="cuda"),
-                                torch.tensor(new, device="cuda"), ptr, out)
+    _ext().build_paged_decode_indices(dev, page_size, torch.tensor(rows, device="cuda"),
+                                      torch.tensor(new, device="cuda"), ptr, out)
     assert out.cpu().numpy().tolist() == want_idx.tolist()
-    assert (dev.cpu().numpy() == r2t_after).all()
+    assert (dev.cpu().numpy() == after).all()
+
+
+def test_paged_kv_cache_decode_matches_block_tables():
+    """The engine's page allocator + device index build over several decode steps with a
+    rollback in between: every step's kv_indices equal the host block tables' expansion
+    (oracle), and a rollback returns exactly the pages that became empty."""
+    from sid.config import EngineConfig, ModelConfig
+    from sid.engine.batch import build_decode_batch
+    from sid.engine.kv_cache import KVCache
+    from sid.engine.request import Request
+    from sid.config import SamplingParams
+    cfg = EngineConfig(kv_pool_tokens=64 * 16, max_reqs=8, max_seq_len=256, kv_page_size=16)
+    kv = KVCache(cfg, ModelConfig(num_layers=1), "cuda")
+    kv.scatter_free_pages(3)
+    reqs = []
+    for i, (p, n) in enumerate([(15, 1), (16, 1), (40, 3)]):
+        r = Request(i, list(range(p)), SamplingParams(max_new_tokens=100), (0,))
+        r.req_row = kv.open_row()
+        kv.grow(r.req_row, p + n - 1)
+        r.output_ids = [5] * n
+        reqs.append(r)
+    kv.sync_rows([r.req_row for r in reqs])
+    free0 = kv.free_pages
+    for step in range(40):
+        fb = build_decode_batch(reqs, kv, "cuda", invariant=False)
+        lens = [r.kv_len + 1 for r in reqs]
+        want_ptr, want_idx = decode_indices_ref(kv.tables, [r.req_row for r in reqs], lens, 16)
+        assert fb.kv_indices.cpu().numpy().tolist() == want_idx.tolist(), step
+        assert fb.out_slots.cpu().tolist() == [int(want_idx[e - 1]) for e in want_ptr[1:]]
+        for r in reqs:
+            r.output_ids.append(7)
+        if step == 25:  # roll request 2 back by 20 tokens
+            r = reqs[2]
+            del r.output_ids[-20:]
+            before = int(kv.held[r.req_row])
+            kv.shrink(r.req_row, r.kv_len)
+            assert kv.held[r.req_row] == kv.pages_for(r.kv_len) < before
+    assert kv.free_pages == free0 - sum(kv.pages_for(r.kv_len) - kv.pages_for(p + n - 1)
+                                        for r, (p, n) in zip(reqs, [(15, 1), (16, 1), (40, 3)]))
+    for r in reqs:
+        kv.close_row(r.req_row)
+    assert kv.free_pages == kv.num_pages - 1
 
 
 def test_argmax_first_index_and_nan():

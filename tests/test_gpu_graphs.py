@@ -26,7 +26,7 @@ def _requests(runner, lens, seed=0):
     for rid, p in enumerate(lens):
         r = Request(rid, torch.randint(0, 151936, (p,), generator=g).tolist(),
                     SamplingParams(max_new_tokens=64), runner.mcfg.eos_token_ids)
-        r.req_row = runner.kv_cache.alloc_row()
+        r.req_row = runner.kv_cache.open_row()
         reqs.append(r)
     return reqs
 

@@ -59,7 +59,7 @@ def test_prefill_then_decode_vs_oracle(layers):
     for rid, p in enumerate([17, 40, 5, 130]):
         r = Request(rid, torch.randint(0, mcfg.vocab_size, (p,), generator=g).tolist(),
                     SamplingParams(max_new_tokens=8), mcfg.eos_token_ids)
-        r.req_row = runner.kv_cache.alloc_row()
+        r.req_row = runner.kv_cache.open_row()
         reqs.append(r)
     kv = runner.kv_cache
 
@@ -106,7 +106,7 @@ def test_decode_backends_agree():
         for rid, p in enumerate([33, 64, 7]):
             r = Request(rid, torch.randint(0, 151936, (p,), generator=g).tolist(),
                         SamplingParams(max_new_tokens=8), runner.mcfg.eos_token_ids)
-            r.req_row = runner.kv_cache.alloc_row()
+            r.req_row = runner.kv_cache.open_row()
             reqs.append(r)
         fb = build_prefill_batch(reqs, runner.kv_cache, "cuda", invariant=False)
         for r, t in zip(reqs, runner.sample(fb, runner.forward(fb)).tolist()):

@@ -29,7 +29,7 @@ def _reqs(runner, lens, seed=0):
         r = Request(rid, torch.randint(0, 151936, (p,), generator=g).tolist(),
                     SamplingParams(max_new_tokens=40, is_deterministic=True, ignore_eos=True),
                     runner.mcfg.eos_token_ids)
-        r.req_row = runner.kv_cache.alloc_row()
+        r.req_row = runner.kv_cache.open_row()
         out.append(r)
     return out
 

@@ -220,7 +220,13 @@ def test_block_table_expansion_brute_force():
 
 
 def test_decode_indices_brute_force():
+    # page_size 1: the block table is the reference's request -> token table
     r2t = np.arange(40, dtype=np.int32).reshape(4, 10) * 3
     indptr, idx = C.decode_indices_ref(r2t, [2, 0], [3, 5])
     assert indptr.tolist() == [0, 3, 8]
     assert idx.tolist() == [60, 63, 66, 0, 3, 6, 9, 12]
+    # pages of 4 slots: row 1 holds pages 7, 2, 9
+    bt = np.zeros((3, 5), dtype=np.int32)
+    bt[1, :3] = [7, 2, 9]
+    indptr, idx = C.decode_indices_ref(bt, [1], [10], page_size=4)
+    assert idx.tolist() == [28, 29, 30, 31, 8, 9, 10, 11, 36, 37]

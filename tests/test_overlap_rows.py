@@ -24,7 +24,7 @@ def _next_rows(decode, inflight):
 
 def test_next_rows_continue_from_the_step_in_flight():
     a, b, c = _req(0, 3, 10), _req(1, 3, 10), _req(2, 9, 10)
-    step = _InFlight([a, b, c], [0, 0, 0], None, None, None, None)
+    step = _InFlight([a, b, c], [0, 0, 0], None, None, None)
     reqs, rows = _next_rows([a, b, c], step)
     # c's in-flight token is its 10th and last: it does not continue
     assert reqs == [a, b] and rows == [0, 1]
@@ -32,7 +32,7 @@ def test_next_rows_continue_from_the_step_in_flight():
 
 def test_next_rows_after_rollback_and_resume():
     a, b, c = _req(0, 3, 10), _req(1, 3, 10), _req(2, 4, 10)
-    step = _InFlight([a, b], [0, 0], None, None, None, None)
+    step = _InFlight([a, b], [0, 0], None, None, None)
     b.epoch = 1  # rolled back after the launch: its in-flight row is stale
     reqs, rows = _next_rows([a, b, c], step)  # c resumed (not in the step in flight)
     assert reqs == [a, b, c] and rows == [0, -1, -1]
@@ -40,7 +40,7 @@ def test_next_rows_after_rollback_and_resume():
 
 def test_next_rows_skip_stopped_requests():
     a, b = _req(0, 3, 10), _req(1, 3, 10)
-    step = _InFlight([a, b], [0, 0], None, None, None, None)
+    step = _InFlight([a, b], [0, 0], None, None, None)
     # b stopped on EOS at the previous step: the scheduler no longer lists it
     reqs, rows = _next_rows([a], step)
     assert reqs == [a] and rows == [0]
