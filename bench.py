@@ -227,7 +227,7 @@ def cpu_baseline(wl, min_seconds=10.0, max_reps=12):
     import torch
     from oracle.qwen3 import forward_ref
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = host_threads()
     torch.set_num_threads(threads)
     fb = wl.build()
     fb.build_indices()
@@ -258,11 +258,33 @@ def cpu_baseline(wl, min_seconds=10.0, max_reps=12):
         times.append(time.perf_counter() - t0)
     step = sum(times) / len(times)
     return {"value": round(len(wl.reqs) / step, 3), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
-            "sample": (f"oracle/qwen3.py forward_ref, whole {n_layers}-layer decode steps on the "
-                       f"same B={len(wl.reqs)} x ctx {rows // len(wl.reqs)} batch (fp32 "
-                       f"arithmetic on bf16 data), {len(times)} steps in {sum(times):.1f} s, "
-                       f"{step:.2f} s per step")}
+            "kind": "port", "host_cpus": os.cpu_count(), "cpu_model": cpu_model(),
+            "sample": (f"scaled run of oracle/qwen3.py forward_ref: whole {n_layers}-layer "
+                       f"decode steps on the same B={len(wl.reqs)} x ctx {rows // len(wl.reqs)} "
+                       f"batch (fp32 arithmetic on bf16 data), with 2 layers' weights and KV "
+                       f"copied to the host and reused by all {n_layers} layers (same "
+                       f"arithmetic, 1/14 of the host memory); {len(times)} steps in "
+                       f"{sum(times):.1f} s, {step:.2f} s per step, on {threads} threads "
+                       f"(every CPU this process may run on)")}
+
+
+def host_threads() -> int:
+    """CPUs this process may run on (its affinity mask: the box's CPU share), which is what
+    the CPU baseline uses; os.cpu_count() is reported beside it."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def gemm_report(wl, reps=50):

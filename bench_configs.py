@@ -92,7 +92,8 @@ def config1(args):
     idx, indptr = _paged(256, [1024], np.random.default_rng(1))
     res, attn, seq = _attn_case(q, k, v, indptr, idx, [1024])
     qc, kc, vc, ic, pc = q.cpu(), k.cpu(), v.cpu(), idx.cpu(), indptr.cpu()
-    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    from bench import cpu_model, host_threads
+    torch.set_num_threads(host_threads())
     t0 = time.perf_counter()
     n = 0
     while time.perf_counter() - t0 < 2.0:
@@ -105,7 +106,8 @@ def config1(args):
             "value": res["nondet"]["us_per_call"], "unit": "us", "higher_is_better": False,
             "policies": res, "max_abs_err_vs_oracle": err,
             "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us", "kind": "port",
-                             "cores": torch.get_num_threads(),
+                             "cores": torch.get_num_threads(), "host_cpus": os.cpu_count(),
+                             "cpu_model": cpu_model(),
                              "sample": "oracle.attention.decode_attention_ref, same inputs"},
             "note": "one request of 1024 tokens is launch/latency bound (4 MiB of K/V)"}
 

@@ -52,6 +52,8 @@ class ModelConfig:
 
 @dataclass
 class EngineConfig:
+    """Engine settings (the reference's fields, plus this build's schedule and paging knobs)."""
+
     # "random:<name>" builds a random-init Qwen3-0.6B-shape model (no download); a directory
     # path loads config.json + safetensors from disk.
     model_path: str = "random:qwen3-0.6b"
@@ -98,7 +100,9 @@ class EngineConfig:
     max_kv_splits: int = 32
     invariant_split_size: int = 256
 
-    decode_backend: str = "hip"  # "hip" split-KV kernel | "extend" (extend kernel, debugging)
+    # "cuda" (the reference's name) or "hip": the split-KV decode kernel; "triton" (the
+    # reference's name) or "extend": decode through the extend kernel (debugging)
+    decode_backend: str = "cuda"
     use_graphs: bool = True  # replay decode / verify forwards as HIP graphs
     # nondet / batch_invariant with graphs: launch decode step N+1 before step N's tokens are
     # read back (N+1 takes them on the device), so the host's per-step work overlaps the GPU.
@@ -110,6 +114,23 @@ class EngineConfig:
     seed: int = 0  # random-init weight seed
     num_layers: Optional[int] = None  # override (smaller random models for tests)
     vocab_size: Optional[int] = None
+
+    def __post_init__(self):
+        self.mode = Mode(self.mode)
+        self.decode_backend = decode_backend_kind(self.decode_backend)
+
+
+_DECODE_BACKENDS = {"cuda": "hip", "hip": "hip", "triton": "extend", "extend": "extend"}
+
+
+def decode_backend_kind(name: str) -> str:
+    """'hip' (split-KV decode kernel) or 'extend'; accepts the reference's 'cuda'/'triton'."""
+    try:
+        return _DECODE_BACKENDS[name]
+    except KeyError:
+        raise ValueError(f"unknown decode_backend {name!r}: use 'cuda' (or 'hip') for the "
+                         "split-KV decode kernel, 'triton' (or 'extend') for the extend "
+                         "kernel") from None
 
 
 @dataclass

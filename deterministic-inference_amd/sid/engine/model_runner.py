@@ -17,7 +17,7 @@ from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_buc
                               build_decode_batch, gather_prev_tokens)
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
-from sid.kernels.decode_attention import DecodeAttention
+from sid.kernels.decode_attention import DecodeAttention, length_bucket, nondet_geometry
 from sid.model.loader import build_model_config, load_weights, random_weights
 from sid.model.qwen3 import Qwen3Model
 
@@ -113,10 +113,14 @@ class ModelRunner:
         if prev_rows is not None and (prev_rows >= 0).any():
             gather_prev_tokens(static, prev_rows, prev_tokens)
         # The attention grid depends on the longest request (fixed-256 splits, or the
-        # segment count of the heuristic splits): bucket it so a graph serves a range.
-        bucket = seq_bucket(fb.max_seq_len)
+        # segment count of the heuristic splits): bucket it so a graph serves a range. The
+        # nondet plan follows the real request count, so it is part of the key.
+        bucket = length_bucket(fb.max_seq_len)
         fb.max_seq_len = bucket
-        fb.graph_key = ("decode", pad, invariant, bucket)
+        plan = None if invariant else nondet_geometry(
+            len(reqs), bucket, self.mcfg.num_kv_heads, self.decode_attn.cu_count(),
+            self.cfg.max_kv_splits)
+        fb.graph_key = ("decode", pad, invariant, bucket, plan)
         return fb
 
     def tag_verify(self, fb: ForwardBatch) -> ForwardBatch:
@@ -129,17 +133,6 @@ class ModelRunner:
         r = logits.shape[0]  # real rows (batch padding already dropped by forward)
         return _sample(logits, fb.temperatures[:r], fb.top_ks[:r], fb.top_ps[:r], fb.seeds[:r],
                        fb.sample_positions[:r], all_greedy=fb.all_greedy)
-
-
-def seq_bucket(n: int) -> int:
-    """Smallest of 256 * {1, 1.5, 2, 3, 4, 6, ...} >= n (graph key of a decode batch)."""
-    b = 256
-    while True:
-        if b >= n:
-            return b
-        if b + b // 2 >= n:
-            return b + b // 2
-        b *= 2
 
 
 class GraphCache:

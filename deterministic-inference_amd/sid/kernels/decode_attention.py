@@ -14,7 +14,12 @@ MI355X addition: the kernel's workgroup reads all KV heads of a token range (who
 2 KiB pool rows), so a split is further cut into segments of at most ``seg`` tokens,
 one workgroup each. batch_invariant uses seg = 256 = the split size (the reference's
 partition, independent of the batch); nondet/dvr take the largest of 256/128/64 that
-still gives 1.5 workgroups per CU for the batch's (bucketed) longest request.
+still gives 1.5 workgroups per CU for the batch's longest request, rounded up to a
+length bucket (so a HIP graph captured for a bucket computes the same plan).
+
+B in the policy is the number of real requests. A caller that pads its batch with empty
+requests (graph replay at a fixed size) passes the real count as ``policy_batch``, so
+padded and unpadded runs of the same requests pick the same splits and give the same bits.
 """
 
 from __future__ import annotations
@@ -57,6 +62,17 @@ def segment_size(batch: int, max_len: int, cu_count: int) -> int:
     return SEGMENT_SIZES[-1]
 
 
+def length_bucket(n: int) -> int:
+    """Smallest of 256 * {1, 1.5, 2, 3, 4, 6, ...} >= n."""
+    b = 256
+    while True:
+        if b >= n:
+            return b
+        if b + b // 2 >= n:
+            return b + b // 2
+        b *= 2
+
+
 def nondet_geometry(batch: int, max_len: int, num_kv_heads: int, cu_count: int,
                     max_kv_splits: int) -> tuple[int, int, int]:
     """(grid splits, segment size, grid slots) of the nondet/dvr plan. A request of length
@@ -65,7 +81,7 @@ def nondet_geometry(batch: int, max_len: int, num_kv_heads: int, cu_count: int,
     splits * ceil(chunk_max/seg) slots cover every request."""
     splits = heuristic_splits(batch, num_kv_heads, cu_count, max_kv_splits)
     chunk_max = max(32, _cdiv(_cdiv(max_len, splits), 32) * 32)
-    seg = segment_size(batch, max_len, cu_count)
+    seg = segment_size(batch, length_bucket(max_len), cu_count)
     return splits, seg, splits * max(1, _cdiv(chunk_max, seg))
 
 
@@ -106,10 +122,12 @@ class DecodeAttention:
         idx = self.device.index if self.device.index is not None else torch.cuda.current_device()
         return _cu_count(idx)
 
-    def plan(self, seq_lens: torch.Tensor, max_seq_len: int, invariant: bool):
+    def plan(self, seq_lens: torch.Tensor, max_seq_len: int, invariant: bool,
+             policy_batch: int | None = None):
         """(num_splits int32 [B] on device, grid splits, fixed split size, segment size,
-        grid slots). max_seq_len bounds every request's length (host-side, no sync)."""
-        bs = seq_lens.shape[0]
+        grid slots). max_seq_len bounds every request's length (host-side, no sync);
+        policy_batch: the real request count when seq_lens has padding rows."""
+        bs = seq_lens.shape[0] if policy_batch is None else int(policy_batch)
         max_len = max(int(max_seq_len), 1)
         if invariant:
             tile = self.invariant_split_size
@@ -123,16 +141,18 @@ class DecodeAttention:
 
     def forward(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, seq_lens: torch.Tensor,
-                max_seq_len: int, sm_scale: float, invariant: bool) -> torch.Tensor:
-        """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync)."""
+                max_seq_len: int, sm_scale: float, invariant: bool,
+                policy_batch: int | None = None) -> torch.Tensor:
+        """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync).
+        policy_batch: real requests among the B rows (the rest are empty padding)."""
         bs = q.shape[0]
         assert bs <= self.part_o.shape[0], "decode batch exceeds workspace"
         # One plan per forward: every layer sees the same seq_lens tensor.
-        key = (invariant, max_seq_len, bs)
+        key = (invariant, max_seq_len, bs, policy_batch)
         if self._plan_src is seq_lens and self._plan[0] == key:
             plan = self._plan[1]
         else:
-            plan = self.plan(seq_lens, max_seq_len, invariant)
+            plan = self.plan(seq_lens, max_seq_len, invariant, policy_batch)
             self._plan_src, self._plan = seq_lens, (key, plan)
         num_splits, grid_splits, fixed, seg, slots = plan
         assert slots <= self.part_o.shape[2], "decode plan exceeds the split workspace"

@@ -3,8 +3,8 @@
 Qwen3 specifics: explicit head_dim 128; per-head q/k RMSNorm after the QKV projection and
 BEFORE RoPE; no biases; SwiGLU; pre-norm with fused residual-add RMSNorm; tied lm_head.
 
-Routing: DECODE -> split-KV decode attention; PREFILL / VERIFY (or
-decode_backend="extend") -> extend attention. Both read all keys from the pool after
+Routing: DECODE -> split-KV decode attention (decode_backend "cuda" / "hip"); PREFILL /
+VERIFY, or DECODE with decode_backend "triton" / "extend" -> extend attention. Both read all keys from the pool after
 this step's K/V were written by reshape_and_cache.
 """
 
@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from sid.config import ModelConfig
+from sid.config import ModelConfig, decode_backend_kind
 from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.kernels.extend_attention import extend_attention_fwd
 from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_preferred,
@@ -74,7 +74,8 @@ class Qwen3Model:
                      self.rope.cos_sin, fb.out_slots, k_pool, v_pool, cfg.num_q_heads)
         if fb.mode == ForwardMode.DECODE and decode_backend == "hip":
             o = decode_attn.forward(q, k_pool, v_pool, fb.kv_indptr, fb.kv_indices, fb.seq_lens,
-                                    fb.max_seq_len, self.sm_scale, invariant=fb.invariant)
+                                    fb.max_seq_len, self.sm_scale, invariant=fb.invariant,
+                                    policy_batch=fb.real_rows)
         else:
             qo = fb.qo_indptr
             if qo is None:  # decode through the extend kernel: one query per request
@@ -86,7 +87,7 @@ class Qwen3Model:
 
     @torch.inference_mode()
     def forward(self, fb: ForwardBatch, kv_cache, decode_attn,
-                decode_backend: str = "hip", greedy: bool = False) -> torch.Tensor:
+                decode_backend: str = "cuda", greedy: bool = False) -> torch.Tensor:
         """fp32 logits [R, vocab] for the sampled rows (bf16-rounded values); with
         greedy=True, the greedy tokens int64 [R] instead (argmax of those logits, fused into
         the lm_head GEMM for decode-sized R).
@@ -94,6 +95,7 @@ class Qwen3Model:
         Same op order as sid/model/qwen3.py:88-115; the residual add + RMSNorm that follows
         each o / down projection consumes the projection directly (fused), and the down
         projection of layer i feeds layer i+1's input norm (or the final norm)."""
+        decode_backend = decode_backend_kind(decode_backend)
         if self.native_extend and fb.mode != ForwardMode.DECODE:
             return self._native_forward(fb, kv_cache, greedy)
         cfg = self.cfg

@@ -7,7 +7,7 @@ import random
 
 import pytest
 
-from sid.engine.model_runner import seq_bucket
+from sid.kernels.decode_attention import length_bucket as seq_bucket
 from sid.kernels.decode_attention import (MAX_GRID_SLOTS, SEGMENT_SIZES, heuristic_splits,
                                           nondet_geometry, segment_size, workspace_slots)
 
@@ -92,3 +92,15 @@ def test_batch_bucket():
     assert [batch_bucket(n, 256) for n in (1, 3, 5, 9, 64, 65, 129, 250)] == [
         1, 4, 8, 16, 64, 80, 160, 256]
     assert batch_bucket(100, 96) == 100  # never below the real size
+
+
+def test_decode_backend_names():
+    """The reference's names select the same paths; anything else is an error."""
+    import pytest
+    from sid.config import EngineConfig
+    assert EngineConfig(decode_backend="cuda").decode_backend == "hip"
+    assert EngineConfig(decode_backend="hip").decode_backend == "hip"
+    assert EngineConfig(decode_backend="triton").decode_backend == "extend"
+    assert EngineConfig().decode_backend == "hip"
+    with pytest.raises(ValueError):
+        EngineConfig(decode_backend="cuDNN")

@@ -102,3 +102,39 @@ def test_dvr_schedule_does_not_change_tokens():
         assert all(o.num_windows > 0 for o, p in zip(res, params) if p.is_deterministic)
     for i in range(0, len(prompts), 2):
         assert outs["reference"][i] == outs["default"][i], i
+
+
+def test_dvr_shared_prefill_equals_isolated_prefill():
+    """A prompt prefilled inside a shared batch gets the same logits, bit for bit, as when
+    prefilled alone (the reference's isolated dvr prefill, scheduler.py:63-86), and the
+    same K/V in the pool: every prefill kernel is batch-invariant."""
+    from sid.engine.batch import build_prefill_batch
+    from sid.engine.model_runner import ModelRunner
+    from sid.engine.request import Request
+    cfg = EngineConfig(mode=Mode.DVR, kv_pool_tokens=32768, max_reqs=64, max_seq_len=2048,
+                       max_decode_batch=64, num_layers=4, seed=7)
+    runner = ModelRunner(cfg, "cuda")
+    prompts = _prompts(5, 77)
+
+    def prefill(groups):
+        logits, kv = {}, {}
+        for grp in groups:
+            reqs = []
+            for i in grp:
+                r = Request(i, prompts[i], SamplingParams(is_deterministic=True), (0,))
+                r.req_row = runner.kv_cache.open_row()
+                reqs.append(r)
+            fb = build_prefill_batch(reqs, runner.kv_cache, "cuda", invariant=False)
+            out = runner.forward(fb)
+            for k, r in enumerate(reqs):
+                logits[r.rid] = out[k].clone()
+                slots = torch.from_numpy(runner.kv_cache.slot_range(r.req_row, 0, r.prompt_len))
+                kv[r.rid] = runner.kv_cache.k_pools[-1][slots.cuda()].clone()
+                runner.kv_cache.close_row(r.req_row)
+        return logits, kv
+
+    alone = prefill([[i] for i in range(5)])
+    shared = prefill([[3, 0, 4, 1, 2]])
+    for i in range(5):
+        assert torch.equal(alone[0][i], shared[0][i]), i
+        assert torch.equal(alone[1][i], shared[1][i]), i

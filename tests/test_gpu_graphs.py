@@ -33,11 +33,10 @@ def _requests(runner, lens, seed=0):
 
 @pytest.mark.parametrize("invariant", [False, True])
 def test_decode_graph_equals_eager(invariant):
-    # A decode graph runs its batch padded to the bucket size, and the nondet split count
-    # follows the (padded) batch size, so eager and graph forwards compute the same plan
-    # only for batch sizes that are buckets: nondet uses 4 then 2 requests. The fixed-256
-    # policy does not depend on the batch, so invariant mode pads 5 -> 8 and 3 -> 4.
-    lens = [30, 300, 7, 64, 129] if invariant else [30, 300, 7, 129]
+    # A decode graph runs its batch padded to the bucket size (5 -> 8, 3 -> 4); the nondet
+    # split policy follows the real request count, so padded and eager runs agree bitwise
+    # in both modes.
+    lens = [30, 300, 7, 64, 129]
     outs = {}
     for graphs in (False, True):
         runner = _runner(graphs)
@@ -47,7 +46,7 @@ def test_decode_graph_equals_eager(invariant):
             r.output_ids.append(t)
         logs = []
         for step in range(6):
-            active = reqs if step < 3 else reqs[:len(reqs) // 2 + 1 if invariant else 2]
+            active = reqs if step < 3 else reqs[:3]
             fb = runner.prepare_decode(active, invariant)
             assert (fb.graph_key is not None) == graphs
             lg = runner.forward(fb)
