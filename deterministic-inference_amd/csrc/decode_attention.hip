@@ -28,6 +28,8 @@
 // atomics, no dependence on batch composition or scheduling.
 #include "common.h"
 
+#include <mutex>
+
 namespace sid {
 namespace {
 
@@ -417,4 +419,85 @@ extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const vo
                                        batch, num_q_heads, num_kv_heads, head_dim, num_slots,
                                        max_splits, fixed_split_size, 0, max_splits, sm_scale,
                                        part_o, part_lse, part_batch, part_stride, o, stream);
+}
+
+// ---- allocation-free entry point ------------------------------------------------------
+//
+// Split partials in a file-scope device array instead of a caller workspace, for callers
+// that cannot allocate. Each GPU the library runs on holds its own copy for the life of the
+// process. Host code never passes the array's name to a kernel (on the host it is only a
+// stand-in symbol): the device address comes from hipGetSymbolAddress, once per device,
+// with that device current.
+namespace sid {
+namespace {
+
+constexpr int64_t kScratchBytes = SID_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+int scratch_for_current_device(unsigned char** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  SID_REQUIRE(err == hipSuccess, "flash_decode_fwd_noalloc: hipGetDevice failed: %s",
+              hipGetErrorString(err));
+  SID_REQUIRE(dev >= 0 && dev < kMaxDevices, "flash_decode_fwd_noalloc: device %d out of range",
+              dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    SID_REQUIRE(err == hipSuccess && ptr != nullptr,
+                "flash_decode_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                dev, hipGetErrorString(err));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = static_cast<unsigned char*>(g_scratch_ptr[dev]);
+  return SID_OK;
+}
+
+}  // namespace
+}  // namespace sid
+
+extern "C" int64_t sid_flash_decode_noalloc_scratch_bytes(void) { return sid::kScratchBytes; }
+
+extern "C" int sid_flash_decode_segments_fwd_noalloc(
+    const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
+    const int32_t* kv_indices, const int32_t* num_splits, int batch, int num_q_heads,
+    int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
+    int segment_size, int grid_slots, float sm_scale, void* o, void* stream) {
+  using namespace sid;
+  SID_REQUIRE(batch >= 0, "flash_decode_fwd_noalloc: negative batch");
+  if (batch == 0) return SID_OK;
+  int rc = check_decode_args(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, o, batch,
+                             num_q_heads, num_kv_heads, head_dim, num_slots, max_splits,
+                             fixed_split_size);
+  if (rc != SID_OK) return rc;
+  SID_REQUIRE(segment_size >= 0, "flash_decode_fwd_noalloc: negative segment_size");
+  SID_REQUIRE(grid_slots >= 1 && grid_slots <= kMaxGridSlots,
+              "flash_decode_fwd_noalloc: grid_slots %d out of range [1, %d]", grid_slots,
+              kMaxGridSlots);
+  // partials: part_o [batch][HQ][grid_slots][D] fp32, then part_lse [batch][HQ][grid_slots]
+  const int64_t o_bytes = (int64_t)batch * HQ * grid_slots * HEAD_DIM * 4;
+  const int64_t lse_off = (o_bytes + 255) / 256 * 256;
+  const int64_t need = lse_off + (int64_t)batch * HQ * grid_slots * 4;
+  SID_REQUIRE(grid_slots == 1 || need <= kScratchBytes,
+              "flash_decode_fwd_noalloc: %lld bytes of split partials (batch %d x %d slots) "
+              "exceed the %lld-byte scratch; use sid_flash_decode_segments_fwd with a "
+              "workspace", (long long)need, batch, grid_slots, (long long)kScratchBytes);
+  float* part_o = nullptr;
+  float* part_lse = nullptr;
+  if (grid_slots > 1) {
+    unsigned char* base = nullptr;
+    rc = scratch_for_current_device(&base);
+    if (rc != SID_OK) return rc;
+    part_o = reinterpret_cast<float*>(base);
+    part_lse = reinterpret_cast<float*>(base + lse_off);
+  }
+  // Stage 2 reads only the slots stage 1 wrote in this call, so nothing is cleared.
+  return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, batch, num_slots,
+                       fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
+                       grid_slots, o, static_cast<hipStream_t>(stream));
 }

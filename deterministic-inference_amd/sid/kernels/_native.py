@@ -40,13 +40,17 @@ _SIGNATURES = {
     "sid_flash_decode_segments_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
                                       _i32, _i32, _i32, _i32, _f32, _vp, _vp, _i32, _i32, _vp,
                                       _vp],
+    "sid_flash_decode_segments_fwd_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
+                                              _i32, _i64, _i32, _i32, _i32, _i32, _f32, _vp,
+                                              _vp],
     "sid_sample_rows": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp],
     "sid_linear_argmax": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
 }
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
             "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes",
-            "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward", *_SIGNATURES)
-ABI_VERSION = 11
+            "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward",
+            "sid_flash_decode_noalloc_scratch_bytes", *_SIGNATURES)
+ABI_VERSION = 12
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -81,6 +85,8 @@ class NativeLib:
         self.lib.sid_linear_argmax_workspace_bytes.argtypes = [_i64]
         self.lib.sid_sample_workspace_bytes.restype = ctypes.c_int64
         self.lib.sid_sample_workspace_bytes.argtypes = [_i64, _i64]
+        self.lib.sid_flash_decode_noalloc_scratch_bytes.restype = ctypes.c_int64
+        self.lib.sid_flash_decode_noalloc_scratch_bytes.argtypes = []
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.argtypes = argtypes
@@ -130,6 +136,32 @@ class NativeLib:
                    int(fixed_split_size), int(segment_size), slots, float(sm_scale),
                    part_o.data_ptr(), part_lse.data_ptr(), part_o.shape[0], part_o.shape[2],
                    o.data_ptr(), _stream(q))
+
+    def flash_decode_fwd_noalloc(self, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
+                                 max_splits: int, fixed_split_size: int, sm_scale: float, o,
+                                 segment_size: int = 0, grid_slots: int | None = None) -> None:
+        """flash_decode_fwd with the split partials in the library's static per-GPU scratch
+        (no workspace argument, nothing allocated). Calls that overlap on one GPU race."""
+        _gpu(q, "q", torch.bfloat16)
+        _check(q.dim() == 3, "q must be [B, HQ, D]")
+        b, hq, d = q.shape
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+            _gpu(t, name, torch.bfloat16)
+            _check(t.dim() == 3 and t.shape[2] == d, f"{name} must be [slots, HKV, {d}]")
+        _check(k_cache.shape == v_cache.shape, "k_cache and v_cache shapes differ")
+        _gpu(kv_indptr, "kv_indptr", torch.int32)
+        _check(kv_indptr.numel() == b + 1, "kv_indptr must have B+1 entries")
+        _gpu(kv_indices, "kv_indices", torch.int32)
+        _gpu(num_splits, "num_splits", torch.int32)
+        _check(num_splits.numel() == b, "num_splits must have B entries")
+        _gpu(o, "o", torch.bfloat16)
+        _check(o.shape == q.shape, "o must have q's shape")
+        slots = int(max_splits) if grid_slots is None else int(grid_slots)
+        self._call("sid_flash_decode_segments_fwd_noalloc", q.data_ptr(), k_cache.data_ptr(),
+                   v_cache.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                   num_splits.data_ptr(), b, hq, k_cache.shape[1], d, k_cache.shape[0],
+                   int(max_splits), int(fixed_split_size), int(segment_size), slots,
+                   float(sm_scale), o.data_ptr(), _stream(q))
 
     def reshape_and_cache(self, k, v, k_cache, v_cache, slot_mapping) -> None:
         _gpu(k, "k", torch.bfloat16)

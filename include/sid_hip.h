@@ -95,6 +95,34 @@ int sid_flash_decode_segments_fwd(const void* q, const void* k_cache, const void
                                   int part_batch, int part_stride, void* o, void* stream);
 
 /*
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): sid_flash_decode_segments_fwd without the part_o /
+ * part_lse workspace. The split partials live in a static device array of
+ * SID_DECODE_SCRATCH_BYTES per GPU (held until the process ends), laid out
+ * as part_o [batch][HQ][grid_slots][D] fp32 followed (256-byte aligned) by
+ * part_lse [batch][HQ][grid_slots]; a call that needs more returns an error
+ * (SID_ERR_INVALID). Same kernels and bits as the workspace version. Nothing is
+ * allocated and nothing needs clearing (stage 2 reads only what stage 1 wrote
+ * in the same call). Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams, or threads) race and must be
+ * serialized by the caller. The first call on a device resolves the array's
+ * device address (hipGetSymbolAddress) with that device current.
+ */
+#define SID_DECODE_SCRATCH_BYTES (32ll << 20)
+int sid_flash_decode_segments_fwd_noalloc(const void* q, const void* k_cache,
+                                          const void* v_cache, const int32_t* kv_indptr,
+                                          const int32_t* kv_indices, const int32_t* num_splits,
+                                          int batch, int num_q_heads, int num_kv_heads,
+                                          int head_dim, int64_t num_slots, int max_splits,
+                                          int fixed_split_size, int segment_size,
+                                          int grid_slots, float sm_scale, void* o,
+                                          void* stream);
+
+/* Size of that scratch array in bytes (SID_DECODE_SCRATCH_BYTES). */
+int64_t sid_flash_decode_noalloc_scratch_bytes(void);
+
+/*
  * Varlen causal attention over the paged pool (prefill, DVR verify). q, o:
  * bf16 [Text, HQ, D]; qo_indptr, kv_indptr int32 [B+1] (kv = prefix +
  * extend, all of it already in the pool); kv_indices int32. Query j of

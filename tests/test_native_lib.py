@@ -40,7 +40,8 @@ def test_python_binding_matches_header(ext):
 
 
 def test_abi_version(ext):
-    assert ext.lib.sid_abi_version() == 11
+    from sid.kernels._native import ABI_VERSION
+    assert ext.lib.sid_abi_version() == ABI_VERSION == 12
 
 
 def test_validation_errors_without_device_work(ext):
