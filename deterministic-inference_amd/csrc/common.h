@@ -89,6 +89,26 @@ __device__ __forceinline__ float lane_xor(float v, int mask) {
 
 __host__ __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// ---- the sampler's seeded Gumbel noise (sid/engine/sampler.py:22-29) ----------------------
+constexpr float kSampleEps = 1e-10f;
+
+// The reference's noise for (seed, position, column): int64 arithmetic with wraparound,
+// floor modulo 2^24 (= the low 24 bits in two's complement), u / 2^24. Only the low 24 bits
+// of the hash are used, and the low bits of a product depend only on the low bits of its
+// factors, so the per-column part is a 32-bit multiply and the per-row part (gumbel_row) is
+// computed once.
+__device__ __forceinline__ uint32_t gumbel_row(int64_t seed, int64_t pos) {
+  const uint64_t step = (static_cast<uint64_t>(seed) * 19349663ull) ^
+                        (static_cast<uint64_t>(pos) * 73856093ull);
+  return static_cast<uint32_t>(step * 8589934591ull);
+}
+
+__device__ __forceinline__ float seeded_gumbel(uint32_t row_hash, int col) {
+  const uint32_t h = row_hash ^ (static_cast<uint32_t>(col) * 479001599u);
+  const float u = static_cast<float>(h & 0xffffffu) / 16777216.0f;
+  return -logf(-logf(u + kSampleEps) + kSampleEps);
+}
+
 // Thread-local error message for the C-ABI (read back via sid_last_error()).
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);

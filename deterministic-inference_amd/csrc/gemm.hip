@@ -644,6 +644,401 @@ __global__ void __launch_bounds__(256) argmax_finalize_kernel(const float* __res
   }
 }
 
+// ---- lm_head with the stochastic sampler fused into its epilogue ---------------------------
+//
+// The draw of sid/engine/sampler.py:32-69 without truncation (top_k <= 0, top_p >= 1):
+// token = argmax_c log(p_c + eps) + g_c with p = softmax(l / T) and g the seeded Gumbel
+// noise; greedy rows (T <= 0) take the argmax of the logits. Nothing of the logits is
+// written. linear_sample_kernel is linear_stream_kernel (same grid, same per-column MFMA
+// sequence and chunk fold, so the same logit bits l_c) with this epilogue: for every row it
+// holds, each lane keeps over its wave's columns
+//   mx, sm   online softmax state of x = l / T (sm = sum of exp(x - mx), rescaled when mx
+//            grows),
+//   a1       the column with the largest x + g (value a1v, its x a1x, index a1i; ties to the
+//            lower index), a2v the second largest x + g;
+// the 16 lanes of a row are merged in a fixed butterfly and written per (wave, row).
+// sample_finalize_kernel takes one row: M = max mx, S = sum of sm exp(mx - M) in wave order,
+// then the exact score log(exp(x - M) / S + eps) + g of every wave's a1 (the formula of the
+// unfused sampler). Any other column c of a wave scores
+//   log(exp(x_c + g_c - M) / S + eps exp(g_c)) <= log(exp(a2v - M) / S + eps exp(G)),
+// increasing in x_c + g_c and in g_c (G: the largest value the noise takes, at u = 1 - 2^-24),
+// so a wave whose bound stays below the best candidate
+// (by a margin far above float rounding) cannot hold the winner. A wave that fails the test
+// (a near-tie, or non-finite statistics: then every wave) has its logits recomputed for the
+// row with the same MFMA sequence (identical bits) and every column scored exactly.
+struct SampleStats {
+  float* mx;
+  float* sm;
+  float* a1v;
+  float* a1x;
+  float* a2v;
+  int* a1i;
+};
+
+__device__ __forceinline__ void softmax_merge(float& m, float& s, float om, float os) {
+  const float nm = fmaxf(m, om);
+  const float a = m == -INFINITY ? 0.0f : s * expf(m - nm);
+  const float b = om == -INFINITY ? 0.0f : os * expf(om - nm);
+  m = nm;
+  s = a + b;
+}
+
+template <int MBS>
+__global__ void __launch_bounds__(STREAM_WAVES * 64) linear_sample_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w, int M, int N,
+    const float* __restrict__ temps, const int64_t* __restrict__ seeds,
+    const int64_t* __restrict__ positions, SampleStats st, int cand_rows, int row0) {
+  extern __shared__ __align__(16) bf16_t lx[];  // [MBS*16][WXS]
+  __shared__ float s_t[64];
+  __shared__ uint32_t s_h[64];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int gw = blockIdx.x * STREAM_WAVES + wave;
+  const int num_waves = gridDim.x * STREAM_WAVES;
+  const int tiles = N / 16;
+  const int t_begin = static_cast<int>(static_cast<int64_t>(gw) * tiles / num_waves);
+  const int t_end = static_cast<int>(static_cast<int64_t>(gw + 1) * tiles / num_waves);
+  const int units = (t_end - t_begin) * WIDE_NCH;
+
+  auto unit_ptr = [&](int u) {
+    u = min(u, max(units - 1, 0));
+    const int64_t col = static_cast<int64_t>(t_begin + (u >> 2)) * 16 + r;
+    return w + col * WIDE_K + (u & 3) * KC + 8 * g;
+  };
+  bf16x8_v b0[NSTEP], b1[NSTEP], b2[NSTEP];
+  if (units > 0) {
+    load_w(b0, unit_ptr(0), 0);
+    load_w(b1, unit_ptr(1), 0);
+  }
+  constexpr int ROWS = MBS * 16;
+  constexpr int VPR = WIDE_K / 8;
+  constexpr int VPT = ROWS * VPR / (STREAM_WAVES * 64);
+  {
+    bf16x8_v xv[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = threadIdx.x + i * STREAM_WAVES * 64;
+      const int row = v / VPR;
+      xv[i] = ld_frag(x + static_cast<int64_t>(min(row, M - 1)) * ldx + (v % VPR) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = threadIdx.x + i * STREAM_WAVES * 64;
+      *reinterpret_cast<bf16x8_v*>(&lx[(v / VPR) * WXS + (v % VPR) * 8]) = xv[i];
+    }
+  }
+  if (threadIdx.x < 64) {
+    const int row = min(static_cast<int>(threadIdx.x), M - 1) + row0;
+    s_t[threadIdx.x] = temps[row];
+    s_h[threadIdx.x] = gumbel_row(seeds[row], positions[row]);
+  }
+  __syncthreads();
+
+  f32x4_v total[MBS];
+  float mx[MBS][4], sm[MBS][4], a1v[MBS][4], a1x[MBS][4], a2v[MBS][4];
+  int a1i[MBS][4];
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mx[mb][i] = -INFINITY;
+      sm[mb][i] = 0.0f;
+      a1v[mb][i] = -INFINITY;
+      a1x[mb][i] = -INFINITY;
+      a2v[mb][i] = -INFINITY;
+      a1i[mb][i] = 0x7fffffff;
+    }
+  }
+
+  auto consume = [&](const bf16x8_v (&wf)[NSTEP], int u) {
+    const int c = u & 3;
+    f32x4_v acc[MBS];
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb) acc[mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+#pragma unroll
+      for (int mb = 0; mb < MBS; ++mb) {
+        const bf16x8_v af = *reinterpret_cast<const bf16x8_v*>(
+            &lx[(16 * mb + r) * WXS + c * KC + KSTEP * s + 8 * g]);
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[s], acc[mb], 0, 0, 0);
+      }
+    }
+    if (c == 0) {
+#pragma unroll
+      for (int mb = 0; mb < MBS; ++mb) total[mb] = acc[mb];
+    } else {
+#pragma unroll
+      for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) total[mb][i] += acc[mb][i];
+      }
+    }
+    if (c != 3) return;
+    const int col = (t_begin + (u >> 2)) * 16 + r;
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * mb + 4 * g + i;
+        const float vr = round_bf16(total[mb][i]);
+        const float t = s_t[row];
+        if (!(t > 0.0f)) {  // greedy row: the logit itself
+          if (argmax_better(vr, col, a1v[mb][i], a1i[mb][i])) {
+            a1v[mb][i] = vr;
+            a1i[mb][i] = col;
+          }
+          continue;
+        }
+        const float xv = vr / t;
+        if (xv > mx[mb][i]) {
+          sm[mb][i] = sm[mb][i] * expf(mx[mb][i] - xv) + 1.0f;
+          mx[mb][i] = xv;
+        } else {
+          sm[mb][i] += expf(xv - mx[mb][i]);
+        }
+        const float gn = seeded_gumbel(s_h[row], col);
+        const float xg = xv + gn;
+        if (xg > a1v[mb][i] || (xg == a1v[mb][i] && col < a1i[mb][i])) {
+          a2v[mb][i] = a1v[mb][i];
+          a1v[mb][i] = xg;
+          a1x[mb][i] = xv;
+          a1i[mb][i] = col;
+        } else {
+          a2v[mb][i] = fmaxf(a2v[mb][i], xg);
+        }
+      }
+    }
+  };
+
+  for (int u = 0; u < units; u += 3) {
+    load_w(b2, unit_ptr(u + 2), 0);
+    consume(b0, u);
+    load_w(b0, unit_ptr(u + 3), 0);
+    if (u + 1 < units) consume(b1, u + 1);
+    load_w(b1, unit_ptr(u + 4), 0);
+    if (u + 2 < units) consume(b2, u + 2);
+  }
+
+  // Merge the 16 column lanes of each row (fixed butterfly), lane r = 0 writes.
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * mb + 4 * g + i;
+      const bool greedy = !(s_t[row] > 0.0f);
+      float m = mx[mb][i], sv = sm[mb][i], v1 = a1v[mb][i], x1 = a1x[mb][i], v2 = a2v[mb][i];
+      int i1 = a1i[mb][i];
+#pragma unroll
+      for (int mask = 1; mask < 16; mask <<= 1) {
+        const int src = (lane ^ mask) << 2;
+        const float om = lane_xor(m, mask);
+        const float os = lane_xor(sv, mask);
+        const float ov1 = lane_xor(v1, mask);
+        const float ox1 = lane_xor(x1, mask);
+        const float ov2 = lane_xor(v2, mask);
+        const int oi1 = __builtin_amdgcn_ds_bpermute(src, i1);
+        if (greedy) {
+          if (argmax_better(ov1, oi1, v1, i1)) {
+            v1 = ov1;
+            i1 = oi1;
+          }
+          continue;
+        }
+        softmax_merge(m, sv, om, os);
+        if (ov1 > v1 || (ov1 == v1 && oi1 < i1)) {
+          v2 = fmaxf(v1, ov2);
+          v1 = ov1;
+          x1 = ox1;
+          i1 = oi1;
+        } else {
+          v2 = fmaxf(v2, fmaxf(ov1, ov2));
+        }
+      }
+      if (r == 0 && row < M) {
+        const int64_t o = static_cast<int64_t>(gw) * cand_rows + row0 + row;
+        st.mx[o] = m;
+        st.sm[o] = sv;
+        st.a1v[o] = v1;
+        st.a1x[o] = x1;
+        st.a2v[o] = v2;
+        st.a1i[o] = i1;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ bool score_better(float v, int i, float bv, int bi) {
+  return argmax_better(v, i, bv, bi);
+}
+
+// Best (value, index) over the block under argmax_better; every thread gets the result.
+__device__ __forceinline__ void block_best_i32(float& bv, int& bi, float* s_v, int* s_i) {
+  for (int mask = 1; mask < 64; mask <<= 1) {
+    const float ov = lane_xor(bv, mask);
+    const int oi = __builtin_amdgcn_ds_bpermute((__lane_id() ^ mask) << 2, bi);
+    if (argmax_better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    s_v[threadIdx.x >> 6] = bv;
+    s_i[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  bv = s_v[0];
+  bi = s_i[0];
+  for (int k = 1; k < static_cast<int>(blockDim.x >> 6); ++k) {
+    if (argmax_better(s_v[k], s_i[k], bv, bi)) {
+      bv = s_v[k];
+      bi = s_i[k];
+    }
+  }
+  __syncthreads();
+}
+
+constexpr int kFinThreads = 256;
+constexpr float kCertMargin = 1e-3f;  // the certificate's slack over float rounding
+
+__global__ void __launch_bounds__(kFinThreads) sample_finalize_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w, int N,
+    SampleStats st, int num_waves, int M, const float* __restrict__ temps,
+    const int64_t* __restrict__ seeds, const int64_t* __restrict__ positions,
+    int* __restrict__ redo, int64_t* __restrict__ out, int recompute_all) {
+  __shared__ float s_v[kFinThreads / 64];
+  __shared__ int s_i[kFinThreads / 64];
+  __shared__ float s_red[kFinThreads / 64];
+  __shared__ int s_nredo;
+  __shared__ __align__(16) bf16_t s_x[WIDE_K];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float t = temps[row];
+  auto at = [&](int wv) { return static_cast<int64_t>(wv) * M + row; };
+
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  if (!(t > 0.0f)) {  // greedy row
+    for (int wv = tid; wv < num_waves; wv += kFinThreads) {
+      if (argmax_better(st.a1v[at(wv)], st.a1i[at(wv)], bv, bi)) {
+        bv = st.a1v[at(wv)];
+        bi = st.a1i[at(wv)];
+      }
+    }
+    block_best_i32(bv, bi, s_v, s_i);
+    if (tid == 0) out[row] = bi == 0x7fffffff ? 0 : bi;
+    return;
+  }
+  // M and S (fixed order: each thread's waves in order, then the butterfly, then waves)
+  float m = -INFINITY;
+  for (int wv = tid; wv < num_waves; wv += kFinThreads) m = fmaxf(m, st.mx[at(wv)]);
+  for (int mask = 1; mask < 64; mask <<= 1) m = fmaxf(m, lane_xor(m, mask));
+  if ((tid & 63) == 0) s_red[tid >> 6] = m;
+  __syncthreads();
+  m = s_red[0];
+  for (int k = 1; k < kFinThreads / 64; ++k) m = fmaxf(m, s_red[k]);
+  __syncthreads();
+  float part = 0.0f;
+  for (int wv = tid; wv < num_waves; wv += kFinThreads) {
+    const float mw = st.mx[at(wv)];
+    if (mw != -INFINITY) part += st.sm[at(wv)] * expf(mw - m);
+  }
+  for (int mask = 1; mask < 64; mask <<= 1) part += lane_xor(part, mask);
+  if ((tid & 63) == 0) s_red[tid >> 6] = part;
+  __syncthreads();
+  float sum = s_red[0];
+  for (int k = 1; k < kFinThreads / 64; ++k) sum += s_red[k];
+  const bool full = recompute_all || !isfinite(m) || !isfinite(sum) || !(sum > 0.0f);
+  // eps * exp(G), G = the largest noise value (u = 1 - 2^-24), rounded up a little
+  const float g_max = -logf(-logf(16777215.0f / 16777216.0f + kSampleEps) + kSampleEps);
+  const float eps_g = kSampleEps * expf(g_max) * 1.0001f;
+  const uint32_t h = gumbel_row(seeds[row], positions[row]);
+  auto score = [&](float xv, int col) {
+    return logf(expf(xv - m) / sum + kSampleEps) + seeded_gumbel(h, col);
+  };
+  // Every wave's candidate, scored exactly.
+  if (!full) {
+    for (int wv = tid; wv < num_waves; wv += kFinThreads) {
+      const int c = st.a1i[at(wv)];
+      if (c == 0x7fffffff) continue;
+      const float sc = score(st.a1x[at(wv)], c);
+      if (argmax_better(sc, c, bv, bi)) {
+        bv = sc;
+        bi = c;
+      }
+    }
+  }
+  block_best_i32(bv, bi, s_v, s_i);
+  // Waves whose other columns might beat the best candidate.
+  if (tid == 0) s_nredo = 0;
+  __syncthreads();
+  int* list = redo + static_cast<int64_t>(row) * num_waves;
+  for (int wv = tid; wv < num_waves; wv += kFinThreads) {
+    bool need = full;
+    if (!need && st.a1i[at(wv)] != 0x7fffffff) {
+      const float bound = logf(expf(st.a2v[at(wv)] - m) / sum + eps_g);
+      need = !(bound + kCertMargin < bv);
+    }
+    if (need) list[atomicAdd(&s_nredo, 1)] = wv;
+  }
+  __syncthreads();
+  const int nredo = s_nredo;
+  if (nredo > 0) {
+    for (int i = tid; i < WIDE_K / 8; i += kFinThreads)
+      *reinterpret_cast<bf16x8_v*>(&s_x[8 * i]) =
+          *reinterpret_cast<const bf16x8_v*>(x + static_cast<int64_t>(row) * ldx + 8 * i);
+    __syncthreads();
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int tiles = N / 16;
+    // Recompute the listed waves' logits (the streaming kernel's MFMA sequence and chunk fold
+    // with this row in all 16 A rows, so every lane's result is the row's logit of its
+    // column) and score every column.
+    for (int k = wave; k < nredo; k += kFinThreads / 64) {
+      const int wv = list[k];
+      const int tb = static_cast<int>(static_cast<int64_t>(wv) * tiles / num_waves);
+      const int te = static_cast<int>(static_cast<int64_t>(wv + 1) * tiles / num_waves);
+      for (int tile = tb; tile < te; ++tile) {
+        const int col = tile * 16 + r;
+        const bf16_t* wrow = w + static_cast<int64_t>(col) * WIDE_K + 8 * g;
+        f32x4_v tot = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < WIDE_NCH; ++c) {
+          bf16x8_v wf[NSTEP];
+          load_w(wf, wrow, c * KC);
+          f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int s = 0; s < NSTEP; ++s) {
+            const bf16x8_v af = *reinterpret_cast<const bf16x8_v*>(&s_x[c * KC + KSTEP * s + 8 * g]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[s], acc, 0, 0, 0);
+          }
+          if (c == 0) {
+            tot = acc;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tot[i] += acc[i];
+          }
+        }
+        if (g == 0) {
+          const float vr = round_bf16(tot[0]);
+          const float sc = score(vr / t, col);
+          if (argmax_better(sc, col, bv, bi)) {
+            bv = sc;
+            bi = col;
+          }
+        }
+      }
+    }
+    block_best_i32(bv, bi, s_v, s_i);
+  }
+  if (tid == 0) out[row] = bi == 0x7fffffff ? 0 : bi;
+}
+
 int check_shapes(const void* x, int64_t ldx, const void* w, int64_t m, int64_t n, int64_t k,
                  const char* name) {
   SID_REQUIRE(x && w, "%s: null pointer", name);
@@ -938,6 +1333,80 @@ extern "C" int sid_linear_argmax(const void* x, int64_t ldx, const void* w, cons
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(256), 0, s, bv, bi, waves,
                      static_cast<int>(m), out_idx);
   return check_launch("linear_argmax finalize");
+}
+
+// Workspace of sid_linear_sample: 6 per-(wave, row) statistics + the finalize's lists.
+static int64_t sample_ws_bytes(int64_t m) {
+  const int64_t waves = static_cast<int64_t>(stream_grid()) * STREAM_WAVES;
+  return waves * m * 4 * 7;
+}
+
+extern "C" int64_t sid_linear_sample_workspace_bytes(int64_t m) {
+  if (m < 1 || m > kStreamMaxM) return 0;
+  return sample_ws_bytes(m);
+}
+
+template <int MBS>
+static void launch_sample_mbs(const bf16_t* x, int64_t ldx, const void* w, int m, int n,
+                              const float* temps, const int64_t* seeds, const int64_t* pos,
+                              SampleStats st, int cand_rows, int row0, hipStream_t s) {
+  const size_t lds = static_cast<size_t>(MBS * 16) * WXS * sizeof(bf16_t);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_sample_kernel<MBS>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((linear_sample_kernel<MBS>), dim3(stream_grid()), dim3(STREAM_WAVES * 64),
+                     lds, s, x, ldx, (const bf16_t*)w, m, n, temps, seeds, pos, st, cand_rows,
+                     row0);
+}
+
+extern "C" int sid_linear_sample(const void* x, int64_t ldx, const void* w, int64_t m, int64_t n,
+                                 int64_t k, const float* temperatures, const int64_t* seeds,
+                                 const int64_t* positions, void* workspace,
+                                 int64_t workspace_bytes, int64_t* out_idx, int flags,
+                                 void* stream) {
+  SID_REQUIRE(m >= 0 && n >= 0 && k >= 0, "linear_sample: negative size");
+  SID_REQUIRE(flags == 0 || flags == 1, "linear_sample: unknown flags %d", flags);
+  if (m == 0) return SID_OK;
+  SID_REQUIRE(n > 0, "linear_sample: no columns");
+  SID_REQUIRE(out_idx && workspace && temperatures && seeds && positions,
+              "linear_sample: null pointer");
+  int rc = check_shapes(x, ldx, w, m, n, k, "linear_sample");
+  if (rc != SID_OK) return rc;
+  SID_REQUIRE(stream_shape_ok(m, n, k),
+              "linear_sample: needs 1 <= M <= %d and K == %d (got M=%lld, K=%lld)",
+              (int)kStreamMaxM, WIDE_K, (long long)m, (long long)k);
+  const int64_t need = sample_ws_bytes(m);
+  SID_REQUIRE(workspace_bytes >= need, "linear_sample: workspace %lld bytes, need %lld",
+              (long long)workspace_bytes, (long long)need);
+  SID_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+              "linear_sample: workspace must be 16-byte aligned");
+  const int waves = stream_grid() * STREAM_WAVES;
+  const int64_t plane = static_cast<int64_t>(waves) * m;
+  float* base = static_cast<float*>(workspace);
+  SampleStats st{base, base + plane, base + 2 * plane, base + 3 * plane, base + 4 * plane,
+                 reinterpret_cast<int*>(base + 5 * plane)};
+  int* redo = reinterpret_cast<int*>(base + 6 * plane);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int mi = static_cast<int>(m);
+  for (int r0 = 0; r0 < mi; r0 += MROWS) {
+    const int mg = min(MROWS, mi - r0);
+    const bf16_t* xg = static_cast<const bf16_t*>(x) + static_cast<int64_t>(r0) * ldx;
+    switch ((mg + 15) / 16) {
+      case 1: launch_sample_mbs<1>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
+      case 2: launch_sample_mbs<2>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
+      case 3: launch_sample_mbs<3>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
+      default: launch_sample_mbs<4>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
+    }
+    rc = check_launch("linear_sample");
+    if (rc != SID_OK) return rc;
+  }
+  hipLaunchKernelGGL(sample_finalize_kernel, dim3((unsigned)m), dim3(kFinThreads), 0, s,
+                     (const bf16_t*)x, ldx, (const bf16_t*)w, (int)n, st, waves, mi, temperatures,
+                     seeds, positions, redo, out_idx, flags);
+  return check_launch("linear_sample finalize");
 }
 
 extern "C" int sid_linear_silu_mul(const void* x, const void* w, void* out, int64_t m, int64_t k,

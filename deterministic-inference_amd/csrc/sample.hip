@@ -110,28 +110,10 @@ __global__ void __launch_bounds__(kThreads) argmax_kernel(const float* __restric
 constexpr int kSampleThreads = 1024;
 constexpr int kSampleWaves = kSampleThreads / 64;
 constexpr double kMassUnit = 281474976710656.0;  // 2^48
-constexpr float kSampleEps = 1e-10f;
 constexpr int kHistCopies = 16;
 
 __device__ __forceinline__ uint64_t mass_of(uint32_t key) {
   return static_cast<uint64_t>(static_cast<double>(__uint_as_float(key)) * kMassUnit);
-}
-
-// The reference's Gumbel noise for (seed, position, column): int64 arithmetic with
-// wraparound, floor modulo 2^24 (= the low 24 bits in two's complement), u / 2^24.
-// Only the low 24 bits of the hash are used, and the low bits of a product depend only on
-// the low bits of its factors, so the per-column part is a 32-bit multiply and the
-// per-row part (gumbel_row) is computed once.
-__device__ __forceinline__ uint32_t gumbel_row(int64_t seed, int64_t pos) {
-  const uint64_t step = (static_cast<uint64_t>(seed) * 19349663ull) ^
-                        (static_cast<uint64_t>(pos) * 73856093ull);
-  return static_cast<uint32_t>(step * 8589934591ull);
-}
-
-__device__ __forceinline__ float seeded_gumbel(uint32_t row_hash, int col) {
-  const uint32_t h = row_hash ^ (static_cast<uint32_t>(col) * 479001599u);
-  const float u = static_cast<float>(h & 0xffffffu) / 16777216.0f;
-  return -logf(-logf(u + kSampleEps) + kSampleEps);
 }
 
 // Calls f(value, column) for every column of a row: 16-byte loads, UNROLL of them in flight

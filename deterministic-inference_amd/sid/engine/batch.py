@@ -52,6 +52,7 @@ class ForwardBatch:
     seeds: Optional[torch.Tensor] = None             # int64 [R]
     invariant: bool = False
     all_greedy: Optional[bool] = None  # host-known: every row has temperature 0
+    untruncated: Optional[bool] = None  # host-known: no row has a top-k / top-p limit
     graph_key: Optional[tuple] = None  # set when the inputs live in graph-static buffers
     real_rows: Optional[int] = None    # rows of real requests when padded (decode graphs)
     # decode batches in the graph-static buffers: build_paged_decode_indices arguments, run at the
@@ -109,6 +110,11 @@ def _sampling_host(reqs, repeat: int = 1):
     return f[:, 0], i[:, 0], f[:, 1], i[:, 1]
 
 
+def _untruncated(top_ks: np.ndarray, top_ps: np.ndarray) -> bool:
+    """No row limits its draw (top_k <= 0 and top_p >= 1 everywhere)."""
+    return bool((np.asarray(top_ks) <= 0).all() and (np.asarray(top_ps) >= 1.0).all())
+
+
 def _to_device(arrays: list, dtype, device) -> list:
     """One host->device copy for several same-dtype 1-D arrays; returns device views."""
     sizes = [int(a.size) for a in arrays]
@@ -148,6 +154,7 @@ def build_prefill_batch(reqs: list, kv, device: str, invariant: bool) -> Forward
         sample_indices=i64[3], sample_positions=i64[4],
         temperatures=f32[0], top_ks=i64[5], top_ps=f32[1], seeds=i64[6],
         invariant=invariant, all_greedy=bool((temps == 0).all()),
+        untruncated=_untruncated(top_ks, top_ps),
     )
 
 
@@ -261,6 +268,6 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         sample_indices=None, sample_positions=d_spos,
         temperatures=d_temps, top_ks=d_topk, top_ps=d_topp, seeds=d_seed,
         invariant=invariant, all_greedy=bool((temps == 0).all()),
-        real_rows=bs if d_ids.shape[0] != bs else None,
+        untruncated=_untruncated(top_ks, top_ps), real_rows=bs if d_ids.shape[0] != bs else None,
         index_build=index_build, new_slots_host=new_slots,
     )

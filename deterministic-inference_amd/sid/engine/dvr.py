@@ -173,6 +173,7 @@ class Verifier:
             sample_indices=self._sample_rows[:rows], sample_positions=dev["sample_positions"],
             temperatures=dev["temperatures"], top_ks=dev["top_ks"], top_ps=dev["top_ps"],
             seeds=dev["seeds"], invariant=True, all_greedy=bool((temps == 0).all()),
+            untruncated=bool((top_k <= 0).all() and (top_p >= 1.0).all()),
         )
         return fb, VerifyMeta(reqs=list(reqs), window_lens=u.tolist(), windows=windows)
 

@@ -18,6 +18,7 @@ from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_buc
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
 from sid.kernels.decode_attention import DecodeAttention, length_bucket, nondet_geometry
+from sid.kernels.matmul_persistent import linear_sample_supported
 from sid.model.loader import build_model_config, load_weights, random_weights
 from sid.model.qwen3 import Qwen3Model
 
@@ -77,25 +78,35 @@ class ModelRunner:
             "kv_indices": z(g * (cfg.max_seq_len + cfg.dvr_window_size), torch.int32),
         }
 
-    def forward(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
-        """Logits of the sampled rows, or (greedy=True) their greedy tokens; rows of batch
+    def forward(self, fb: ForwardBatch, greedy: bool = False,
+                sample: bool = False) -> torch.Tensor:
+        """Logits of the sampled rows, or (greedy=True) their greedy tokens, or (sample=True,
+        decode batches without top-k / top-p limits) their sampled tokens; rows of batch
         padding are dropped."""
         if self.graphs is not None and fb.graph_key is not None:
-            out = self.graphs.run(fb, greedy)
+            out = self.graphs.run(fb, greedy, sample)
         else:
-            out = self._forward_eager(fb, greedy)
+            out = self._forward_eager(fb, greedy, sample)
         return out if fb.real_rows is None else out[:fb.real_rows]
 
-    def _forward_eager(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
+    def _forward_eager(self, fb: ForwardBatch, greedy: bool = False,
+                       sample: bool = False) -> torch.Tensor:
         fb.build_indices()
         return self.model.forward(fb, self.kv_cache, self.decode_attn,
-                                  decode_backend=self.cfg.decode_backend, greedy=greedy)
+                                  decode_backend=self.cfg.decode_backend, greedy=greedy,
+                                  sample=sample)
 
     def step(self, fb: ForwardBatch) -> torch.Tensor:
         """forward + sample -> int64 tokens [R]. An all-greedy batch takes the fused
-        lm_head + argmax path (same tokens as sampling the logits; no logits written)."""
+        lm_head + argmax path, a decode batch of at most 256 rows without top-k / top-p
+        limits the fused lm_head + sampler (same tokens as sampling the logits, up to float
+        near-ties of the scores; no logits written); the rest writes the logits and runs the
+        sampler kernel over them."""
         if fb.all_greedy:
             return self.forward(fb, greedy=True)
+        if (fb.mode == ForwardMode.DECODE and fb.untruncated
+                and linear_sample_supported(fb.input_ids.shape[0], self.mcfg.hidden_size)):
+            return self.forward(fb, sample=True)
         return self.sample(fb, self.forward(fb))
 
     def prepare_decode(self, reqs: list, invariant: bool, prev_rows=None,
@@ -156,11 +167,11 @@ class GraphCache:
         self.decode_static = DecodeStatic(cfg.max_decode_batch,
                                           cfg.max_decode_batch * cfg.max_seq_len, runner.device)
 
-    def run(self, fb: ForwardBatch, greedy: bool = False) -> torch.Tensor:
-        key = (fb.graph_key, greedy)
+    def run(self, fb: ForwardBatch, greedy: bool = False, sample: bool = False) -> torch.Tensor:
+        key = (fb.graph_key, greedy, sample)
         entry = self.graphs.get(key)
         if entry is None:
-            entry = self._capture(fb, greedy)
+            entry = self._capture(fb, greedy, sample)
             self.graphs[key] = entry
             while len(self.graphs) > self.max_graphs:
                 self.graphs.popitem(last=False)
@@ -170,7 +181,7 @@ class GraphCache:
         graph.replay()
         return out
 
-    def _capture(self, fb: ForwardBatch, greedy: bool):
+    def _capture(self, fb: ForwardBatch, greedy: bool, sample: bool):
         runner = self.runner
         kind = fb.graph_key[0]
         if kind not in self._warm:
@@ -178,10 +189,10 @@ class GraphCache:
             # (library load, descriptors, torch's first-use work) happens outside a capture;
             # it computes exactly what the replay recomputes. Later captures of the kind run
             # the same host code and skip it.
-            runner._forward_eager(fb, greedy)
+            runner._forward_eager(fb, greedy, sample)
             self._warm.add(kind)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self.pools[fb.graph_key[0]]):
-            out = runner._forward_eager(fb, greedy)
+            out = runner._forward_eager(fb, greedy, sample)
         return graph, out

@@ -44,13 +44,16 @@ _SIGNATURES = {
                                               _i32, _i64, _i32, _i32, _i32, _i32, _f32, _vp,
                                               _vp],
     "sid_sample_rows": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp],
+    "sid_linear_sample": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i32,
+                          _vp],
     "sid_linear_argmax": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
 }
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
             "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes",
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward",
-            "sid_flash_decode_noalloc_scratch_bytes", *_SIGNATURES)
-ABI_VERSION = 12
+            "sid_flash_decode_noalloc_scratch_bytes", "sid_linear_sample_workspace_bytes",
+            *_SIGNATURES)
+ABI_VERSION = 13
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -85,6 +88,8 @@ class NativeLib:
         self.lib.sid_linear_argmax_workspace_bytes.argtypes = [_i64]
         self.lib.sid_sample_workspace_bytes.restype = ctypes.c_int64
         self.lib.sid_sample_workspace_bytes.argtypes = [_i64, _i64]
+        self.lib.sid_linear_sample_workspace_bytes.restype = ctypes.c_int64
+        self.lib.sid_linear_sample_workspace_bytes.argtypes = [_i64]
         self.lib.sid_flash_decode_noalloc_scratch_bytes.restype = ctypes.c_int64
         self.lib.sid_flash_decode_noalloc_scratch_bytes.argtypes = []
         for name, argtypes in _SIGNATURES.items():
@@ -279,6 +284,23 @@ class NativeLib:
                    logits.data_ptr() if logits is not None else None, m, n, k,
                    workspace.data_ptr(), workspace.numel() * workspace.element_size(),
                    out.data_ptr(), _stream(x))
+
+    def linear_sample_workspace_bytes(self, m: int) -> int:
+        return int(self.lib.sid_linear_sample_workspace_bytes(m))
+
+    def linear_sample(self, x, w, temperatures, seeds, positions, workspace, out,
+                      recompute_all: bool = False) -> None:
+        m, k, n = self._linear_check(x, w)
+        for name, t, dt in (("temperatures", temperatures, torch.float32),
+                            ("seeds", seeds, torch.int64), ("positions", positions, torch.int64),
+                            ("out", out, torch.int64)):
+            _gpu(t, name, dt)
+            _check(t.numel() == m, f"{name} must have M entries")
+        _gpu(workspace, "workspace")
+        self._call("sid_linear_sample", x.data_ptr(), x.stride(0) if m > 1 else k, w.data_ptr(),
+                   m, n, k, temperatures.data_ptr(), seeds.data_ptr(), positions.data_ptr(),
+                   workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                   out.data_ptr(), int(recompute_all), _stream(x))
 
     @staticmethod
     def _linear_check(x, w):

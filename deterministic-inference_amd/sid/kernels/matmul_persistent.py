@@ -110,3 +110,30 @@ def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Te
         out = torch.empty(m, dtype=torch.int64, device=x.device)
     ext.linear_argmax(x, weight, bias, logits, workspace, out)
     return out
+
+
+def linear_sample_supported(m: int, k: int) -> bool:
+    """Shapes the fused lm_head + sampler kernel takes (M <= 256, K = 1024)."""
+    return 1 <= m <= 256 and k == 1024
+
+
+def linear_sample(x: torch.Tensor, weight: torch.Tensor, temperatures: torch.Tensor,
+                  seeds: torch.Tensor, positions: torch.Tensor,
+                  workspace: Optional[torch.Tensor] = None,
+                  out: Optional[torch.Tensor] = None,
+                  recompute_all: bool = False) -> torch.Tensor:
+    """Tokens int64 [M] drawn from the logits x @ weight^T without writing them: greedy rows
+    (temperature 0) take the argmax, the others the seeded Gumbel-max draw of
+    sid/engine/sampler.py:32-69 with no top-k / top-p limit. The logits are exactly those
+    of linear(..., out_fp32=True); needs linear_sample_supported(M, K). recompute_all scores
+    every column exactly instead of certifying per-wave candidates (a check; slow)."""
+    m, k = x.shape
+    ext = load_ext()
+    if workspace is None:
+        workspace = torch.empty(ext.linear_sample_workspace_bytes(m), dtype=torch.uint8,
+                                device=x.device)
+    if out is None:
+        out = torch.empty(m, dtype=torch.int64, device=x.device)
+    ext.linear_sample(x, weight, temperatures.float().contiguous(), seeds.long().contiguous(),
+                      positions.long().contiguous(), workspace, out, recompute_all)
+    return out

@@ -16,7 +16,7 @@ from sid.config import ModelConfig, decode_backend_kind
 from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.kernels.extend_attention import extend_attention_fwd
 from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_preferred,
-                                            linear_partials, linear_silu_mul,
+                                            linear_partials, linear_sample, linear_silu_mul,
                                             linear_silu_mul_preferred)
 from sid.kernels.ops import (argmax_rows, embedding, fused_add_rmsnorm_partials, gather_rows, qkv_post,
                              silu_mul, silu_mul_partials)
@@ -87,15 +87,19 @@ class Qwen3Model:
 
     @torch.inference_mode()
     def forward(self, fb: ForwardBatch, kv_cache, decode_attn,
-                decode_backend: str = "cuda", greedy: bool = False) -> torch.Tensor:
+                decode_backend: str = "cuda", greedy: bool = False,
+                sample: bool = False) -> torch.Tensor:
         """fp32 logits [R, vocab] for the sampled rows (bf16-rounded values); with
         greedy=True, the greedy tokens int64 [R] instead (argmax of those logits, fused into
-        the lm_head GEMM for decode-sized R).
+        the lm_head GEMM for decode-sized R); with sample=True (decode batches of at most 256
+        rows, no top-k / top-p limit), the sampled tokens int64 [R], drawn inside the lm_head
+        GEMM without writing the logits.
 
         Same op order as sid/model/qwen3.py:88-115; the residual add + RMSNorm that follows
         each o / down projection consumes the projection directly (fused), and the down
         projection of layer i feeds layer i+1's input norm (or the final norm)."""
         decode_backend = decode_backend_kind(decode_backend)
+        assert not sample or fb.mode == ForwardMode.DECODE, "fused sampling serves decode batches"
         if self.native_extend and fb.mode != ForwardMode.DECODE:
             return self._native_forward(fb, kv_cache, greedy)
         cfg = self.cfg
@@ -131,6 +135,10 @@ class Qwen3Model:
             else:
                 x, residual = fused_add_rmsnorm(linear(act, lw["down"]), residual, next_w, eps)
         rows = x if fb.sample_indices is None else gather_rows(x, fb.sample_indices)
+        if sample:  # the sampler fused into the lm_head (rows without top-k / top-p)
+            r = rows.shape[0]
+            return linear_sample(rows, self.w["lm_head"], fb.temperatures[:r], fb.seeds[:r],
+                                 fb.sample_positions[:r])
         if greedy:
             if linear_argmax_preferred(rows.shape[0], rows.shape[1]):
                 return linear_argmax(rows, self.w["lm_head"])

@@ -368,6 +368,27 @@ int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_extend_batch* b
                              void* stream);
 
 /*
+ * lm_head + sampler without the logits: out[r] = the token the sampler
+ * (sid/engine/sampler.py:32-69) draws from logits x[r] w^T (bf16 x [M, K] with
+ * row stride ldx, w [N, K], K = 1024, 1 <= M <= 256, N a multiple of 16):
+ * temperatures[r] <= 0: argmax (first index, NaN first); else
+ * argmax_c log(softmax(l / T)_c + 1e-10) + gumbel(seeds[r], positions[r], c)
+ * with the reference's hash, i.e. sample() with top_k <= 0 and top_p >= 1
+ * (rows with a top-k / top-p limit need sid_sample_rows over the logits).
+ * The logits have the bits of sid_linear's fp32 output. Workspace:
+ * sid_linear_sample_workspace_bytes(M) bytes, 16-byte aligned. Replaces the
+ * logits epilogue of Qwen3Model.forward (sid/model/qwen3.py:113-115) plus
+ * sample() for untruncated rows. flags: 0; 1 = recompute every column of every
+ * stochastic row exactly instead of certifying the per-wave candidates (a
+ * check of the certificate: same tokens, much slower).
+ */
+int64_t sid_linear_sample_workspace_bytes(int64_t m);
+int sid_linear_sample(const void* x, int64_t ldx, const void* w, int64_t m, int64_t n, int64_t k,
+                      const float* temperatures, const int64_t* seeds, const int64_t* positions,
+                      void* workspace, int64_t workspace_bytes, int64_t* out, int flags,
+                      void* stream);
+
+/*
  * out[r] = argmax(logits[r, :]) with first-index tie-break; fp32 logits
  * [rows, cols] with row stride ld; out int64 [rows]. NaN compares greater
  * than every number (torch.argmax semantics). Replaces the greedy branch of
