@@ -103,18 +103,20 @@ class DecodeWorkload:
         self.rollback()
         return toks
 
-    def rollback(self):
-        """Back to `context` positions per request: the page this step opened goes back to
-        the top of the free stack, so the next step takes the same one (identical work)."""
+    def rollback(self, extra: int = 0):
+        """Back to context + extra positions per request: a page the step opened beyond
+        them goes back to the top of the free stack, so the next step takes the same one
+        (identical work)."""
         for r in self.reqs:
-            self.kv.shrink(r.req_row, self.context)
+            self.kv.shrink(r.req_row, self.context + extra)
 
 
 def time_steps(wl, steps, warmup, pipelined=True):
     """Seconds per decode step. pipelined: step k+1 is launched before step k's tokens are
-    read back and its slots released, as the engine's overlapped decode runs
-    (EngineConfig.overlap_decode); every step still feeds the same positions, so each does
-    identical work. Otherwise one synchronous step at a time."""
+    read back, as the engine's overlapped decode runs (EngineConfig.overlap_decode): it
+    feeds step k's tokens, gathered on the device, one position further on (context
+    2048 + 2); the state is rolled back after each readback, so every step does the same
+    work. Otherwise one synchronous step at a time (context 2048 + 1)."""
     torch = wl.torch
     if not pipelined:
         for _ in range(warmup):
@@ -127,28 +129,38 @@ def time_steps(wl, steps, warmup, pipelined=True):
         return (time.perf_counter() - t0) / steps
     host = [torch.empty(len(wl.reqs), dtype=torch.int64, pin_memory=True) for _ in range(2)]
     turn = [0]
+    import numpy as np
+    rows = np.arange(len(wl.reqs), dtype=np.int64)
 
-    def launch():
-        fb = wl.build()
+    def launch(prev=None):
+        # As Engine._launch_decode: each request continues from its row of the step still
+        # in flight, whose token is gathered on the device (position one further on).
+        if prev is None:
+            fb = wl.build()
+        else:
+            fb = wl.runner.prepare_decode(wl.reqs, wl.invariant, prev_rows=rows,
+                                          prev_tokens=prev[3])
         tok = wl.runner.step(fb)
         h = host[turn[0]]
         turn[0] ^= 1
         h.copy_(tok, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()
-        return fb, h, ev
+        return fb, h, ev, tok
 
     def finish(step):
-        fb, h, ev = step
+        fb, h, ev, _ = step
         ev.synchronize()
         toks = h.tolist()
-        wl.rollback()  # same positions next time
+        # same positions next time; a step launched after the first feeds the previous
+        # step's token at position context + 1, whose page stays held
+        wl.rollback(extra=1)
         return toks
 
     def run(n):
         prev = launch()
         for _ in range(n - 1):
-            nxt = launch()
+            nxt = launch(prev)
             finish(prev)
             prev = nxt
         finish(prev)
@@ -371,7 +383,7 @@ def main():
         "config": {"workload": f"Qwen3-0.6B-shape decode step, batch {b}, context "
                                f"{args.context}+1, greedy, {args.mode} split policy, "
                                f"{'eager launches' if args.eager else 'HIP graph replay'}"
-                               f"{'' if (args.sync_steps or args.eager) else ', next step launched before the readback (overlapped decode)'}",
+                               f"{'' if (args.sync_steps or args.eager) else ', next step launched before the readback and fed its tokens on the device (overlapped decode; those steps run at context 2048+2)'}",
                    "batch": b, "context": args.context, "layers": wl.runner.mcfg.num_layers,
                    "mode": args.mode},
         "roofline": roof,

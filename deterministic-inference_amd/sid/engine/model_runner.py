@@ -7,7 +7,9 @@ change bits between runs of the same shape.
 
 from __future__ import annotations
 
+import gc
 import logging
+import weakref
 from collections import OrderedDict
 
 import torch
@@ -156,7 +158,10 @@ class GraphCache:
 
     def __init__(self, runner: "ModelRunner", max_graphs: int = 64):
         cfg = runner.cfg
-        self.runner = runner
+        # A weak back-reference: no runner <-> cache cycle, so a dropped runner (and its
+        # graphs) is freed at once by reference counting, never by a later garbage
+        # collection that could run in the middle of another graph's capture.
+        self._runner = weakref.ref(runner)
         self.max_graphs = max_graphs
         self.graphs: OrderedDict = OrderedDict()
         # Graphs of one kind replay in order on one stream and share a memory pool; decode
@@ -182,7 +187,7 @@ class GraphCache:
         return out
 
     def _capture(self, fb: ForwardBatch, greedy: bool, sample: bool):
-        runner = self.runner
+        runner = self._runner()
         kind = fb.graph_key[0]
         if kind not in self._warm:
             # One eager pass before the first capture of a kind, so lazy initialisation
@@ -193,6 +198,16 @@ class GraphCache:
             self._warm.add(kind)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, pool=self.pools[fb.graph_key[0]]):
-            out = runner._forward_eager(fb, greedy, sample)
+        # No garbage collection inside the capture: a collected object that owns device
+        # resources (a graph, an event, pinned memory) would release them with HIP calls
+        # that are illegal while a stream is being captured, and the process aborts.
+        gc.collect()
+        was_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.graph(graph, pool=self.pools[fb.graph_key[0]]):
+                out = runner._forward_eager(fb, greedy, sample)
+        finally:
+            if was_enabled:
+                gc.enable()
         return graph, out

@@ -117,3 +117,44 @@ def test_overlap_manual_step_loop_returns_every_slot():
     got = [eng.get_output(r).token_ids for r in rids]
     assert got == want
     assert eng.kv.free_count == free0
+
+
+def test_overlap_dvr_stop_tokens_and_rollbacks():
+    """dvr with stop tokens: a deterministic request may stop on a fast-path token while the
+    next step is in flight and be rolled back later (its finish cleared, decoding resumed,
+    the in-flight row discarded under the bumped epoch). Deterministic requests' tokens and
+    finish reasons equal the synchronous engine's, and every KV page comes back."""
+    prompts = _prompts(16, 15)
+    print("overlap dvr with stop tokens", flush=True)
+    g = torch.Generator().manual_seed(6)
+    lens = torch.randint(30, 90, (16,), generator=g).tolist()
+
+    def params(stops):
+        return [SamplingParams(max_new_tokens=lens[i], temperature=0.7 if i % 3 else 0.0,
+                               seed=11 + i, is_deterministic=i % 2 == 0,
+                               ignore_eos=stops is None,
+                               stop_token_ids=None if stops is None else [stops[i]])
+                for i in range(16)]
+
+    def run(overlap, ps):
+        eng = _engine(Mode.DVR, overlap, max_batch=8)
+        free0 = eng.kv.free_count
+        outs = eng.generate(prompts, ps)
+        assert eng._inflight is None
+        assert eng.kv.free_count == free0, "KV pages leaked"
+        return outs
+
+    base = run(False, params(None))
+    # a deterministic request's 6th committed token stops it (when it is not earlier too)
+    stops = [151935] * 16
+    for i in range(0, 16, 2):
+        t = base[i].token_ids
+        if len(t) > 8 and t[5] not in t[:5]:
+            stops[i] = t[5]
+    assert sum(s != 151935 for s in stops) >= 3
+    a, b = run(False, params(stops)), run(True, params(stops))
+    for i in range(0, 16, 2):
+        assert a[i].token_ids == b[i].token_ids, f"request {i}"
+        assert a[i].finish_reason == b[i].finish_reason
+    assert any(a[i].finish_reason == "stop" for i in range(0, 16, 2))
+    assert sum(o.num_rollbacks for o in b) > 0
