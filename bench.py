@@ -187,7 +187,7 @@ def attention_roofline(wl, reps):
     for layer in range(mcfg.num_layers):
         kp, vp = wl.kv.layer(layer)
         attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len, scale,
-                     wl.invariant)
+                     wl.invariant, policy_batch=fb.real_rows, variant=fb.decode_variant)
     torch.cuda.synchronize()
     # One event pair around reps x 28 back-to-back launches on the launch stream: the
     # average is the kernel's steady-state duration (launch overhead overlaps execution).
@@ -198,7 +198,8 @@ def attention_roofline(wl, reps):
         for layer in range(mcfg.num_layers):
             kp, vp = wl.kv.layer(layer)
             attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len,
-                         scale, wl.invariant)
+                         scale, wl.invariant, policy_batch=fb.real_rows,
+                         variant=fb.decode_variant)
             launches += 1
     end.record()
     torch.cuda.synchronize()
@@ -212,11 +213,14 @@ def attention_roofline(wl, reps):
     achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-            "kernel": "decode_stage1_kernel + decode_stage2_kernel (all-heads segments of "
-                      "<= 256 tokens, then the in-order merge)",
+            "kernel": f"decode_stage1_kernel (workgroup shape {VARIANT_NAMES[fb.decode_variant]}) "
+                      "+ decode_stage2_kernel (all-heads segments of <= 256 tokens, then the "
+                      "in-order merge)",
             "avg_launch_us": round(avg_ms * 1e3, 2), "bytes_per_launch": bytes_launch,
             "launches_timed": launches}
 
+
+VARIANT_NAMES = {0: "4 waves x 4 tokens", 1: "4 waves x 1 token", 2: "8 waves x 2 tokens"}
 
 TRAFFIC_FILE = ROOT / "profiles" / "decode_attention_b64_ctx2048_traffic.json"
 

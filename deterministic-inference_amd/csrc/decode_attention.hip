@@ -28,6 +28,7 @@
 // atomics, no dependence on batch composition or scheduling.
 #include "common.h"
 
+#include <cstdlib>
 #include <mutex>
 
 namespace sid {
@@ -330,23 +331,32 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_kernel(
   o[row * HEAD_DIM + d] = f32_to_bf16(num / den);
 }
 
-// Production configuration (the bits of a result depend on NW and TPL, which fix the
-// in-segment reduction order; they are constants, independent of batch and policy).
-constexpr int kWaves = 4;
-constexpr int kTokPerLane = 4;
+// Stage-1 shapes (waves per workgroup x tokens per wave iteration). They fix the in-segment
+// reduction order, so the bits of a result depend on the shape; every shape is a constant of
+// the call (sid_flash_decode_segments_fwd's `variant`), never of the data.
+//   0: 4 x 4  the default (the reference-signature entry points, batch_invariant)
+//   1: 4 x 1  fewest registers, 4 waves/SIMD: best when the grid is full and HBM-bound
+//   2: 8 x 2  half the per-wave round trips of a segment: best when fewer workgroups than CUs
+// (measured on 20 batch shapes, uniform and lognormal lengths, B = 1..256).
+constexpr int kNumVariants = 3;
 
-template <int NW = kWaves, int TPL = kTokPerLane>
 int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
                   int batch, int64_t num_slots, int fixed_split_size, int seg, int grid_slots,
                   float sm_scale, float* part_o, float* part_lse, int part_stride, void* o,
-                  hipStream_t s) {
+                  int variant, hipStream_t s) {
   const bool direct = (grid_slots == 1);
-  hipLaunchKernelGGL((decode_stage1_kernel<NW, TPL>), dim3(batch, grid_slots),
-                     dim3(NW * 64), 0, s, (const bf16_t*)q, (const bf16_t*)k_cache,
-                     (const bf16_t*)v_cache, kv_indptr, kv_indices, num_splits, fixed_split_size,
-                     seg, sm_scale, num_slots, part_stride, part_o, part_lse,
-                     direct ? (bf16_t*)o : nullptr);
+  auto stage1 = [&](auto kern, int nw) {
+    hipLaunchKernelGGL(kern, dim3(batch, grid_slots), dim3(nw * 64), 0, s, (const bf16_t*)q,
+                       (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr, kv_indices,
+                       num_splits, fixed_split_size, seg, sm_scale, num_slots, part_stride, part_o,
+                       part_lse, direct ? (bf16_t*)o : nullptr);
+  };
+  switch (variant) {
+    case 1: stage1(decode_stage1_kernel<4, 1>, 4); break;
+    case 2: stage1(decode_stage1_kernel<8, 2>, 8); break;
+    default: stage1(decode_stage1_kernel<4, 4>, 4); break;
+  }
   int rc = check_launch("flash_decode_fwd stage1");
   if (rc != SID_OK || direct) return rc;
   hipLaunchKernelGGL(decode_stage2_kernel, dim3(HQ, batch), dim3(HEAD_DIM), 0, s, part_o, part_lse,
@@ -384,9 +394,11 @@ extern "C" int sid_flash_decode_segments_fwd(
     const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
     const int32_t* kv_indices, const int32_t* num_splits, int batch, int num_q_heads,
     int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
-    int segment_size, int grid_slots, float sm_scale, float* part_o, float* part_lse,
-    int part_batch, int part_stride, void* o, void* stream) {
+    int segment_size, int grid_slots, int variant, float sm_scale, float* part_o,
+    float* part_lse, int part_batch, int part_stride, void* o, void* stream) {
   SID_REQUIRE(batch >= 0, "flash_decode_fwd: negative batch");
+  SID_REQUIRE(variant >= 0 && variant < kNumVariants, "flash_decode_fwd: unknown variant %d",
+              variant);
   if (batch == 0) return SID_OK;
   int rc = check_decode_args(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, o, batch,
                              num_q_heads, num_kv_heads, head_dim, num_slots, max_splits,
@@ -404,7 +416,7 @@ extern "C" int sid_flash_decode_segments_fwd(
   }
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, batch, num_slots,
                        fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       part_stride, o, static_cast<hipStream_t>(stream));
+                       part_stride, o, variant, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -417,7 +429,7 @@ extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const vo
   // One segment per split: the grid has exactly the reference's max_splits slots.
   return sid_flash_decode_segments_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                        batch, num_q_heads, num_kv_heads, head_dim, num_slots,
-                                       max_splits, fixed_split_size, 0, max_splits, sm_scale,
+                                       max_splits, fixed_split_size, 0, max_splits, 0, sm_scale,
                                        part_o, part_lse, part_batch, part_stride, o, stream);
 }
 
@@ -467,9 +479,11 @@ extern "C" int sid_flash_decode_segments_fwd_noalloc(
     const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
     const int32_t* kv_indices, const int32_t* num_splits, int batch, int num_q_heads,
     int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
-    int segment_size, int grid_slots, float sm_scale, void* o, void* stream) {
+    int segment_size, int grid_slots, int variant, float sm_scale, void* o, void* stream) {
   using namespace sid;
   SID_REQUIRE(batch >= 0, "flash_decode_fwd_noalloc: negative batch");
+  SID_REQUIRE(variant >= 0 && variant < kNumVariants,
+              "flash_decode_fwd_noalloc: unknown variant %d", variant);
   if (batch == 0) return SID_OK;
   int rc = check_decode_args(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, o, batch,
                              num_q_heads, num_kv_heads, head_dim, num_slots, max_splits,
@@ -499,5 +513,5 @@ extern "C" int sid_flash_decode_segments_fwd_noalloc(
   // Stage 2 reads only the slots stage 1 wrote in this call, so nothing is cleared.
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, batch, num_slots,
                        fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       grid_slots, o, static_cast<hipStream_t>(stream));
+                       grid_slots, o, variant, static_cast<hipStream_t>(stream));
 }

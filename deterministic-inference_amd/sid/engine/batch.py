@@ -59,6 +59,8 @@ class ForwardBatch:
     # start of the forward (inside the graph) instead of by the builder
     index_build: Optional[tuple] = None
     new_slots_host: Optional[np.ndarray] = None  # decode: the KV slot each row writes
+    seq_lens_host: Optional[np.ndarray] = None  # decode: kv length of each real row
+    decode_variant: int = 0  # decode: stage-1 workgroup shape of the attention kernel
 
     def build_indices(self) -> None:
         """Enqueue the deferred kv_indices build (a no-op when the builder already ran it).
@@ -269,5 +271,5 @@ def build_decode_batch(reqs: list, kv, device: str, invariant: bool,
         temperatures=d_temps, top_ks=d_topk, top_ps=d_topp, seeds=d_seed,
         invariant=invariant, all_greedy=bool((temps == 0).all()),
         untruncated=_untruncated(top_ks, top_ps), real_rows=bs if d_ids.shape[0] != bs else None,
-        index_build=index_build, new_slots_host=new_slots,
+        index_build=index_build, new_slots_host=new_slots, seq_lens_host=seq_lens,
     )

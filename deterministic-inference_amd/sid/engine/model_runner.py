@@ -19,7 +19,8 @@ from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_buc
                               build_decode_batch, gather_prev_tokens)
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
-from sid.kernels.decode_attention import DecodeAttention, length_bucket, nondet_geometry
+from sid.kernels.decode_attention import (DecodeAttention, length_bucket, nondet_geometry,
+                                          nonempty_workgroups, stage1_variant)
 from sid.kernels.matmul_persistent import linear_sample_supported
 from sid.model.loader import build_model_config, load_weights, random_weights
 from sid.model.qwen3 import Qwen3Model
@@ -118,7 +119,10 @@ class ModelRunner:
         flight: row prev_rows[i] of prev_tokens, gathered on the device."""
         if self.graphs is None:
             assert prev_rows is None or not (prev_rows >= 0).any(), "a pending token needs graphs"
-            return build_decode_batch(reqs, self.kv_cache, self.device, invariant)
+            fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant)
+            if not invariant:
+                self._pick_variant(fb, len(reqs), fb.max_seq_len)
+            return fb
         static = self.graphs.decode_static
         pad = batch_bucket(len(reqs), static.max_bs)
         fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant,
@@ -130,11 +134,24 @@ class ModelRunner:
         # nondet plan follows the real request count, so it is part of the key.
         bucket = length_bucket(fb.max_seq_len)
         fb.max_seq_len = bucket
-        plan = None if invariant else nondet_geometry(
-            len(reqs), bucket, self.mcfg.num_kv_heads, self.decode_attn.cu_count(),
-            self.cfg.max_kv_splits)
-        fb.graph_key = ("decode", pad, invariant, bucket, plan)
+        plan = None
+        if not invariant:
+            plan = self._pick_variant(fb, len(reqs), bucket)
+        fb.graph_key = ("decode", pad, invariant, bucket, plan, fb.decode_variant)
         return fb
+
+    def _pick_variant(self, fb: ForwardBatch, bs: int, max_len: int) -> tuple:
+        """The nondet plan's geometry and its stage-1 workgroup shape (fb.decode_variant),
+        from the requests' host-known lengths."""
+        cu = self.decode_attn.cu_count()
+        splits, seg, slots = nondet_geometry(bs, max_len, self.mcfg.num_kv_heads, cu,
+                                             self.cfg.max_kv_splits)
+        lens = fb.seq_lens_host
+        wg = nonempty_workgroups(lens, splits, seg)
+        # the grid the batch would fill if every request were as long as its longest one
+        full = bs * nonempty_workgroups([int(lens.max())], splits, seg) if len(lens) else 0
+        fb.decode_variant = stage1_variant(wg, full, cu, invariant=False)
+        return splits, seg, slots
 
     def tag_verify(self, fb: ForwardBatch) -> ForwardBatch:
         """Verify batches always live in the persistent verify buffers: graph them."""

@@ -26,6 +26,7 @@ from __future__ import annotations
 
 import functools
 
+import numpy as np
 import torch
 
 from sid.kernels.jit import load_ext
@@ -85,6 +86,44 @@ def nondet_geometry(batch: int, max_len: int, num_kv_heads: int, cu_count: int,
     return splits, seg, splits * max(1, _cdiv(chunk_max, seg))
 
 
+def nonempty_workgroups(lengths, splits: int, seg: int) -> int:
+    """Stage-1 workgroups of a nondet/dvr plan that hold tokens: per request of length n,
+    its min(splits, ceil(n/32)) splits of kv_per_split tokens, each cut into segments of at
+    most seg (host-side, from the requests' lengths)."""
+    lens = np.asarray(lengths, dtype=np.int64)
+    lens = lens[lens > 0]
+    if lens.size == 0:
+        return 0
+    n = np.minimum(splits, -(-lens // 32))
+    chunk = -(-(-(-lens // n)) // 32) * 32
+    sl = np.minimum(seg, chunk)
+    total = 0
+    for s in range(int(n.max())):
+        part = np.clip(lens - s * chunk, 0, chunk)
+        total += int((-(-part // sl) * (s < n)).sum())
+    return total
+
+
+# Stage-1 workgroup shapes (sid_flash_decode_segments_fwd `variant`): 0 = 4 waves x 4 tokens
+# per iteration, 1 = 4 x 1, 2 = 8 x 2. The shape is part of the in-segment reduction order.
+# batch_invariant keeps 0 for every batch (results depend on the request alone); nondet/dvr
+# pick by the number of non-empty workgroups W against the CU count, measured on 20 shapes
+# (uniform and lognormal lengths, B = 1..256): a full grid of at least two workgroups per CU
+# is HBM-bound and runs best with the fewest registers (1: config 3, 91.5 -> 88.9 us); fewer
+# workgroups than CUs are bound by each workgroup's chain of round trips (2: lognormal
+# B = 64, 77.7 -> 60.1 us; B = 1, ctx 1024, 13.3 -> 12.5 us); 0 in between.
+def stage1_variant(workgroups: int, grid_workgroups: int, cu_count: int, invariant: bool) -> int:
+    """grid_workgroups: the non-empty workgroups if every request were as long as the longest
+    (workgroups / grid_workgroups < 1 measures how ragged the batch is)."""
+    if invariant:
+        return 0
+    if workgroups >= 2 * cu_count and workgroups >= 0.9 * grid_workgroups:
+        return 1
+    if workgroups < cu_count:
+        return 2
+    return 0
+
+
 def workspace_slots(max_seq_len: int, max_kv_splits: int, invariant_split_size: int) -> int:
     """Partial slots per request the workspace must hold for any plan."""
     nondet = -(-max_seq_len // SEGMENT_SIZES[-1]) + max_kv_splits
@@ -142,9 +181,11 @@ class DecodeAttention:
     def forward(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, seq_lens: torch.Tensor,
                 max_seq_len: int, sm_scale: float, invariant: bool,
-                policy_batch: int | None = None) -> torch.Tensor:
+                policy_batch: int | None = None, variant: int = 0) -> torch.Tensor:
         """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync).
-        policy_batch: real requests among the B rows (the rest are empty padding)."""
+        policy_batch: real requests among the B rows (the rest are empty padding); variant:
+        the stage-1 workgroup shape (stage1_variant; 0 in batch_invariant mode)."""
+        assert not (invariant and variant), "batch_invariant mode keeps the default shape"
         bs = q.shape[0]
         assert bs <= self.part_o.shape[0], "decode batch exceeds workspace"
         # One plan per forward: every layer sees the same seq_lens tensor.
@@ -159,5 +200,5 @@ class DecodeAttention:
         o = torch.empty_like(q)
         self.ext.flash_decode_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                   grid_splits, fixed, sm_scale, self.part_o, self.part_lse, o,
-                                  segment_size=seg, grid_slots=slots)
+                                  segment_size=seg, grid_slots=slots, variant=variant)
         return o

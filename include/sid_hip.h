@@ -84,15 +84,20 @@ int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache
  * one workgroup per head and split; here a workgroup reads all heads of its
  * tokens), and it is part of the reduction order: with a fixed split size
  * and a fixed segment size the result depends on the request alone. When
- * grid_slots == 1 the workspace is not touched.
+ * grid_slots == 1 the workspace is not touched. variant picks the stage-1
+ * workgroup shape, which is part of the in-segment reduction order: 0 = 4
+ * waves x 4 tokens per wave iteration (what sid_flash_decode_fwd uses), 1 =
+ * 4 x 1 (full, HBM-bound grids), 2 = 8 x 2 (fewer workgroups than CUs); a
+ * fixed variant keeps the batch independence of fixed splits.
  */
 int sid_flash_decode_segments_fwd(const void* q, const void* k_cache, const void* v_cache,
                                   const int32_t* kv_indptr, const int32_t* kv_indices,
                                   const int32_t* num_splits, int batch, int num_q_heads,
                                   int num_kv_heads, int head_dim, int64_t num_slots,
                                   int max_splits, int fixed_split_size, int segment_size,
-                                  int grid_slots, float sm_scale, float* part_o, float* part_lse,
-                                  int part_batch, int part_stride, void* o, void* stream);
+                                  int grid_slots, int variant, float sm_scale, float* part_o,
+                                  float* part_lse, int part_batch, int part_stride, void* o,
+                                  void* stream);
 
 /*
  * No counterpart in the reference. For callers that cannot allocate device
@@ -116,7 +121,7 @@ int sid_flash_decode_segments_fwd_noalloc(const void* q, const void* k_cache,
                                           int batch, int num_q_heads, int num_kv_heads,
                                           int head_dim, int64_t num_slots, int max_splits,
                                           int fixed_split_size, int segment_size,
-                                          int grid_slots, float sm_scale, void* o,
+                                          int grid_slots, int variant, float sm_scale, void* o,
                                           void* stream);
 
 /* Size of that scratch array in bytes (SID_DECODE_SCRATCH_BYTES). */

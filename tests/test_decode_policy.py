@@ -104,3 +104,33 @@ def test_decode_backend_names():
     assert EngineConfig().decode_backend == "hip"
     with pytest.raises(ValueError):
         EngineConfig(decode_backend="cuDNN")
+
+
+def test_nonempty_workgroups_brute_force():
+    """Counted segment by segment with the oracle's split ranges."""
+    import numpy as np
+    from oracle.attention import kv_per_split, split_ranges
+    from sid.kernels.decode_attention import nonempty_workgroups
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        lens = rng.integers(0, 5000, size=int(rng.integers(1, 20))).tolist()
+        splits = int(rng.integers(1, 33))
+        seg = int(rng.choice([64, 128, 256]))
+        want = 0
+        for n in lens:
+            ns = min(splits, -(-n // 32))
+            if n == 0:
+                continue
+            sl = min(seg, kv_per_split(n, ns, 0))
+            for a, b in split_ranges(n, ns, 0):
+                want += len(range(a, b, sl))
+        assert nonempty_workgroups(lens, splits, seg) == want, (lens, splits, seg)
+
+
+def test_stage1_variant_rule():
+    from sid.kernels.decode_attention import stage1_variant
+    assert stage1_variant(576, 576, 256, invariant=False) == 1     # full, >= 2 per CU
+    assert stage1_variant(576, 576, 256, invariant=True) == 0      # invariant: fixed shape
+    assert stage1_variant(230, 896, 256, invariant=False) == 2     # fewer than the CUs
+    assert stage1_variant(600, 2176, 256, invariant=False) == 0    # ragged, in between
+    assert stage1_variant(32, 32, 256, invariant=False) == 2

@@ -36,8 +36,12 @@ pytestmark = pytest.mark.gpu
 def _check(logits, ref):
     """28 layers at full context: bf16 rounding flips compound over depth, so the bar is
     statistical: mean |error| < 2e-2 (about one bf16 ulp at |logit| ~ 2), fewer than 1 in
-    10^4 logits off by more than 0.1 (measured: 1-2 in 10^5), none by more than 0.25; argmax equal on every row
-    unless the oracle's top two logits are within 0.05 (a near-tie either side may break)."""
+    10^4 logits off by more than 0.1 (measured: 1-2 in 10^5), none by more than 0.25.
+    Argmax: a row whose token differs from the oracle's must be a near-tie within the
+    measured error band (the oracle's gap between the two tokens below twice the largest
+    error on this batch: two logits moving that far in opposite directions). The random-init
+    model's logits are flat (top-2 gaps ~0.1, the size of 28 layers of bf16 noise), so some
+    rows do flip; at least half must agree exactly (garbage would agree on none)."""
     got = logits.float().cpu()
     err = (got - ref).abs()
     print(f"logits vs oracle: mean {err.mean().item():.2e}  max {err.max().item():.3f}  "
@@ -46,10 +50,14 @@ def _check(logits, ref):
     assert (err > 0.1).float().mean().item() < 1e-4
     assert err.max().item() < 0.25
     a, b = got.argmax(-1), ref.argmax(-1)
+    band = 2 * err.max().item()
+    agree = (a == b).float().mean().item()
+    print(f"argmax agreement {agree:.3f}", flush=True)
+    assert agree >= 0.5
     for r in range(ref.shape[0]):
         if a[r] != b[r]:
             gap = (ref[r, b[r]] - ref[r, a[r]]).item()
-            assert gap < 0.05, f"row {r}: argmax {a[r]} vs oracle {b[r]} (oracle gap {gap})"
+            assert gap < band, f"row {r}: argmax {a[r]} vs oracle {b[r]} (gap {gap}, band {band})"
 
 
 def _compact(kv, fb, layers):

@@ -26,7 +26,7 @@ def _ext():
     return load_ext()
 
 
-def _run(q, k, v, indptr, idx, num_splits, grid, fixed, seg=0, slots=None):
+def _run(q, k, v, indptr, idx, num_splits, grid, fixed, seg=0, slots=None, variant=0):
     bs = q.shape[0]
     slots = grid if slots is None else slots
     part_o = torch.full((bs, HQ, max(slots, 1), D), float("nan"), device="cuda")
@@ -34,7 +34,7 @@ def _run(q, k, v, indptr, idx, num_splits, grid, fixed, seg=0, slots=None):
     o = torch.empty_like(q)
     ns = torch.tensor(num_splits, dtype=torch.int32, device="cuda")
     _ext().flash_decode_fwd(q, k, v, indptr, idx, ns, grid, fixed, SCALE, part_o, part_lse, o,
-                            segment_size=seg, grid_slots=slots)
+                            segment_size=seg, grid_slots=slots, variant=variant)
     return o
 
 
@@ -81,17 +81,34 @@ def test_decode_vs_oracle(seq_lens, policy):
 @pytest.mark.parametrize("seq_lens", CASES, ids=lambda s: f"b{len(s)}_max{max(s)}")
 @pytest.mark.parametrize("policy", ["heuristic", "fixed256", "splits1", "splits8"])
 @pytest.mark.parametrize("seg", [64, 128, 256])
-def test_decode_segments_vs_oracle(seq_lens, policy, seg):
+@pytest.mark.parametrize("variant", [0, 1, 2])
+def test_decode_segments_vs_oracle(seq_lens, policy, seg, variant):
     """Splits cut into segments of <= seg tokens (one workgroup each), merged in token
-    order by stage 2. Workspace pre-filled with NaN: a slot read but never written, or a
-    token dropped, shows up."""
+    order by stage 2, for every stage-1 workgroup shape. Workspace pre-filled with NaN: a
+    slot read but never written, or a token dropped, shows up."""
     q, k, v, indptr, idx = decode_inputs(seq_lens)
     ns, grid, fixed = _policy(seq_lens, policy)
     slots = _slots(seq_lens, ns, fixed, seg)
-    print(f"lens={seq_lens[:4]} policy={policy} seg={seg} slots={slots}", flush=True)
-    out = _run(q, k, v, indptr, idx, ns, grid, fixed, seg, slots)
+    print(f"lens={seq_lens[:4]} policy={policy} seg={seg} slots={slots} variant={variant}",
+          flush=True)
+    out = _run(q, k, v, indptr, idx, ns, grid, fixed, seg, slots, variant)
     ref = decode_attention_ref(q, k, v, indptr, idx, SCALE)
     assert_close_bf16(out, ref)
+
+
+@pytest.mark.parametrize("variant", [1, 2])
+def test_variant_changes_bits_but_is_run_to_run_stable(variant):
+    """The workgroup shape is part of the reduction order: another shape gives other bits
+    (within tolerance), the same shape the same bits on every run."""
+    lens = [1500, 2049, 700]
+    q, k, v, indptr, idx = decode_inputs(lens, seed=9)
+    ns, grid, fixed = _policy(lens, "fixed256")
+    slots = _slots(lens, ns, fixed, 256)
+    base = _run(q, k, v, indptr, idx, ns, grid, fixed, 256, slots, 0)
+    a = _run(q, k, v, indptr, idx, ns, grid, fixed, 256, slots, variant)
+    b = _run(q, k, v, indptr, idx, ns, grid, fixed, 256, slots, variant)
+    assert torch.equal(a, b) and not torch.equal(a, base)
+    assert_close_bf16(a, base)
 
 
 @pytest.mark.parametrize("invariant", [False, True])
