@@ -220,7 +220,8 @@ def attention_roofline(wl, reps):
             "launches_timed": launches}
 
 
-VARIANT_NAMES = {0: "4 waves x 4 tokens", 1: "4 waves x 1 token", 2: "8 waves x 2 tokens"}
+VARIANT_NAMES = {0: "4 waves x 4 tokens", 1: "4 waves x 1 token", 2: "8 waves x 2 tokens",
+                 3: "4 waves x 2 tokens"}
 
 TRAFFIC_FILE = ROOT / "profiles" / "decode_attention_b64_ctx2048_traffic.json"
 

@@ -69,47 +69,85 @@ def _paged(num_pages, lens, rng):
 
 
 def _attn_case(q, k, v, indptr, idx, lens):
-    from sid.kernels.decode_attention import DecodeAttention
+    """Both split policies as the engine plans them (nondet: the heuristic splits, segment
+    size and stage-1 workgroup shape; batch_invariant: fixed 256-token splits), timed as the
+    model runs them: the plan once, then back-to-back kernel launches."""
+    from sid.kernels.decode_attention import DecodeAttention, plan_variant
+    from sid.kernels.jit import load_ext
+    ext = load_ext()
     attn = DecodeAttention(len(lens), HQ, HKV, D, 32, 256, 32768, "cuda")
     seq = torch.tensor(lens, dtype=torch.int32, device="cuda")
     bytes_ = sum(lens) * (HKV * D * 2 * 2 + 4) + 2 * len(lens) * HQ * D * 2
     out = {}
+    o = torch.empty_like(q)
     for name, inv in (("nondet", False), ("fixed256", True)):
-        us = _time_us(lambda: attn.forward(q, k, v, indptr, idx, seq, max(lens), D ** -0.5, inv))
-        ns, grid, _, seg, slots = attn.plan(seq, max(lens), inv)
+        ns, grid, fixed, seg, slots = attn.plan(seq, max(lens), inv)
+        _, variant = plan_variant(lens, max(lens), HKV, attn.cu_count(), 32, inv)
+        fn = lambda: ext.flash_decode_fwd(q, k, v, indptr, idx, ns, grid, fixed, D ** -0.5,
+                                          attn.part_o, attn.part_lse, o, segment_size=seg,
+                                          grid_slots=slots, variant=variant)
+        us = _time_us(fn)
         out[name] = {"us_per_call": round(us, 2), "GB_s": round(bytes_ / us / 1e3, 1),
                      "frac_of_hbm_peak": round(bytes_ / us / 1e3 / HBM_PEAK_GBS, 4),
-                     "grid_splits": grid, "segment_tokens": seg, "grid_slots": slots}
-    return out, attn, seq
+                     "grid_splits": grid, "segment_tokens": seg, "grid_slots": slots,
+                     "stage1_variant": variant}
+    return out, attn, seq, bytes_
+
+
+def _cpu_attention(q, k, v, indptr, idx, min_seconds):
+    """The CPU oracle (oracle/attention.py decode_attention_ref) on the same inputs, repeated
+    for at least min_seconds; -> (us per call, reference output)."""
+    from oracle.attention import decode_attention_ref
+    from bench import host_threads
+    torch.set_num_threads(host_threads())
+    qc, kc, vc, ic, pc = q.cpu(), k.cpu(), v.cpu(), idx.cpu(), indptr.cpu()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < min_seconds or n < 2:
+        ref = decode_attention_ref(qc, kc, vc, pc, ic, D ** -0.5)
+        n += 1
+    return (time.perf_counter() - t0) / n * 1e6, ref, n
+
+
+def _line(metric, value, unit, higher, workload, roof, cpu, extra):
+    from bench import cpu_model, host_threads
+    out = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": 50,
+           "warmup": 5, "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
+           "dtype": "bf16", "data": "synthetic: N(0,1) q/K/V, seeded page-shuffled block tables",
+           "config": {"workload": workload}, "roofline": roof,
+           "cpu_baseline": dict(cpu, cores=host_threads(), kind="port",
+                                host_cpus=os.cpu_count(), cpu_model=cpu_model())}
+    out.update(extra)
+    return out
+
+
+def _roof(bytes_, us, kernel):
+    gbs = bytes_ / us / 1e3
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
+            "avg_launch_us": round(us, 2), "bytes_per_launch": int(bytes_)}
 
 
 def config1(args):
-    from oracle.attention import decode_attention_ref
     g = torch.Generator(device="cuda").manual_seed(1)
     q = torch.randn(1, HQ, D, device="cuda", generator=g).to(torch.bfloat16)
     k = torch.randn(4096, HKV, D, device="cuda", generator=g).to(torch.bfloat16)
     v = torch.randn(4096, HKV, D, device="cuda", generator=g).to(torch.bfloat16)
     idx, indptr = _paged(256, [1024], np.random.default_rng(1))
-    res, attn, seq = _attn_case(q, k, v, indptr, idx, [1024])
-    qc, kc, vc, ic, pc = q.cpu(), k.cpu(), v.cpu(), idx.cpu(), indptr.cpu()
-    from bench import cpu_model, host_threads
-    torch.set_num_threads(host_threads())
-    t0 = time.perf_counter()
-    n = 0
-    while time.perf_counter() - t0 < 2.0:
-        ref = decode_attention_ref(qc, kc, vc, pc, ic, D ** -0.5)
-        n += 1
-    cpu_us = (time.perf_counter() - t0) / n * 1e6
+    res, attn, seq, bytes_ = _attn_case(q, k, v, indptr, idx, [1024])
+    cpu_us, ref, n = _cpu_attention(q, k, v, indptr, idx, 2.0)
     o = attn.forward(q, k, v, indptr, idx, seq, 1024, D ** -0.5, False)
     err = (o.float().cpu() - ref).abs().max().item()
-    return {"metric": "decode attention op latency, B=1 ctx 1024 page 16 (config 1)",
-            "value": res["nondet"]["us_per_call"], "unit": "us", "higher_is_better": False,
-            "policies": res, "max_abs_err_vs_oracle": err,
-            "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us", "kind": "port",
-                             "cores": torch.get_num_threads(), "host_cpus": os.cpu_count(),
-                             "cpu_model": cpu_model(),
-                             "sample": "oracle.attention.decode_attention_ref, same inputs"},
-            "note": "one request of 1024 tokens is launch/latency bound (4 MiB of K/V)"}
+    us = res["nondet"]["us_per_call"]
+    return _line("decode attention op latency, B=1 ctx 1024 page 16 (config 1)", us, "us", False,
+                 "split-KV decode attention, one request of 1024 tokens in 16-token pages of a "
+                 "256-page shuffled pool, nondet split plan (the reference's heuristic: 32 splits "
+                 "of 32 tokens)",
+                 _roof(bytes_, us, f"decode_stage1_kernel (variant {res['nondet']['stage1_variant']}) + decode_stage2_kernel"),
+                 {"value": round(cpu_us, 1), "unit": "us",
+                  "sample": f"oracle.attention.decode_attention_ref on the same inputs, {n} calls"},
+                 {"policies": res, "max_abs_err_vs_oracle": err,
+                  "note": "4 MiB of K/V: two launches whose fixed latency dominates"})
 
 
 def config2(args):
@@ -128,12 +166,23 @@ def config2(args):
     ext = load_ext()
     us_cache = _time_us(lambda: ext.reshape_and_cache(kn, vn, k, v, new_slots))
     exact = bool(torch.equal(k[new_slots], kn) and torch.equal(v[new_slots], vn))
-    res, _, _ = _attn_case(q, k, v, indptr, idx, lens)
-    return {"metric": "cache write + decode attention, B=32 ctx U[128,4096] (config 2)",
-            "value": res["nondet"]["GB_s"], "unit": "GB/s", "higher_is_better": True,
-            "policies": res, "sum_ctx": int(sum(lens)),
-            "reshape_and_cache": {"us_per_call": round(us_cache, 2), "bit_exact": exact,
-                                  "bytes": 32 * HKV * D * 2 * 2 * 2}}
+    res, attn, seq, bytes_ = _attn_case(q, k, v, indptr, idx, lens)
+    cpu_us, ref, n = _cpu_attention(q, k, v, indptr, idx, 3.0)
+    o = attn.forward(q, k, v, indptr, idx, seq, max(lens), D ** -0.5, False)
+    err = (o.float().cpu() - ref).abs().max().item()
+    us = res["nondet"]["us_per_call"]
+    return _line("cache write + decode attention, B=32 ctx U[128,4096] (config 2)",
+                 res["nondet"]["GB_s"], "GB/s", True,
+                 "reshape_and_cache of 32 new K/V rows into a 32k-page x 16 pool, then split-KV "
+                 f"decode attention over sum(ctx) = {sum(lens)} tokens in shuffled pages, nondet "
+                 "plan (the fixed-256 policy beside it in `policies`)",
+                 _roof(bytes_, us, f"decode_stage1_kernel (variant {res['nondet']['stage1_variant']}) + decode_stage2_kernel"),
+                 {"value": round(bytes_ / cpu_us / 1e3, 2), "unit": "GB/s",
+                  "sample": f"oracle.attention.decode_attention_ref on the same batch, {n} calls, "
+                            f"{cpu_us / 1e3:.1f} ms each"},
+                 {"policies": res, "max_abs_err_vs_oracle": err, "sum_ctx": int(sum(lens)),
+                  "reshape_and_cache": {"us_per_call": round(us_cache, 2), "bit_exact": exact,
+                                        "bytes": 32 * HKV * D * 2 * 2 * 2}})
 
 
 def _engine(mode, layers=None, pool=None, max_reqs=64, seq=4096, batch=64):

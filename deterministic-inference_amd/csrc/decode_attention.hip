@@ -337,8 +337,9 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_kernel(
 //   0: 4 x 4  the default (the reference-signature entry points, batch_invariant)
 //   1: 4 x 1  fewest registers, 4 waves/SIMD: best when the grid is full and HBM-bound
 //   2: 8 x 2  half the per-wave round trips of a segment: best when fewer workgroups than CUs
+//   3: 4 x 2  between the two: grids of one to two workgroups per CU
 // (measured on 20 batch shapes, uniform and lognormal lengths, B = 1..256).
-constexpr int kNumVariants = 3;
+constexpr int kNumVariants = 4;
 
 int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
@@ -355,6 +356,7 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
   switch (variant) {
     case 1: stage1(decode_stage1_kernel<4, 1>, 4); break;
     case 2: stage1(decode_stage1_kernel<8, 2>, 8); break;
+    case 3: stage1(decode_stage1_kernel<4, 2>, 4); break;
     default: stage1(decode_stage1_kernel<4, 4>, 4); break;
   }
   int rc = check_launch("flash_decode_fwd stage1");

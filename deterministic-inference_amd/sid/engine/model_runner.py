@@ -19,8 +19,7 @@ from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_buc
                               build_decode_batch, gather_prev_tokens)
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
-from sid.kernels.decode_attention import (DecodeAttention, length_bucket, nondet_geometry,
-                                          nonempty_workgroups, stage1_variant)
+from sid.kernels.decode_attention import DecodeAttention, length_bucket, plan_variant
 from sid.kernels.matmul_persistent import linear_sample_supported
 from sid.model.loader import build_model_config, load_weights, random_weights
 from sid.model.qwen3 import Qwen3Model
@@ -143,15 +142,11 @@ class ModelRunner:
     def _pick_variant(self, fb: ForwardBatch, bs: int, max_len: int) -> tuple:
         """The nondet plan's geometry and its stage-1 workgroup shape (fb.decode_variant),
         from the requests' host-known lengths."""
-        cu = self.decode_attn.cu_count()
-        splits, seg, slots = nondet_geometry(bs, max_len, self.mcfg.num_kv_heads, cu,
-                                             self.cfg.max_kv_splits)
-        lens = fb.seq_lens_host
-        wg = nonempty_workgroups(lens, splits, seg)
-        # the grid the batch would fill if every request were as long as its longest one
-        full = bs * nonempty_workgroups([int(lens.max())], splits, seg) if len(lens) else 0
-        fb.decode_variant = stage1_variant(wg, full, cu, invariant=False)
-        return splits, seg, slots
+        geom, fb.decode_variant = plan_variant(fb.seq_lens_host, max_len,
+                                               self.mcfg.num_kv_heads,
+                                               self.decode_attn.cu_count(),
+                                               self.cfg.max_kv_splits, invariant=False)
+        return geom
 
     def tag_verify(self, fb: ForwardBatch) -> ForwardBatch:
         """Verify batches always live in the persistent verify buffers: graph them."""

@@ -105,13 +105,16 @@ def nonempty_workgroups(lengths, splits: int, seg: int) -> int:
 
 
 # Stage-1 workgroup shapes (sid_flash_decode_segments_fwd `variant`): 0 = 4 waves x 4 tokens
-# per iteration, 1 = 4 x 1, 2 = 8 x 2. The shape is part of the in-segment reduction order.
-# batch_invariant keeps 0 for every batch (results depend on the request alone); nondet/dvr
-# pick by the number of non-empty workgroups W against the CU count, measured on 20 shapes
-# (uniform and lognormal lengths, B = 1..256): a full grid of at least two workgroups per CU
-# is HBM-bound and runs best with the fewest registers (1: config 3, 91.5 -> 88.9 us); fewer
-# workgroups than CUs are bound by each workgroup's chain of round trips (2: lognormal
-# B = 64, 77.7 -> 60.1 us; B = 1, ctx 1024, 13.3 -> 12.5 us); 0 in between.
+# per iteration, 1 = 4 x 1, 2 = 8 x 2, 3 = 4 x 2. The shape is part of the in-segment
+# reduction order. batch_invariant keeps 0 for every batch (results depend on the request
+# alone); nondet/dvr pick by the number of non-empty workgroups W against the CU count and by
+# how ragged the batch is, measured on 20 shapes (uniform and lognormal lengths, B = 1..256):
+# a full grid of at least two workgroups per CU is HBM-bound and runs best with the fewest
+# registers (1: config 3, 91.5 -> 88.9 us); fewer workgroups than CUs are bound by each
+# workgroup's chain of round trips (2: lognormal B = 64, 77.7 -> 60.1 us; B = 1, ctx 1024,
+# 13.3 -> 12.5 us); a grid at least half as full as its longest request would make it runs
+# best with 3 (config 2, 59.3 -> 56.1 us; uniform B = 48 x 2k, 73.6 -> 70.3 us); very ragged
+# batches with 0 (lognormal B = 128, 130.9 us against 142.0 with 3).
 def stage1_variant(workgroups: int, grid_workgroups: int, cu_count: int, invariant: bool) -> int:
     """grid_workgroups: the non-empty workgroups if every request were as long as the longest
     (workgroups / grid_workgroups < 1 measures how ragged the batch is)."""
@@ -121,7 +124,24 @@ def stage1_variant(workgroups: int, grid_workgroups: int, cu_count: int, invaria
         return 1
     if workgroups < cu_count:
         return 2
+    if workgroups >= 0.5 * grid_workgroups:
+        return 3
     return 0
+
+
+def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv_splits: int,
+                 invariant: bool) -> tuple:
+    """(nondet geometry or None, stage-1 variant) for a batch of known lengths; max_len is
+    the (possibly bucketed) bound the plan is built for."""
+    if invariant:
+        return None, 0
+    lens = np.asarray(lengths, dtype=np.int64)
+    geom = nondet_geometry(len(lens), max_len, num_kv_heads, cu_count, max_kv_splits)
+    splits, seg, _ = geom
+    wg = nonempty_workgroups(lens, splits, seg)
+    # the workgroups if every request were as long as the longest (the batch's raggedness)
+    full = len(lens) * nonempty_workgroups([int(lens.max())], splits, seg) if lens.size else 0
+    return geom, stage1_variant(wg, full, cu_count, invariant=False)
 
 
 def workspace_slots(max_seq_len: int, max_kv_splits: int, invariant_split_size: int) -> int:

@@ -87,8 +87,9 @@ int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache
  * grid_slots == 1 the workspace is not touched. variant picks the stage-1
  * workgroup shape, which is part of the in-segment reduction order: 0 = 4
  * waves x 4 tokens per wave iteration (what sid_flash_decode_fwd uses), 1 =
- * 4 x 1 (full, HBM-bound grids), 2 = 8 x 2 (fewer workgroups than CUs); a
- * fixed variant keeps the batch independence of fixed splits.
+ * 4 x 1 (full, HBM-bound grids), 2 = 8 x 2 (fewer workgroups than CUs), 3 =
+ * 4 x 2 (in between); a fixed variant keeps the batch independence of fixed
+ * splits.
  */
 int sid_flash_decode_segments_fwd(const void* q, const void* k_cache, const void* v_cache,
                                   const int32_t* kv_indptr, const int32_t* kv_indices,

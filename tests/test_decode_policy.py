@@ -133,4 +133,5 @@ def test_stage1_variant_rule():
     assert stage1_variant(576, 576, 256, invariant=True) == 0      # invariant: fixed shape
     assert stage1_variant(230, 896, 256, invariant=False) == 2     # fewer than the CUs
     assert stage1_variant(600, 2176, 256, invariant=False) == 0    # ragged, in between
+    assert stage1_variant(270, 512, 256, invariant=False) == 3     # half full, in between
     assert stage1_variant(32, 32, 256, invariant=False) == 2

@@ -81,7 +81,7 @@ def test_decode_vs_oracle(seq_lens, policy):
 @pytest.mark.parametrize("seq_lens", CASES, ids=lambda s: f"b{len(s)}_max{max(s)}")
 @pytest.mark.parametrize("policy", ["heuristic", "fixed256", "splits1", "splits8"])
 @pytest.mark.parametrize("seg", [64, 128, 256])
-@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_decode_segments_vs_oracle(seq_lens, policy, seg, variant):
     """Splits cut into segments of <= seg tokens (one workgroup each), merged in token
     order by stage 2, for every stage-1 workgroup shape. Workspace pre-filled with NaN: a
@@ -96,7 +96,7 @@ def test_decode_segments_vs_oracle(seq_lens, policy, seg, variant):
     assert_close_bf16(out, ref)
 
 
-@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("variant", [1, 2, 3])
 def test_variant_changes_bits_but_is_run_to_run_stable(variant):
     """The workgroup shape is part of the reduction order: another shape gives other bits
     (within tolerance), the same shape the same bits on every run."""
