@@ -115,6 +115,18 @@ __host__ __device__ __forceinline__ bool segment_range(int seq_len, int n_splits
   return start < end;
 }
 
+// Number of non-empty slots of a request: they are slots 0 .. used-1. (A split holds tokens
+// only if every earlier split is full, and inside a split only trailing segments can be
+// empty, so segment_range(y) is true exactly for y < used.)
+__host__ __device__ __forceinline__ int used_slots(int seq_len, int n_splits, int fixed_split,
+                                                   int seg) {
+  const int chunk = kv_per_split(seq_len, n_splits, fixed_split);
+  const int sl = seg > 0 ? min(seg, chunk) : chunk;
+  const int sps = ceil_div(chunk, sl);
+  const int splits = min(n_splits, ceil_div(seq_len, chunk));
+  return (splits - 1) * sps + ceil_div(seq_len - (splits - 1) * chunk, sl);
+}
+
 // NW waves per workgroup; TPL tokens per wave iteration. (A software-pipelined variant,
 // the next iteration's rows loading during this one's math, doubled the tile registers,
 // lowered occupancy and measured no faster.)
@@ -331,6 +343,66 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_kernel(
   o[row * HEAD_DIM + d] = f32_to_bf16(num / den);
 }
 
+// Stage 2 for batches of at most kLatencyBatch requests (at most 64 workgroups, so latency,
+// not throughput, is the cost): the same merge in the same order, with the loads of a chunk
+// of up to kChunk used slots (log-sum-exp and partial) all issued before the first is used:
+// one dependent round trip where decode_stage2_kernel takes one for the log-sum-exps and then
+// one per 8 slots. The used slots are a prefix (used_slots), so the bound is uniform across
+// the workgroup and nothing is loaded from a slot stage 1 left empty. Measured: one request
+// of 1024 tokens (32 slots) 11.5 -> 10.7 us per call; from 8 requests up it is slower than
+// decode_stage2_kernel (more code per slot, 1 us at B = 64, 7 us at B = 256).
+constexpr int kChunk = 32;
+constexpr int kLatencyBatch = 4;
+
+__global__ void __launch_bounds__(HEAD_DIM) decode_stage2_latency_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_lse,
+    const int32_t* __restrict__ kv_indptr, const int32_t* __restrict__ num_splits,
+    int fixed_split, int seg, int grid_slots, int part_stride, bf16_t* __restrict__ o) {
+  const int hq = blockIdx.x;
+  const int b = blockIdx.y;
+  const int d = threadIdx.x;
+  const int64_t row = static_cast<int64_t>(b) * HQ + hq;
+  const int seq_len = kv_indptr[b + 1] - kv_indptr[b];
+  const int n_splits = num_splits[b];
+  if (n_splits <= 0 || seq_len <= 0) {
+    o[row * HEAD_DIM + d] = 0;
+    return;
+  }
+  const float* lse = part_lse + row * part_stride;
+  const float* po = part_o + row * part_stride * HEAD_DIM;
+  const int n_used = min(grid_slots, used_slots(seq_len, n_splits, fixed_split, seg));
+  float mx = NEG_BIG;
+  float num = 0.0f, den = 0.0f;
+  // Pass 1 finds the max over all used slots; when they fit one chunk (the common case) the
+  // chunk's values stay in registers for pass 2.
+  float lv[kChunk], pv[kChunk];
+  for (int c0 = 0; c0 < n_used; c0 += kChunk) {
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      lv[j] = c0 + j < n_used ? lse[c0 + j] : NEG_BIG;
+    }
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      if (c0 + j < n_used) mx = fmaxf(mx, lv[j]);
+    }
+  }
+  for (int c0 = 0; c0 < n_used; c0 += kChunk) {
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      if (n_used > kChunk) lv[j] = c0 + j < n_used ? lse[c0 + j] : NEG_BIG;
+      pv[j] = c0 + j < n_used ? po[(c0 + j) * HEAD_DIM + d] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const bool valid = c0 + j < n_used;
+      const float w = valid ? __expf(lv[j] - mx) : 0.0f;
+      num += w * (valid ? pv[j] : 0.0f);
+      den += w;
+    }
+  }
+  o[row * HEAD_DIM + d] = f32_to_bf16(num / den);
+}
+
 // Stage-1 shapes (waves per workgroup x tokens per wave iteration). They fix the in-segment
 // reduction order, so the bits of a result depend on the shape; every shape is a constant of
 // the call (sid_flash_decode_segments_fwd's `variant`), never of the data.
@@ -361,9 +433,9 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
   }
   int rc = check_launch("flash_decode_fwd stage1");
   if (rc != SID_OK || direct) return rc;
-  hipLaunchKernelGGL(decode_stage2_kernel, dim3(HQ, batch), dim3(HEAD_DIM), 0, s, part_o, part_lse,
-                     kv_indptr, num_splits, fixed_split_size, seg, grid_slots, part_stride,
-                     (bf16_t*)o);
+  hipLaunchKernelGGL(batch <= kLatencyBatch ? decode_stage2_latency_kernel : decode_stage2_kernel,
+                     dim3(HQ, batch), dim3(HEAD_DIM), 0, s, part_o, part_lse, kv_indptr,
+                     num_splits, fixed_split_size, seg, grid_slots, part_stride, (bf16_t*)o);
   return check_launch("flash_decode_fwd stage2");
 }
 

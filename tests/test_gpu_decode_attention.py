@@ -195,6 +195,47 @@ def test_fixed256_is_batch_invariant():
         assert torch.equal(base, run(comp))
 
 
+@pytest.mark.parametrize("plan", [(0, 32, 0), (0, 32, 64), (256, 0, 64), (256, 0, 0), (0, 5, 32)],
+                         ids=["heur32", "heur32_seg64", "fixed256_seg64", "fixed256", "split5_seg32"])
+def test_stage2_latency_kernel_bits_equal_batch_kernel(plan):
+    """Batches of at most 4 requests merge with the latency-oriented stage 2 and larger ones
+    with the throughput one; both fold the same slots in the same order, so a request's
+    output must be bitwise the same alone (B=1) and among 7 others (B=8), for 1 to 128 used
+    slots (more than one 32-slot load chunk)."""
+    fixed, max_splits, seg = plan
+    g = torch.Generator().manual_seed(21)
+    pool = 40000
+    k = torch.randn(pool, HKV, D, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(pool, HKV, D, generator=g).to(torch.bfloat16).cuda()
+
+    def splits(n):
+        return -(-n // fixed) if fixed else min(-(-n // 32), max_splits)
+
+    for L in (1, 33, 1024, 2047, 8192):
+        q0 = torch.randn(1, HQ, D, generator=g).to(torch.bfloat16).cuda()
+        idx0 = (torch.randperm(pool - 1, generator=g)[:L] + 1).to(torch.int32)
+        others = [int(x) for x in torch.randint(1, 3000, (7,), generator=g)]
+        outs = []
+        for lens in ([L], others[:3] + [L] + others[3:]):
+            qs, idxs = [], []
+            for n in lens:
+                if n == L and len(qs) == (0 if len(lens) == 1 else 3):
+                    qs.append(q0)
+                    idxs.append(idx0)
+                else:
+                    qs.append(torch.randn(1, HQ, D, generator=g).to(torch.bfloat16).cuda())
+                    idxs.append(torch.randint(1, pool, (n,), generator=g, dtype=torch.int32))
+            indptr = torch.zeros(len(lens) + 1, dtype=torch.int32)
+            indptr[1:] = torch.cumsum(torch.tensor(lens), 0)
+            ns = [splits(n) for n in lens]
+            slots = _slots(lens, ns, fixed, seg)
+            o = _run(torch.cat(qs), k, v, indptr.cuda(), torch.cat(idxs).cuda(), ns, max(ns), fixed,
+                     seg=seg, slots=slots)
+            outs.append(o[0 if len(lens) == 1 else 3])
+        assert torch.isfinite(outs[0].float()).all()
+        assert torch.equal(outs[0], outs[1]), f"L={L}"
+
+
 def _paged_case(num_pages, seq_lens, seed):
     rng = np.random.default_rng(seed)
     bs = len(seq_lens)
