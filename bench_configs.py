@@ -269,7 +269,7 @@ def config5(args):
                          "generated_tokens": toks,
                          "rollbacks": sum(o.num_rollbacks for o in outs)}
         del eng
-        gc.collect()  # the runner and its graph cache reference each other
+        gc.collect()
         torch.cuda.empty_cache()
     return {"metric": f"continuous batching, {n} requests, T=0.7 (config 5)",
             "value": results["dvr"]["tokens_per_s"], "unit": "tokens/s", "higher_is_better": True,

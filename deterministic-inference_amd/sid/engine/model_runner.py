@@ -98,16 +98,31 @@ class ModelRunner:
                                   decode_backend=self.cfg.decode_backend, greedy=greedy,
                                   sample=sample)
 
+    def fused_sample(self, fb: ForwardBatch) -> bool:
+        """Whether a decode batch without top-k / top-p limits draws its tokens inside the
+        lm_head (sid_linear_sample) instead of writing logits for the sampler kernel. The
+        two agree except at float near-ties of the scores (their softmax sums run in
+        different orders), so in batch_invariant mode the choice is one per engine, never
+        per batch: fused when every decode batch fits it (max_decode_batch <= 256). Elsewhere
+        by speed: fused up to 128 rows (it streams the weights once per 64 rows; measured at
+        T = 0.7: 1 row 74 vs 178 us, 64: 114 vs 205, 128: 205 vs 231, 256: 393 vs 329); dvr
+        commits only the verifier's tokens, so its decode rows may take either path."""
+        if fb.mode != ForwardMode.DECODE or not fb.untruncated:
+            return False
+        k = self.mcfg.hidden_size
+        if fb.invariant:
+            return linear_sample_supported(self.cfg.max_decode_batch, k)
+        rows = fb.input_ids.shape[0]
+        return linear_sample_supported(rows, k) and rows <= 128
+
     def step(self, fb: ForwardBatch) -> torch.Tensor:
         """forward + sample -> int64 tokens [R]. An all-greedy batch takes the fused
-        lm_head + argmax path, a decode batch of at most 256 rows without top-k / top-p
-        limits the fused lm_head + sampler (same tokens as sampling the logits, up to float
-        near-ties of the scores; no logits written); the rest writes the logits and runs the
+        lm_head + argmax path, a decode batch the fused lm_head + sampler where
+        fused_sample says so (no logits written); the rest writes the logits and runs the
         sampler kernel over them."""
         if fb.all_greedy:
             return self.forward(fb, greedy=True)
-        if (fb.mode == ForwardMode.DECODE and fb.untruncated
-                and linear_sample_supported(fb.input_ids.shape[0], self.mcfg.hidden_size)):
+        if self.fused_sample(fb):
             return self.forward(fb, sample=True)
         return self.sample(fb, self.forward(fb))
 
@@ -212,8 +227,9 @@ class GraphCache:
         graph = torch.cuda.CUDAGraph()
         # No garbage collection inside the capture: a collected object that owns device
         # resources (a graph, an event, pinned memory) would release them with HIP calls
-        # that are illegal while a stream is being captured, and the process aborts.
-        gc.collect()
+        # that are illegal while a stream is being captured, and the process aborts. The
+        # collector is only paused (cycles found later are freed after the capture); a full
+        # collection first would cost ~50 ms per capture on a serving process's heap.
         was_enabled = gc.isenabled()
         gc.disable()
         try:
