@@ -304,54 +304,79 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def gemm_report(wl, reps=50):
-    """The decode step's projections at its real shape (M = batch rows, the layer-0
-    weights): average duration per launch (HIP events around one replay of a graph of reps
-    back-to-back launches), MFMA rate against the bf16 dense peak and weight-read rate
-    against HBM.
-    At M = 64 every projection is bound by reading its weights, not by MFMA throughput."""
+def gemm_report(wl):
+    """The decode step's projections at its real shape (M = batch rows) with their weights
+    coming from HBM: the four projections of every layer run in the step's order (qkv, o,
+    gate_up with its SwiGLU epilogue, down) over all 28 layers' weights, 880 MB, more than the
+    256 MB last-level cache holds, captured in one HIP graph and timed with HIP events around
+    a replay. A projection's figure is the chain's time minus the time of the same chain
+    without it, per layer: its in-chain cost, launch boundary included. The lm_head (311 MB,
+    also larger than the cache) is timed alone, with its greedy argmax finalize. MFMA rate is
+    against the bf16 dense peak, weight-read rate against HBM; at M = 64 the projections are
+    bound by latency, not by either."""
     torch = wl.torch
-    from sid.kernels.matmul_persistent import linear_argmax, linear_partials
+    from sid.kernels.matmul_persistent import linear_argmax, linear_partials, linear_silu_mul
     w = wl.runner.model.w
-    lw = w["layers"][0]
+    layers = w["layers"]
     m = len(wl.reqs)
     g = torch.Generator(device="cuda").manual_seed(7)
-    out = {}
-    shapes = [("qkv", lw["qkv"]), ("o", lw["o"]), ("gate_up", lw["gate_up"]),
-              ("down", lw["down"]), ("lm_head+argmax", w["lm_head"])]
-    for name, wt in shapes:
-        n, k = wt.shape
-        x = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
-        fn = (lambda: linear_argmax(x, wt)) if name == "lm_head+argmax" else \
-            (lambda: linear_partials(x, wt))
-        for _ in range(3):
+    xs = {k: torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+          for k in (1024, 2048, 3072)}
+    ops = {"qkv": lambda lw: linear_partials(xs[1024], lw["qkv"]),
+           "o": lambda lw: linear_partials(xs[2048], lw["o"]),
+           "gate_up+silu": lambda lw: linear_silu_mul(xs[1024], lw["gate_up"]),
+           "down": lambda lw: linear_partials(xs[3072], lw["down"])}
+
+    def timed(fn, reps=1):
+        for _ in range(2):
             fn()
         torch.cuda.synchronize()
-        # reps launches captured in one HIP graph, so host launch cost is not timed
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             for _ in range(reps):
                 fn()
         graph.replay()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        us = start.elapsed_time(end) / reps * 1e3
+        best = float("inf")
+        for _ in range(3):
+            start.record()
+            graph.replay()
+            end.record()
+            torch.cuda.synchronize()
+            best = min(best, start.elapsed_time(end) * 1e3)
         del graph
+        return best / reps
+
+    def chain(skip=None):
+        def run():
+            for lw in layers:
+                for name, op in ops.items():
+                    if name != skip:
+                        op(lw)
+        return timed(run)
+
+    full = chain()
+    out = {}
+    for name, wt in (("qkv", layers[0]["qkv"]), ("o", layers[0]["o"]),
+                     ("gate_up+silu", layers[0]["gate_up"]), ("down", layers[0]["down"])):
+        us = (full - chain(skip=name)) / len(layers)
+        out[name] = (wt.shape, us)
+    lm = w["lm_head"]
+    out["lm_head+argmax"] = (lm.shape, timed(lambda: linear_argmax(xs[1024], lm), reps=20))
+    shapes = {}
+    for name, ((n, k), us) in out.items():
         flops = 2 * m * n * k
-        out[name] = {"m": m, "n": n, "k": k, "us": round(us, 2),
-                     "tflops": round(flops / us / 1e6, 1),
-                     "mfma_frac": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "weight_GBps": round(n * k * 2 / us / 1e3, 1)}
+        shapes[name] = {"m": m, "n": n, "k": k, "us": round(us, 2),
+                        "tflops": round(flops / us / 1e6, 1),
+                        "mfma_frac": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "weight_GBps": round(n * k * 2 / us / 1e3, 1),
+                        "hbm_frac": round(n * k * 2 / us / 1e3 / HBM_PEAK_GBS, 4)}
     return {"peak_bf16_tflops": MFMA_BF16_PEAK_TFLOPS, "peak_hbm_GBps": HBM_PEAK_GBS,
-            "note": "split-K projections (fp32 chunk partials, folded by the consumer kernel) "
-                    "and the lm_head with fused greedy argmax (+ its finalize kernel), "
-                    "back-to-back in one HIP graph; the same weights every launch, so after the "
-                    "first they come from the 256 MB last-level cache: inside the decode step "
-                    "(weights from HBM) the profile shows 5.1-7.5 us per projection",
-            "shapes": out}
+            "chain_us_per_layer": round(full / len(layers), 2),
+            "note": "weights from HBM: the 28 layers' projections in step order (880 MB per "
+                    "pass); per-projection figures are in-chain costs (chain minus chain "
+                    "without it), launch boundaries included",
+            "shapes": shapes}
 
 
 def main():
