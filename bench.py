@@ -187,7 +187,8 @@ def attention_roofline(wl, reps):
     for layer in range(mcfg.num_layers):
         kp, vp = wl.kv.layer(layer)
         attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len, scale,
-                     wl.invariant, policy_batch=fb.real_rows, variant=fb.decode_variant)
+                     wl.invariant, policy_batch=fb.real_rows, variant=fb.decode_variant,
+                     geometry=fb.decode_geometry)
     torch.cuda.synchronize()
     # One event pair around reps x 28 back-to-back launches on the launch stream: the
     # average is the kernel's steady-state duration (launch overhead overlaps execution).
@@ -199,7 +200,7 @@ def attention_roofline(wl, reps):
             kp, vp = wl.kv.layer(layer)
             attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len,
                          scale, wl.invariant, policy_batch=fb.real_rows,
-                         variant=fb.decode_variant)
+                         variant=fb.decode_variant, geometry=fb.decode_geometry)
             launches += 1
     end.record()
     torch.cuda.synchronize()

@@ -81,8 +81,8 @@ def _attn_case(q, k, v, indptr, idx, lens):
     out = {}
     o = torch.empty_like(q)
     for name, inv in (("nondet", False), ("fixed256", True)):
-        ns, grid, fixed, seg, slots = attn.plan(seq, max(lens), inv)
-        _, variant = plan_variant(lens, max(lens), HKV, attn.cu_count(), 32, inv)
+        geom, variant = plan_variant(lens, max(lens), HKV, attn.cu_count(), 32, inv)
+        ns, grid, fixed, seg, slots = attn.plan(seq, max(lens), inv, geometry=geom)
         fn = lambda: ext.flash_decode_fwd(q, k, v, indptr, idx, ns, grid, fixed, D ** -0.5,
                                           attn.part_o, attn.part_lse, o, segment_size=seg,
                                           grid_slots=slots, variant=variant)

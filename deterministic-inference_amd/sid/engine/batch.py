@@ -61,6 +61,7 @@ class ForwardBatch:
     new_slots_host: Optional[np.ndarray] = None  # decode: the KV slot each row writes
     seq_lens_host: Optional[np.ndarray] = None  # decode: kv length of each real row
     decode_variant: int = 0  # decode: stage-1 workgroup shape of the attention kernel
+    decode_geometry: Optional[tuple] = None  # decode, nondet: plan_variant's attention geometry
 
     def build_indices(self) -> None:
         """Enqueue the deferred kv_indices build (a no-op when the builder already ran it).

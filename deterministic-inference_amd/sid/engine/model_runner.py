@@ -161,6 +161,7 @@ class ModelRunner:
                                                self.mcfg.num_kv_heads,
                                                self.decode_attn.cu_count(),
                                                self.cfg.max_kv_splits, invariant=False)
+        fb.decode_geometry = geom
         return geom
 
     def tag_verify(self, fb: ForwardBatch) -> ForwardBatch:

@@ -129,15 +129,29 @@ def stage1_variant(workgroups: int, grid_workgroups: int, cu_count: int, invaria
     return 0
 
 
+# Long segments for large batches: when 512-token segments still give every CU two non-empty
+# workgroups, they beat 256 (half the workgroups and partials; measured at B = 256: uniform
+# 1024-token contexts 177.4 -> 166.3 us, config-5-like lognormal lengths 189.7 -> 177.6 us).
+# Below two per CU they lose (lognormal B = 128: 109 -> 146 us), so the count is taken over
+# the batch's actual lengths.
+LONG_SEGMENT = 512
+
+
 def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv_splits: int,
                  invariant: bool) -> tuple:
     """(nondet geometry or None, stage-1 variant) for a batch of known lengths; max_len is
-    the (possibly bucketed) bound the plan is built for."""
+    the (possibly bucketed) bound the plan is built for. The geometry (grid splits, segment
+    size, grid slots) is what DecodeAttention.forward runs when given it."""
     if invariant:
         return None, 0
     lens = np.asarray(lengths, dtype=np.int64)
     geom = nondet_geometry(len(lens), max_len, num_kv_heads, cu_count, max_kv_splits)
-    splits, seg, _ = geom
+    splits, seg, slots = geom
+    if (seg == SEGMENT_SIZES[0] and lens.size
+            and nonempty_workgroups(lens, splits, LONG_SEGMENT) >= 2 * cu_count):
+        chunk_max = max(32, _cdiv(_cdiv(max_len, splits), 32) * 32)
+        seg = LONG_SEGMENT
+        geom = (splits, seg, splits * max(1, _cdiv(chunk_max, seg)))
     wg = nonempty_workgroups(lens, splits, seg)
     # the workgroups if every request were as long as the longest (the batch's raggedness)
     full = len(lens) * nonempty_workgroups([int(lens.max())], splits, seg) if lens.size else 0
@@ -182,10 +196,11 @@ class DecodeAttention:
         return _cu_count(idx)
 
     def plan(self, seq_lens: torch.Tensor, max_seq_len: int, invariant: bool,
-             policy_batch: int | None = None):
+             policy_batch: int | None = None, geometry: tuple | None = None):
         """(num_splits int32 [B] on device, grid splits, fixed split size, segment size,
         grid slots). max_seq_len bounds every request's length (host-side, no sync);
-        policy_batch: the real request count when seq_lens has padding rows."""
+        policy_batch: the real request count when seq_lens has padding rows; geometry: the
+        nondet (grid splits, segment size, grid slots) chosen by plan_variant, if any."""
         bs = seq_lens.shape[0] if policy_batch is None else int(policy_batch)
         max_len = max(int(max_seq_len), 1)
         if invariant:
@@ -193,27 +208,32 @@ class DecodeAttention:
             num_splits = ((seq_lens + tile - 1) // tile).to(torch.int32)
             grid = max(1, -(-max_len // tile))
             return num_splits, grid, tile, tile, grid
-        splits, seg, slots = nondet_geometry(bs, max_len, self.num_kv_heads, self.cu_count(),
-                                             self.max_kv_splits)
+        if geometry is None:
+            geometry = nondet_geometry(bs, max_len, self.num_kv_heads, self.cu_count(),
+                                       self.max_kv_splits)
+        splits, seg, slots = geometry
         num_splits = torch.clamp((seq_lens + 31) // 32, max=splits).to(torch.int32)
         return num_splits, splits, 0, seg, slots
 
     def forward(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, seq_lens: torch.Tensor,
                 max_seq_len: int, sm_scale: float, invariant: bool,
-                policy_batch: int | None = None, variant: int = 0) -> torch.Tensor:
+                policy_batch: int | None = None, variant: int = 0,
+                geometry: tuple | None = None) -> torch.Tensor:
         """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync).
         policy_batch: real requests among the B rows (the rest are empty padding); variant:
-        the stage-1 workgroup shape (stage1_variant; 0 in batch_invariant mode)."""
+        the stage-1 workgroup shape (stage1_variant; 0 in batch_invariant mode); geometry:
+        plan_variant's nondet geometry for this batch (None: from the batch size and
+        max_seq_len alone)."""
         assert not (invariant and variant), "batch_invariant mode keeps the default shape"
         bs = q.shape[0]
         assert bs <= self.part_o.shape[0], "decode batch exceeds workspace"
         # One plan per forward: every layer sees the same seq_lens tensor.
-        key = (invariant, max_seq_len, bs, policy_batch)
+        key = (invariant, max_seq_len, bs, policy_batch, geometry)
         if self._plan_src is seq_lens and self._plan[0] == key:
             plan = self._plan[1]
         else:
-            plan = self.plan(seq_lens, max_seq_len, invariant, policy_batch)
+            plan = self.plan(seq_lens, max_seq_len, invariant, policy_batch, geometry)
             self._plan_src, self._plan = seq_lens, (key, plan)
         num_splits, grid_splits, fixed, seg, slots = plan
         assert slots <= self.part_o.shape[2], "decode plan exceeds the split workspace"

@@ -135,3 +135,24 @@ def test_stage1_variant_rule():
     assert stage1_variant(600, 2176, 256, invariant=False) == 0    # ragged, in between
     assert stage1_variant(270, 512, 256, invariant=False) == 3     # half full, in between
     assert stage1_variant(32, 32, 256, invariant=False) == 2
+
+
+def test_long_segments_only_with_two_workgroups_per_cu():
+    """plan_variant takes 512-token segments when they still give every CU two non-empty
+    workgroups (counted over the batch's real lengths), and keeps the size-based rule
+    otherwise."""
+    import numpy as np
+
+    from sid.kernels.decode_attention import LONG_SEGMENT, plan_variant
+    cu = 256
+    geom, _ = plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=False)
+    assert geom[1] == LONG_SEGMENT and geom[2] == 2            # 512 workgroups = 2 per CU
+    geom, _ = plan_variant([2049] * 64, 2049, 8, cu, 32, invariant=False)
+    assert geom[1] == 256                                      # config 3: 320 < 512
+    rng = np.random.default_rng(5)
+    lens = (np.minimum(rng.lognormal(np.log(512), 0.8, 128).astype(int), 8192) + 200).tolist()
+    geom, _ = plan_variant(lens, max(lens), 8, cu, 32, invariant=False)
+    assert geom[1] == 256                                      # ragged B = 128: too few
+    geom, _ = plan_variant([1024] * 255 + [1], 1024, 8, cu, 32, invariant=False)
+    assert geom[1] == 256                                      # 511 workgroups
+    assert plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=True) == (None, 0)
