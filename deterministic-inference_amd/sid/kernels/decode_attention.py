@@ -129,12 +129,13 @@ def stage1_variant(workgroups: int, grid_workgroups: int, cu_count: int, invaria
     return 0
 
 
-# Long segments for large batches: when 512-token segments still give every CU two non-empty
-# workgroups, they beat 256 (half the workgroups and partials; measured at B = 256: uniform
-# 1024-token contexts 177.4 -> 166.3 us, config-5-like lognormal lengths 189.7 -> 177.6 us).
-# Below two per CU they lose (lognormal B = 128: 109 -> 146 us), so the count is taken over
-# the batch's actual lengths.
-LONG_SEGMENT = 512
+# Long segments for large batches: the longest of LONG_SEGMENTS that still gives every CU two
+# non-empty workgroups (counted over the batch's actual lengths) beats 256 (fewer workgroups,
+# fewer partials, longer streams per workgroup). Measured: B = 256 x 1024 177.4 -> 166.3 us
+# (512); config-5-like lognormal B = 256 189.7 -> 177.6 us (512); B = 256 x 2048 360 -> 315
+# us (1024); B = 256 x 4096 722 -> 627 us (2048, 6.9 TB/s). Below two per CU they lose
+# (lognormal B = 128 with 512: 109 -> 146 us).
+LONG_SEGMENTS = (2048, 1024, 512)
 
 
 def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv_splits: int,
@@ -147,11 +148,13 @@ def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv
     lens = np.asarray(lengths, dtype=np.int64)
     geom = nondet_geometry(len(lens), max_len, num_kv_heads, cu_count, max_kv_splits)
     splits, seg, slots = geom
-    if (seg == SEGMENT_SIZES[0] and lens.size
-            and nonempty_workgroups(lens, splits, LONG_SEGMENT) >= 2 * cu_count):
-        chunk_max = max(32, _cdiv(_cdiv(max_len, splits), 32) * 32)
-        seg = LONG_SEGMENT
-        geom = (splits, seg, splits * max(1, _cdiv(chunk_max, seg)))
+    if seg == SEGMENT_SIZES[0] and lens.size:
+        for long_seg in LONG_SEGMENTS:
+            if nonempty_workgroups(lens, splits, long_seg) >= 2 * cu_count:
+                chunk_max = max(32, _cdiv(_cdiv(max_len, splits), 32) * 32)
+                seg = long_seg
+                geom = (splits, seg, splits * max(1, _cdiv(chunk_max, seg)))
+                break
     wg = nonempty_workgroups(lens, splits, seg)
     # the workgroups if every request were as long as the longest (the batch's raggedness)
     full = len(lens) * nonempty_workgroups([int(lens.max())], splits, seg) if lens.size else 0

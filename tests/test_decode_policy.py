@@ -138,15 +138,19 @@ def test_stage1_variant_rule():
 
 
 def test_long_segments_only_with_two_workgroups_per_cu():
-    """plan_variant takes 512-token segments when they still give every CU two non-empty
-    workgroups (counted over the batch's real lengths), and keeps the size-based rule
-    otherwise."""
+    """plan_variant takes the longest of 2048/1024/512-token segments that still gives every CU
+    two non-empty workgroups (counted over the batch's real lengths), and keeps the
+    size-based rule otherwise."""
     import numpy as np
 
-    from sid.kernels.decode_attention import LONG_SEGMENT, plan_variant
+    from sid.kernels.decode_attention import plan_variant
     cu = 256
     geom, _ = plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=False)
-    assert geom[1] == LONG_SEGMENT and geom[2] == 2            # 512 workgroups = 2 per CU
+    assert geom[1] == 512 and geom[2] == 2                     # 512 workgroups = 2 per CU
+    geom, _ = plan_variant([4096] * 256, 4096, 8, cu, 32, invariant=False)
+    assert geom[1] == 2048 and geom[2] == 2                    # the longest that keeps 2 per CU
+    geom, _ = plan_variant([2048] * 256, 2048, 8, cu, 32, invariant=False)
+    assert geom[1] == 1024
     geom, _ = plan_variant([2049] * 64, 2049, 8, cu, 32, invariant=False)
     assert geom[1] == 256                                      # config 3: 320 < 512
     rng = np.random.default_rng(5)

@@ -125,6 +125,27 @@ def test_planned_decode_vs_oracle(invariant, lens):
     assert_close_bf16(out, decode_attention_ref(q, k, v, indptr, idx, SCALE))
 
 
+@pytest.mark.parametrize("lens", [[1024] * 256, [2048] * 256, [8192] * 64,
+                                  [int(x) for x in (np.minimum(np.random.default_rng(3).lognormal(
+                                      np.log(700), 0.8, 256), 8192) + 1).astype(int)]],
+                         ids=["b256x1024", "b256x2048", "b64x8192", "b256_lognormal"])
+def test_long_segment_plans_vs_oracle(lens):
+    """plan_variant's long segments (512/1024/2048 tokens for large batches) with the
+    workgroup shape it picks, run through DecodeAttention.forward, against the oracle."""
+    from sid.kernels.decode_attention import DecodeAttention, plan_variant
+    q, k, v, indptr, idx = decode_inputs(lens, seed=8)
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    geom, variant = plan_variant(lens, max(lens), HKV, cu, 32, invariant=False)
+    print(f"B={len(lens)} max={max(lens)} geometry={geom} variant={variant}", flush=True)
+    assert geom[1] >= 512
+    attn = DecodeAttention(len(lens), HQ, HKV, D, 32, 256, 8192, "cuda")
+    seq = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    out = attn.forward(q, k, v, indptr, idx, seq, max(lens), SCALE, False, variant=variant,
+                       geometry=geom)
+    torch.set_num_threads(16)
+    assert_close_bf16(out, decode_attention_ref(q, k, v, indptr, idx, SCALE))
+
+
 def test_direct_single_split_equals_two_stage():
     """Grid 1 writes o directly; a grid of 2 with every request on one split runs the
     merge pass. Both must give the same bits (merge of one split is the identity)."""
