@@ -115,18 +115,6 @@ __host__ __device__ __forceinline__ bool segment_range(int seq_len, int n_splits
   return start < end;
 }
 
-// Number of non-empty slots of a request: they are slots 0 .. used-1. (A split holds tokens
-// only if every earlier split is full, and inside a split only trailing segments can be
-// empty, so segment_range(y) is true exactly for y < used.)
-__host__ __device__ __forceinline__ int used_slots(int seq_len, int n_splits, int fixed_split,
-                                                   int seg) {
-  const int chunk = kv_per_split(seq_len, n_splits, fixed_split);
-  const int sl = seg > 0 ? min(seg, chunk) : chunk;
-  const int sps = ceil_div(chunk, sl);
-  const int splits = min(n_splits, ceil_div(seq_len, chunk));
-  return (splits - 1) * sps + ceil_div(seq_len - (splits - 1) * chunk, sl);
-}
-
 // NW waves per workgroup; TPL tokens per wave iteration. (A software-pipelined variant,
 // the next iteration's rows loading during this one's math, doubled the tile registers,
 // lowered occupancy and measured no faster.)
@@ -157,15 +145,25 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   __shared__ float s_acc[NW][HQ][HEAD_DIM];
 
   const int64_t out_row = static_cast<int64_t>(b) * HQ;
+  // A slot with no tokens marks itself empty (log-sum-exp NEG_BIG): every slot below the
+  // grid's slot count is written on every call, so stage 2 can tell used slots from the
+  // log-sum-exps alone.
+  auto mark_empty = [&]() {
+    if (o_direct == nullptr && tid < HQ) part_lse[(out_row + tid) * part_stride + y] = NEG_BIG;
+  };
   if (n_splits <= 0 || seq_len <= 0) {
     // Empty request: stage 2 would write zeros (flash_decode.cu:246-249).
     if (o_direct != nullptr && y == 0) {
       for (int i = tid; i < HQ * HEAD_DIM; i += NW * 64) o_direct[out_row * HEAD_DIM + i] = 0;
     }
+    mark_empty();
     return;
   }
   int start, end;
-  if (!segment_range(seq_len, n_splits, fixed_split, seg, y, start, end)) return;
+  if (!segment_range(seq_len, n_splits, fixed_split, seg, y, start, end)) {
+    mark_empty();
+    return;
+  }
 
   // Query heads 2*grp and 2*grp+1, packed bf16: lane `sub` holds the dims it owns.
   u32x4_v qv[QPK][2];
@@ -273,28 +271,52 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   }
   __syncthreads();
 
-  // Merge the waves in increasing wave order; thread -> (head, dim). A wave that saw no
-  // token of the segment has m = NEG_BIG and l = 0 and drops out (its scale underflows).
-  for (int i = tid; i < HQ * HEAD_DIM; i += NW * 64) {
-    const int h = i / HEAD_DIM;
-    const int d = i % HEAD_DIM;
-    float mx = s_m[0][h];
+  // Merge the waves in increasing wave order. A wave that saw no token of the segment has
+  // m = NEG_BIG and l = 0 and drops out (its scale underflows). One thread per query head
+  // takes the max over the waves, every wave's scale and the denominator once; then each
+  // thread folds 4 consecutive dims of one head (128-bit LDS reads), with the same
+  // per-output operations in the same order as folding every dim on its own.
+  __shared__ float s_sc[NW][HQ];
+  __shared__ float s_den[HQ];
+  __shared__ float s_mx[HQ];
+  if (tid < HQ) {
+    float mx = s_m[0][tid];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_m[w][h]);
-    float den = 0.0f, num = 0.0f;
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_m[w][tid]);
+    float den = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float sc = __expf(s_m[w][h] - mx);
-      den += s_l[w][h] * sc;
-      num += s_acc[w][h][d] * sc;
+      const float sc = __expf(s_m[w][tid] - mx);
+      s_sc[w][tid] = sc;
+      den += s_l[w][tid] * sc;
     }
-    const float out = num / den;
+    s_den[tid] = den;
+    s_mx[tid] = mx;
+  }
+  __syncthreads();
+  constexpr int Q4 = HEAD_DIM / 4;
+  for (int i = tid; i < HQ * Q4; i += NW * 64) {
+    const int h = i / Q4;
+    const int d0 = (i % Q4) * 4;
+    float num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float sc = s_sc[w][h];
+      const float4 a = *reinterpret_cast<const float4*>(&s_acc[w][h][d0]);
+      num[0] += a.x * sc;
+      num[1] += a.y * sc;
+      num[2] += a.z * sc;
+      num[3] += a.w * sc;
+    }
+    const float den = s_den[h];
+    const float4 out = make_float4(num[0] / den, num[1] / den, num[2] / den, num[3] / den);
     if (o_direct != nullptr) {
-      o_direct[(out_row + h) * HEAD_DIM + d] = f32_to_bf16(out);
+      *reinterpret_cast<uint2*>(&o_direct[(out_row + h) * HEAD_DIM + d0]) =
+          make_uint2(pack_bf16x2(out.x, out.y), pack_bf16x2(out.z, out.w));
     } else {
       const int64_t prow = (out_row + h) * part_stride + y;
-      part_o[prow * HEAD_DIM + d] = out;
-      if (d == 0) part_lse[prow] = mx + __logf(den);
+      *reinterpret_cast<float4*>(&part_o[prow * HEAD_DIM + d0]) = out;
+      if (d0 == 0) part_lse[prow] = s_mx[h] + __logf(den);
     }
   }
 }
@@ -345,56 +367,52 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_kernel(
 
 // Stage 2 for batches of at most kLatencyBatch requests (at most 64 workgroups, so latency,
 // not throughput, is the cost): the same merge in the same order, with the loads of a chunk
-// of up to kChunk used slots (log-sum-exp and partial) all issued before the first is used:
-// one dependent round trip where decode_stage2_kernel takes one for the log-sum-exps and then
-// one per 8 slots. The used slots are a prefix (used_slots), so the bound is uniform across
-// the workgroup and nothing is loaded from a slot stage 1 left empty. Measured: one request
-// of 1024 tokens (32 slots) 11.5 -> 10.7 us per call; from 8 requests up it is slower than
-// decode_stage2_kernel (more code per slot, 1 us at B = 64, 7 us at B = 256).
+// of kChunk slots (log-sum-exp and partial) all issued at once and nothing loaded before
+// them: stage 1 marks the slots it leaves empty (log-sum-exp NEG_BIG), so the used slots
+// are known from the log-sum-exps and the kernel makes one dependent round trip, where
+// decode_stage2_kernel takes one for the request's geometry, one for the log-sum-exps and
+// then one per 8 slots. Unused slots' partials are loaded (in bounds: part_stride >=
+// grid_slots) and dropped by a select. Measured: one request of 1024 tokens (32 slots) 11.5
+// -> 10.7 us per call; from 8 requests up it is slower than decode_stage2_kernel (more code
+// per slot, 1 us at B = 64, 7 us at B = 256).
 constexpr int kChunk = 32;
 constexpr int kLatencyBatch = 4;
 
 __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_latency_kernel(
-    const float* __restrict__ part_o, const float* __restrict__ part_lse,
-    const int32_t* __restrict__ kv_indptr, const int32_t* __restrict__ num_splits,
-    int fixed_split, int seg, int grid_slots, int part_stride, bf16_t* __restrict__ o) {
+    const float* __restrict__ part_o, const float* __restrict__ part_lse, int grid_slots,
+    int part_stride, bf16_t* __restrict__ o) {
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
   const int d = threadIdx.x;
   const int64_t row = static_cast<int64_t>(b) * HQ + hq;
-  const int seq_len = kv_indptr[b + 1] - kv_indptr[b];
-  const int n_splits = num_splits[b];
-  if (n_splits <= 0 || seq_len <= 0) {
+  const float* lse = part_lse + row * part_stride;
+  const float* po = part_o + row * part_stride * HEAD_DIM;
+  float mx = NEG_BIG;
+  float num = 0.0f, den = 0.0f;
+  // Pass 1 finds the max over the used slots; when the grid fits one chunk (the common
+  // case) the chunk's values stay in registers for pass 2.
+  float lv[kChunk], pv[kChunk];
+  for (int c0 = 0; c0 < grid_slots; c0 += kChunk) {
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      lv[j] = c0 + j < grid_slots ? lse[c0 + j] : NEG_BIG;
+    }
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) mx = fmaxf(mx, lv[j]);
+  }
+  if (mx == NEG_BIG) {  // empty request (flash_decode.cu:246-249)
     o[row * HEAD_DIM + d] = 0;
     return;
   }
-  const float* lse = part_lse + row * part_stride;
-  const float* po = part_o + row * part_stride * HEAD_DIM;
-  const int n_used = min(grid_slots, used_slots(seq_len, n_splits, fixed_split, seg));
-  float mx = NEG_BIG;
-  float num = 0.0f, den = 0.0f;
-  // Pass 1 finds the max over all used slots; when they fit one chunk (the common case) the
-  // chunk's values stay in registers for pass 2.
-  float lv[kChunk], pv[kChunk];
-  for (int c0 = 0; c0 < n_used; c0 += kChunk) {
+  for (int c0 = 0; c0 < grid_slots; c0 += kChunk) {
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
-      lv[j] = c0 + j < n_used ? lse[c0 + j] : NEG_BIG;
+      if (grid_slots > kChunk) lv[j] = c0 + j < grid_slots ? lse[c0 + j] : NEG_BIG;
+      pv[j] = c0 + j < grid_slots ? po[(c0 + j) * HEAD_DIM + d] : 0.0f;
     }
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
-      if (c0 + j < n_used) mx = fmaxf(mx, lv[j]);
-    }
-  }
-  for (int c0 = 0; c0 < n_used; c0 += kChunk) {
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
-      if (n_used > kChunk) lv[j] = c0 + j < n_used ? lse[c0 + j] : NEG_BIG;
-      pv[j] = c0 + j < n_used ? po[(c0 + j) * HEAD_DIM + d] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
-      const bool valid = c0 + j < n_used;
+      const bool valid = lv[j] != NEG_BIG;
       const float w = valid ? __expf(lv[j] - mx) : 0.0f;
       num += w * (valid ? pv[j] : 0.0f);
       den += w;
@@ -433,9 +451,14 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
   }
   int rc = check_launch("flash_decode_fwd stage1");
   if (rc != SID_OK || direct) return rc;
-  hipLaunchKernelGGL(batch <= kLatencyBatch ? decode_stage2_latency_kernel : decode_stage2_kernel,
-                     dim3(HQ, batch), dim3(HEAD_DIM), 0, s, part_o, part_lse, kv_indptr,
-                     num_splits, fixed_split_size, seg, grid_slots, part_stride, (bf16_t*)o);
+  if (batch <= kLatencyBatch) {
+    hipLaunchKernelGGL(decode_stage2_latency_kernel, dim3(HQ, batch), dim3(HEAD_DIM), 0, s,
+                       part_o, part_lse, grid_slots, part_stride, (bf16_t*)o);
+  } else {
+    hipLaunchKernelGGL(decode_stage2_kernel, dim3(HQ, batch), dim3(HEAD_DIM), 0, s, part_o,
+                       part_lse, kv_indptr, num_splits, fixed_split_size, seg, grid_slots,
+                       part_stride, (bf16_t*)o);
+  }
   return check_launch("flash_decode_fwd stage2");
 }
 
