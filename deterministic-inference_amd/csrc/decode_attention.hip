@@ -328,36 +328,33 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
 }
 
 // Stage 2: one workgroup per (query head, request), thread = output dim. The slots'
-// log-sum-exps (NEG_BIG for empty slots) are staged in LDS in parallel; every thread then
-// merges the non-empty slots sequentially in increasing slot order (increasing token
-// order), as in sid/csrc/flash_decode.cu:231-273 with segments in place of splits. The
-// partial loads of different slots are independent, so they overlap.
+// log-sum-exps are staged in LDS in parallel (stage 1 writes every slot below grid_slots on
+// every call: a partial, or NEG_BIG for a slot without tokens, so the request's geometry is
+// not needed here); every thread then merges the non-empty slots sequentially in
+// increasing slot order (increasing token order), as in sid/csrc/flash_decode.cu:231-273
+// with segments in place of splits. A request with no used slot gets zeros
+// (flash_decode.cu:246-249). The partial loads of different slots are independent, so they
+// overlap.
 constexpr int kMaxGridSlots = 1024;
 
 __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_kernel(
-    const float* __restrict__ part_o, const float* __restrict__ part_lse,
-    const int32_t* __restrict__ kv_indptr, const int32_t* __restrict__ num_splits,
-    int fixed_split, int seg, int grid_slots, int part_stride, bf16_t* __restrict__ o) {
+    const float* __restrict__ part_o, const float* __restrict__ part_lse, int grid_slots,
+    int part_stride, bf16_t* __restrict__ o) {
   __shared__ float s_lse[kMaxGridSlots];
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
   const int d = threadIdx.x;
   const int64_t row = static_cast<int64_t>(b) * HQ + hq;
-  const int seq_len = kv_indptr[b + 1] - kv_indptr[b];
-  const int n_splits = num_splits[b];
-  if (n_splits <= 0 || seq_len <= 0) {
-    o[row * HEAD_DIM + d] = 0;
-    return;
-  }
   const float* lse = part_lse + row * part_stride;
   const float* po = part_o + row * part_stride * HEAD_DIM;
-  for (int y = d; y < grid_slots; y += HEAD_DIM) {
-    int st, en;
-    s_lse[y] = segment_range(seq_len, n_splits, fixed_split, seg, y, st, en) ? lse[y] : NEG_BIG;
-  }
+  for (int y = d; y < grid_slots; y += HEAD_DIM) s_lse[y] = lse[y];
   __syncthreads();
   float mx = NEG_BIG;
   for (int y = 0; y < grid_slots; ++y) mx = fmaxf(mx, s_lse[y]);
+  if (mx == NEG_BIG) {
+    o[row * HEAD_DIM + d] = 0;
+    return;
+  }
   float num = 0.0f, den = 0.0f;
 #pragma unroll 8
   for (int y = 0; y < grid_slots; ++y) {
@@ -462,8 +459,7 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                        part_o, part_lse, grid_slots, part_stride, (bf16_t*)o);
   } else {
     hipLaunchKernelGGL(decode_stage2_kernel, dim3(HQ, batch), dim3(HEAD_DIM), 0, s, part_o,
-                       part_lse, kv_indptr, num_splits, fixed_split_size, seg, grid_slots,
-                       part_stride, (bf16_t*)o);
+                       part_lse, grid_slots, part_stride, (bf16_t*)o);
   }
   return check_launch("flash_decode_fwd stage2");
 }
