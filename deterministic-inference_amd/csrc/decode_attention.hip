@@ -373,11 +373,11 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_stage2_kernel(
 // of kChunk slots (log-sum-exp and partial) all issued at once and nothing loaded before
 // them: stage 1 marks the slots it leaves empty (log-sum-exp NEG_BIG), so the used slots
 // are known from the log-sum-exps and the kernel makes one dependent round trip, where
-// decode_stage2_kernel takes one for the request's geometry, one for the log-sum-exps and
-// then one per 8 slots. Unused slots' partials are loaded (in bounds: part_stride >=
-// grid_slots) and dropped by a select. Measured: one request of 1024 tokens (32 slots) 11.5
-// -> 10.7 us per call; from 8 requests up it is slower than decode_stage2_kernel (more code
-// per slot, 1 us at B = 64, 7 us at B = 256).
+// decode_stage2_kernel takes one for the log-sum-exps (staged in LDS) and then one per 8
+// slots. Unused slots' partials are loaded (in bounds: part_stride >= grid_slots) and
+// dropped by a select. Measured: one request of 1024 tokens (32 slots) 11.5 -> 10.7 us per
+// call; from 8 requests up it is slower than decode_stage2_kernel (more code per slot,
+// 1 us at B = 64, 7 us at B = 256).
 constexpr int kChunk = 32;
 constexpr int kLatencyBatch = 4;
 
