@@ -15,7 +15,9 @@ MI355X addition: the kernel's workgroup reads all KV heads of a token range (who
 one workgroup each. batch_invariant uses seg = 256 = the split size (the reference's
 partition, independent of the batch); nondet/dvr take the largest of 256/128/64 that
 still gives 1.5 workgroups per CU for the batch's longest request, rounded up to a
-length bucket (so a HIP graph captured for a bucket computes the same plan).
+length bucket (so a HIP graph captured for a bucket computes the same plan), and
+plan_variant lengthens 256 to 512-2048 when the batch's real lengths still give two
+workgroups per CU. The stage-1 workgroup shape is picked with the plan (stage1_variant).
 
 B in the policy is the number of real requests. A caller that pads its batch with empty
 requests (graph replay at a fixed size) passes the real count as ``policy_batch``, so
