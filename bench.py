@@ -188,7 +188,7 @@ def attention_roofline(wl, reps):
         kp, vp = wl.kv.layer(layer)
         attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len, scale,
                      wl.invariant, policy_batch=fb.real_rows, variant=fb.decode_variant,
-                     geometry=fb.decode_geometry)
+                     geometry=fb.decode_geometry, wg_order=fb.decode_wg_order)
     torch.cuda.synchronize()
     # One event pair around reps x 28 back-to-back launches on the launch stream: the
     # average is the kernel's steady-state duration (launch overhead overlaps execution).
@@ -200,7 +200,8 @@ def attention_roofline(wl, reps):
             kp, vp = wl.kv.layer(layer)
             attn.forward(q, kp, vp, fb.kv_indptr, fb.kv_indices, fb.seq_lens, fb.max_seq_len,
                          scale, wl.invariant, policy_batch=fb.real_rows,
-                         variant=fb.decode_variant, geometry=fb.decode_geometry)
+                         variant=fb.decode_variant, geometry=fb.decode_geometry,
+                         wg_order=fb.decode_wg_order)
             launches += 1
     end.record()
     torch.cuda.synchronize()

@@ -70,9 +70,11 @@ def _paged(num_pages, lens, rng):
 
 def _attn_case(q, k, v, indptr, idx, lens):
     """Both split policies as the engine plans them (nondet: the heuristic splits, segment
-    size and stage-1 workgroup shape; batch_invariant: fixed 256-token splits), timed as the
-    model runs them: the plan once, then back-to-back kernel launches."""
-    from sid.kernels.decode_attention import DecodeAttention, plan_variant
+    size and stage-1 workgroup shape; batch_invariant: fixed 256-token splits; both with the
+    heaviest-first workgroup order), timed as the model runs them: the plan once, then
+    back-to-back kernel launches."""
+    from sid.kernels.decode_attention import (DecodeAttention, plan_variant, segment_tokens,
+                                              workgroup_order)
     from sid.kernels.jit import load_ext
     ext = load_ext()
     attn = DecodeAttention(len(lens), HQ, HKV, D, 32, 256, 32768, "cuda")
@@ -83,9 +85,13 @@ def _attn_case(q, k, v, indptr, idx, lens):
     for name, inv in (("nondet", False), ("fixed256", True)):
         geom, variant = plan_variant(lens, max(lens), HKV, attn.cu_count(), 32, inv)
         ns, grid, fixed, seg, slots = attn.plan(seq, max(lens), inv, geometry=geom)
+        tok = segment_tokens(lens, len(lens), grid, fixed, seg, slots)
+        order = None  # the engine's rule: an order once the busy segments fill the CUs
+        if int((tok > 0).sum()) >= attn.cu_count():
+            order = torch.from_numpy(workgroup_order(tok, attn.cu_count())).cuda()
         fn = lambda: ext.flash_decode_fwd(q, k, v, indptr, idx, ns, grid, fixed, D ** -0.5,
                                           attn.part_o, attn.part_lse, o, segment_size=seg,
-                                          grid_slots=slots, variant=variant)
+                                          grid_slots=slots, variant=variant, wg_order=order)
         us = _time_us(fn)
         out[name] = {"us_per_call": round(us, 2), "GB_s": round(bytes_ / us / 1e3, 1),
                      "frac_of_hbm_peak": round(bytes_ / us / 1e3 / HBM_PEAK_GBS, 4),

@@ -41,6 +41,7 @@ constexpr int HQ = HKV * QPK;
 constexpr bool kNonTemporal = true;  // K/V rows are streamed once: +9% HBM throughput
 constexpr int HEUR_TILE = 32;       // granularity of the heuristic split size
 constexpr float NEG_BIG = -1e30f;   // finite "minus infinity" for running maxima
+constexpr int kOrderSlotBits = 12;  // wg_order entries: request << 12 | slot
 
 __host__ __device__ __forceinline__ int kv_per_split(int seq_len, int n_splits, int fixed_split) {
   if (fixed_split > 0) return fixed_split;
@@ -126,10 +127,20 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
     const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ kv_indptr,
     const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ num_splits,
     int fixed_split, int seg, float sm_scale, int64_t num_slots, int part_stride,
-    float* __restrict__ part_o, float* __restrict__ part_lse, bf16_t* __restrict__ o_direct) {
+    float* __restrict__ part_o, float* __restrict__ part_lse, bf16_t* __restrict__ o_direct,
+    const int32_t* __restrict__ wg_order) {
   constexpr int IT = NW * TPL;  // tokens per workgroup iteration
-  const int b = blockIdx.x;
-  const int y = blockIdx.y;
+  // The (request, slot) this workgroup computes: its own grid position, or the entry of
+  // wg_order at its linear id (a permutation of the grid, heaviest segments first; only the
+  // placement changes, not what is computed).
+  int b = blockIdx.x;
+  int y = blockIdx.y;
+  if (wg_order != nullptr) {
+    const int packed = wg_order[blockIdx.x + blockIdx.y * gridDim.x];
+    b = packed >> kOrderSlotBits;
+    y = packed & ((1 << kOrderSlotBits) - 1);
+    if (b >= static_cast<int>(gridDim.x) || y >= static_cast<int>(gridDim.y)) return;
+  }
   const int tid = threadIdx.x;
   // Wave index as a wave-uniform value: token positions derived from it are uniform, so
   // slot indices come in through scalar loads with no per-lane branches.
@@ -438,13 +449,13 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
                   int batch, int64_t num_slots, int fixed_split_size, int seg, int grid_slots,
                   float sm_scale, float* part_o, float* part_lse, int part_stride, void* o,
-                  int variant, hipStream_t s) {
+                  int variant, const int32_t* wg_order, hipStream_t s) {
   const bool direct = (grid_slots == 1);
   auto stage1 = [&](auto kern, int nw) {
     hipLaunchKernelGGL(kern, dim3(batch, grid_slots), dim3(nw * 64), 0, s, (const bf16_t*)q,
                        (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr, kv_indices,
                        num_splits, fixed_split_size, seg, sm_scale, num_slots, part_stride, part_o,
-                       part_lse, direct ? (bf16_t*)o : nullptr);
+                       part_lse, direct ? (bf16_t*)o : nullptr, wg_order);
   };
   switch (variant) {
     case 1: stage1(decode_stage1_kernel<4, 1>, 4); break;
@@ -493,8 +504,8 @@ extern "C" int sid_flash_decode_segments_fwd(
     const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
     const int32_t* kv_indices, const int32_t* num_splits, int batch, int num_q_heads,
     int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
-    int segment_size, int grid_slots, int variant, float sm_scale, float* part_o,
-    float* part_lse, int part_batch, int part_stride, void* o, void* stream) {
+    int segment_size, int grid_slots, int variant, const int32_t* wg_order, float sm_scale,
+    float* part_o, float* part_lse, int part_batch, int part_stride, void* o, void* stream) {
   SID_REQUIRE(batch >= 0, "flash_decode_fwd: negative batch");
   SID_REQUIRE(variant >= 0 && variant < kNumVariants, "flash_decode_fwd: unknown variant %d",
               variant);
@@ -506,6 +517,8 @@ extern "C" int sid_flash_decode_segments_fwd(
   SID_REQUIRE(segment_size >= 0, "flash_decode_fwd: negative segment_size");
   SID_REQUIRE(grid_slots >= 1 && grid_slots <= kMaxGridSlots,
               "flash_decode_fwd: grid_slots %d out of range [1, %d]", grid_slots, kMaxGridSlots);
+  SID_REQUIRE(batch < (1 << (31 - kOrderSlotBits)) && kMaxGridSlots <= (1 << kOrderSlotBits),
+              "flash_decode_fwd: batch %d too large for the workgroup order", batch);
   if (grid_slots > 1) {
     SID_REQUIRE(part_o && part_lse, "flash_decode_fwd: null workspace");
     SID_REQUIRE(part_batch >= batch && part_stride >= grid_slots,
@@ -515,7 +528,7 @@ extern "C" int sid_flash_decode_segments_fwd(
   }
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, batch, num_slots,
                        fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       part_stride, o, variant, static_cast<hipStream_t>(stream));
+                       part_stride, o, variant, wg_order, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -528,8 +541,9 @@ extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const vo
   // One segment per split: the grid has exactly the reference's max_splits slots.
   return sid_flash_decode_segments_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                        batch, num_q_heads, num_kv_heads, head_dim, num_slots,
-                                       max_splits, fixed_split_size, 0, max_splits, 0, sm_scale,
-                                       part_o, part_lse, part_batch, part_stride, o, stream);
+                                       max_splits, fixed_split_size, 0, max_splits, 0, nullptr,
+                                       sm_scale, part_o, part_lse, part_batch, part_stride, o,
+                                       stream);
 }
 
 // ---- allocation-free entry point ------------------------------------------------------
@@ -578,7 +592,8 @@ extern "C" int sid_flash_decode_segments_fwd_noalloc(
     const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
     const int32_t* kv_indices, const int32_t* num_splits, int batch, int num_q_heads,
     int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
-    int segment_size, int grid_slots, int variant, float sm_scale, void* o, void* stream) {
+    int segment_size, int grid_slots, int variant, const int32_t* wg_order, float sm_scale,
+    void* o, void* stream) {
   using namespace sid;
   SID_REQUIRE(batch >= 0, "flash_decode_fwd_noalloc: negative batch");
   SID_REQUIRE(variant >= 0 && variant < kNumVariants,
@@ -612,5 +627,5 @@ extern "C" int sid_flash_decode_segments_fwd_noalloc(
   // Stage 2 reads only the slots stage 1 wrote in this call, so nothing is cleared.
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, batch, num_slots,
                        fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       grid_slots, o, variant, static_cast<hipStream_t>(stream));
+                       grid_slots, o, variant, wg_order, static_cast<hipStream_t>(stream));
 }

@@ -62,6 +62,7 @@ class ForwardBatch:
     seq_lens_host: Optional[np.ndarray] = None  # decode: kv length of each real row
     decode_variant: int = 0  # decode: stage-1 workgroup shape of the attention kernel
     decode_geometry: Optional[tuple] = None  # decode, nondet: plan_variant's attention geometry
+    decode_wg_order: Optional[torch.Tensor] = None  # decode: the attention's workgroup order
 
     def build_indices(self) -> None:
         """Enqueue the deferred kv_indices build (a no-op when the builder already ran it).
@@ -78,7 +79,7 @@ class DecodeStatic:
     host->device copy; the host block is reused only after the event of its previous copy
     has completed."""
 
-    def __init__(self, max_bs: int, kv_capacity: int, device):
+    def __init__(self, max_bs: int, kv_capacity: int, device, max_slots: int = 1):
         self.max_bs = max_bs
         n64, n32, nf = 8 * max_bs, 2 * max_bs + 1, 2 * max_bs
         o32 = 8 * n64
@@ -97,6 +98,21 @@ class DecodeStatic:
         self.kv_indices = torch.zeros(kv_capacity, dtype=torch.int32, device=device)
         self.copied = torch.cuda.Event()
         self.copied.record()
+        # the attention's workgroup order (known once the step's plan is), its own copy
+        self.order_host = torch.zeros(max_bs * max_slots, dtype=torch.int32, pin_memory=True)
+        self.order_dev = torch.zeros(max_bs * max_slots, dtype=torch.int32, device=device)
+        self.order_copied = torch.cuda.Event()
+        self.order_copied.record()
+
+    def set_order(self, order: np.ndarray) -> torch.Tensor:
+        """Queue the copy of a step's workgroup order; returns its fixed-address device view."""
+        n = order.size
+        self.order_copied.synchronize()  # the pinned block is free once its last copy ran
+        self.order_host.numpy()[:n] = order
+        dst = self.order_dev[:n]
+        dst.copy_(self.order_host[:n], non_blocking=True)
+        self.order_copied.record()
+        return dst
 
 
 def _sampling_host(reqs, repeat: int = 1):

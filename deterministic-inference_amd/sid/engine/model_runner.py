@@ -12,6 +12,7 @@ import logging
 import weakref
 from collections import OrderedDict
 
+import numpy as np
 import torch
 
 from sid.config import EngineConfig, Mode, ModelConfig
@@ -19,7 +20,8 @@ from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_buc
                               build_decode_batch, gather_prev_tokens)
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
-from sid.kernels.decode_attention import DecodeAttention, length_bucket, plan_variant
+from sid.kernels.decode_attention import (DecodeAttention, length_bucket, plan_variant,
+                                          segment_tokens, workgroup_order)
 from sid.kernels.matmul_persistent import linear_sample_supported
 from sid.model.loader import build_model_config, load_weights, random_weights
 from sid.model.qwen3 import Qwen3Model
@@ -134,8 +136,8 @@ class ModelRunner:
         if self.graphs is None:
             assert prev_rows is None or not (prev_rows >= 0).any(), "a pending token needs graphs"
             fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant)
-            if not invariant:
-                self._pick_variant(fb, len(reqs), fb.max_seq_len)
+            geom = None if invariant else self._pick_variant(fb, len(reqs), fb.max_seq_len)
+            self._attach_order(fb, len(reqs), invariant, fb.max_seq_len, geom)
             return fb
         static = self.graphs.decode_static
         pad = batch_bucket(len(reqs), static.max_bs)
@@ -151,8 +153,34 @@ class ModelRunner:
         plan = None
         if not invariant:
             plan = self._pick_variant(fb, len(reqs), bucket)
-        fb.graph_key = ("decode", pad, invariant, bucket, plan, fb.decode_variant)
+        ordered = self._attach_order(fb, pad, invariant, bucket, plan)
+        fb.graph_key = ("decode", pad, invariant, bucket, plan, fb.decode_variant, ordered)
         return fb
+
+    def _attach_order(self, fb: ForwardBatch, rows: int, invariant: bool, max_len: int,
+                      geom: tuple | None) -> bool:
+        """The attention's stage-1 workgroup order for this step (heaviest segments first,
+        balanced over the CUs; workgroup_order), from the host-known lengths and the plan the
+        forward will run: fixed splits in batch_invariant mode, else the nondet geometry.
+        Batches with fewer non-empty segments than CUs keep the grid's order (nothing to
+        balance, and reading the order first costs a small batch 0.2-0.4 us). Returns
+        whether an order was attached."""
+        da = self.decode_attn
+        if invariant:
+            tile = da.invariant_split_size
+            splits, fixed, seg, slots = 0, tile, tile, max(1, -(-max(max_len, 1) // tile))
+        else:
+            (splits, seg, slots), fixed = geom, 0
+        tokens = segment_tokens(fb.seq_lens_host, rows, splits, fixed, seg, slots)
+        fb.decode_wg_order = None
+        if int(np.count_nonzero(tokens)) < da.cu_count():
+            return False
+        order = workgroup_order(tokens, da.cu_count())
+        if self.graphs is not None:
+            fb.decode_wg_order = self.graphs.decode_static.set_order(order)
+        else:
+            fb.decode_wg_order = torch.from_numpy(order).to(self.device)
+        return True
 
     def _pick_variant(self, fb: ForwardBatch, bs: int, max_len: int) -> tuple:
         """The nondet plan's geometry and its stage-1 workgroup shape (fb.decode_variant),
@@ -198,7 +226,8 @@ class GraphCache:
                       "verify": torch.cuda.graph_pool_handle()}
         self._warm: set = set()
         self.decode_static = DecodeStatic(cfg.max_decode_batch,
-                                          cfg.max_decode_batch * cfg.max_seq_len, runner.device)
+                                          cfg.max_decode_batch * cfg.max_seq_len, runner.device,
+                                          max_slots=runner.decode_attn.ws_splits)
 
     def run(self, fb: ForwardBatch, greedy: bool = False, sample: bool = False) -> torch.Tensor:
         key = (fb.graph_key, greedy, sample)

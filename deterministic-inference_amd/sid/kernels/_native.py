@@ -38,11 +38,11 @@ _SIGNATURES = {
     "sid_argmax_rows": [_vp, _i64, _vp, _i64, _i64, _vp],
     "sid_build_paged_decode_indices": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _vp],
     "sid_flash_decode_segments_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
-                                      _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _i32, _i32,
-                                      _vp, _vp],
+                                      _i32, _i32, _i32, _i32, _i32, _vp, _f32, _vp, _vp, _i32,
+                                      _i32, _vp, _vp],
     "sid_flash_decode_segments_fwd_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
-                                              _i32, _i64, _i32, _i32, _i32, _i32, _i32, _f32,
-                                              _vp, _vp],
+                                              _i32, _i64, _i32, _i32, _i32, _i32, _i32, _vp,
+                                              _f32, _vp, _vp],
     "sid_sample_rows": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp],
     "sid_linear_sample": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i32,
                           _vp],
@@ -53,7 +53,7 @@ EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward",
             "sid_flash_decode_noalloc_scratch_bytes", "sid_linear_sample_workspace_bytes",
             *_SIGNATURES)
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -109,10 +109,11 @@ class NativeLib:
     def flash_decode_fwd(self, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                          max_splits: int, fixed_split_size: int, sm_scale: float,
                          part_o, part_lse, o, segment_size: int = 0,
-                         grid_slots: int | None = None, variant: int = 0) -> None:
-        """segment_size / grid_slots / variant: see sid_flash_decode_segments_fwd (defaults:
-        one segment per split, grid of max_splits slots = the reference's partition, the
-        default workgroup shape)."""
+                         grid_slots: int | None = None, variant: int = 0,
+                         wg_order=None) -> None:
+        """segment_size / grid_slots / variant / wg_order: see sid_flash_decode_segments_fwd
+        (defaults: one segment per split, grid of max_splits slots = the reference's
+        partition, the default workgroup shape, the grid's own order)."""
         _gpu(q, "q", torch.bfloat16)
         _check(q.dim() == 3, "q must be [B, HQ, D]")
         b, hq, d = q.shape
@@ -136,17 +137,19 @@ class NativeLib:
         _gpu(o, "o", torch.bfloat16)
         _check(o.shape == q.shape, "o must have q's shape")
         slots = int(max_splits) if grid_slots is None else int(grid_slots)
+        order = self._order_ptr(wg_order, b * slots)
         self._call("sid_flash_decode_segments_fwd", q.data_ptr(), k_cache.data_ptr(),
                    v_cache.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
                    num_splits.data_ptr(), b, hq, hkv, d, k_cache.shape[0], int(max_splits),
-                   int(fixed_split_size), int(segment_size), slots, int(variant), float(sm_scale),
+                   int(fixed_split_size), int(segment_size), slots, int(variant), order,
+                   float(sm_scale),
                    part_o.data_ptr(), part_lse.data_ptr(), part_o.shape[0], part_o.shape[2],
                    o.data_ptr(), _stream(q))
 
     def flash_decode_fwd_noalloc(self, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                  max_splits: int, fixed_split_size: int, sm_scale: float, o,
                                  segment_size: int = 0, grid_slots: int | None = None,
-                                 variant: int = 0) -> None:
+                                 variant: int = 0, wg_order=None) -> None:
         """flash_decode_fwd with the split partials in the library's static per-GPU scratch
         (no workspace argument, nothing allocated). Calls that overlap on one GPU race."""
         _gpu(q, "q", torch.bfloat16)
@@ -164,11 +167,20 @@ class NativeLib:
         _gpu(o, "o", torch.bfloat16)
         _check(o.shape == q.shape, "o must have q's shape")
         slots = int(max_splits) if grid_slots is None else int(grid_slots)
+        order = self._order_ptr(wg_order, b * slots)
         self._call("sid_flash_decode_segments_fwd_noalloc", q.data_ptr(), k_cache.data_ptr(),
                    v_cache.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
                    num_splits.data_ptr(), b, hq, k_cache.shape[1], d, k_cache.shape[0],
                    int(max_splits), int(fixed_split_size), int(segment_size), slots,
-                   int(variant), float(sm_scale), o.data_ptr(), _stream(q))
+                   int(variant), order, float(sm_scale), o.data_ptr(), _stream(q))
+
+    @staticmethod
+    def _order_ptr(wg_order, n: int) -> int:
+        if wg_order is None:
+            return 0
+        _gpu(wg_order, "wg_order", torch.int32)
+        _check(wg_order.numel() >= n, "wg_order must have B * grid_slots entries")
+        return wg_order.data_ptr()
 
     def reshape_and_cache(self, k, v, k_cache, v_cache, slot_mapping) -> None:
         _gpu(k, "k", torch.bfloat16)

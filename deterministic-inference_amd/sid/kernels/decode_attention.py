@@ -163,6 +163,63 @@ def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv
     return geom, stage1_variant(wg, full, cu_count, invariant=False)
 
 
+ORDER_SLOT_BITS = 12  # sid_flash_decode_segments_fwd wg_order entries: request << 12 | slot
+
+
+def segment_tokens(lengths, rows: int, splits: int, fixed_split: int, seg: int,
+                   slots: int) -> np.ndarray:
+    """int64 [slots, rows]: tokens of partial slot y of request b, as the kernel's
+    segment_range cuts them (rows past len(lengths) are empty padding). fixed_split > 0 is
+    the batch_invariant plan (one segment per fixed split); else the nondet plan of
+    `splits` grid splits, min(splits, ceil(len/32)) per request, segments of at most seg."""
+    lens = np.zeros(rows, dtype=np.int64)
+    lens[:len(lengths)] = np.asarray(lengths, dtype=np.int64)
+    pos = lens > 0
+    safe = np.maximum(lens, 1)
+    if fixed_split > 0:
+        n = -(-lens // fixed_split)
+        chunk = np.full(rows, fixed_split, dtype=np.int64)
+    else:
+        n = np.where(pos, np.minimum(splits, -(-safe // 32)), 0)
+        chunk = -(-(-(-safe // np.maximum(n, 1))) // 32) * 32
+    sl = np.minimum(seg, chunk) if seg > 0 else chunk
+    sps = -(-chunk // sl)
+    y = np.arange(slots, dtype=np.int64)[:, None]
+    s = y // sps
+    split_start = s * chunk
+    split_end = np.minimum(split_start + chunk, lens)
+    start = split_start + (y % sps) * sl
+    end = np.minimum(start + sl, split_end)
+    return np.where(s < n, np.maximum(end - start, 0), 0)
+
+
+def workgroup_order(tokens: np.ndarray, cu_count: int) -> np.ndarray:
+    """The stage-1 workgroup order (wg_order) for segment sizes tokens[slot, request]:
+    heaviest segments first (ties in the grid's own order, request fastest), dealt to
+    linear ids in rounds of cu_count, every other full round reversed when its segments
+    differ in size, so the segments that share a CU balance (the longest-processing-time
+    rule; empty slots go last). Uniform batches keep the grid's order. Only the placement
+    changes, never a result. Measured on ragged batches: lognormal lengths B = 64 54.8 ->
+    33.9 us, B = 128 112.5 -> 83.6, B = 256 200.7 -> 167.6; config 2 53.2 -> 47.8."""
+    slots, rows = tokens.shape
+    n = slots * rows
+    flat = tokens.reshape(-1)  # index = y * rows + b = the grid's linear id
+    rank = np.lexsort((np.arange(n), -flat))
+    p = max(int(cu_count), 1)
+    r = np.arange(n)
+    rnd, j = r // p, r % p
+    work = flat[rank]
+    nr = -(-n // p)
+    pad = np.full(nr * p, work[-1] if n else 0, dtype=work.dtype)
+    pad[:n] = work
+    varied = pad.reshape(nr, p).max(axis=1) != pad.reshape(nr, p).min(axis=1)
+    flip = (rnd % 2 == 1) & ((rnd + 1) * p <= n) & varied[rnd]
+    pos = rnd * p + np.where(flip, p - 1 - j, j)
+    order = np.empty(n, dtype=np.int32)
+    order[pos] = ((rank % rows) << ORDER_SLOT_BITS) | (rank // rows)
+    return order
+
+
 def workspace_slots(max_seq_len: int, max_kv_splits: int, invariant_split_size: int) -> int:
     """Partial slots per request the workspace must hold for any plan."""
     nondet = -(-max_seq_len // SEGMENT_SIZES[-1]) + max_kv_splits
@@ -224,12 +281,14 @@ class DecodeAttention:
                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, seq_lens: torch.Tensor,
                 max_seq_len: int, sm_scale: float, invariant: bool,
                 policy_batch: int | None = None, variant: int = 0,
-                geometry: tuple | None = None) -> torch.Tensor:
+                geometry: tuple | None = None,
+                wg_order: torch.Tensor | None = None) -> torch.Tensor:
         """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync).
         policy_batch: real requests among the B rows (the rest are empty padding); variant:
         the stage-1 workgroup shape (stage1_variant; 0 in batch_invariant mode); geometry:
         plan_variant's nondet geometry for this batch (None: from the batch size and
-        max_seq_len alone)."""
+        max_seq_len alone); wg_order: workgroup_order of this plan, on the device (None: the
+        grid's own order)."""
         assert not (invariant and variant), "batch_invariant mode keeps the default shape"
         bs = q.shape[0]
         assert bs <= self.part_o.shape[0], "decode batch exceeds workspace"
@@ -245,5 +304,6 @@ class DecodeAttention:
         o = torch.empty_like(q)
         self.ext.flash_decode_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                   grid_splits, fixed, sm_scale, self.part_o, self.part_lse, o,
-                                  segment_size=seg, grid_slots=slots, variant=variant)
+                                  segment_size=seg, grid_slots=slots, variant=variant,
+                                  wg_order=wg_order)
         return o

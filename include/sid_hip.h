@@ -89,16 +89,22 @@ int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache
  * waves x 4 tokens per wave iteration (what sid_flash_decode_fwd uses), 1 =
  * 4 x 1 (full, HBM-bound grids), 2 = 8 x 2 (fewer workgroups than CUs), 3 =
  * 4 x 2 (in between); a fixed variant keeps the batch independence of fixed
- * splits.
+ * splits. wg_order (may be NULL): int32 [batch * grid_slots], a permutation of
+ * the grid's (request, slot) pairs packed as request << 12 | slot; the
+ * stage-1 workgroup with linear id b + batch * y computes the pair at entry
+ * b + batch * y. It changes which workgroup runs which segment, never the
+ * result (a heaviest-first order balances ragged batches over the CUs);
+ * entries outside the grid are skipped, so a map that is not a permutation
+ * leaves partials unwritten (ABI 15).
  */
 int sid_flash_decode_segments_fwd(const void* q, const void* k_cache, const void* v_cache,
                                   const int32_t* kv_indptr, const int32_t* kv_indices,
                                   const int32_t* num_splits, int batch, int num_q_heads,
                                   int num_kv_heads, int head_dim, int64_t num_slots,
                                   int max_splits, int fixed_split_size, int segment_size,
-                                  int grid_slots, int variant, float sm_scale, float* part_o,
-                                  float* part_lse, int part_batch, int part_stride, void* o,
-                                  void* stream);
+                                  int grid_slots, int variant, const int32_t* wg_order,
+                                  float sm_scale, float* part_o, float* part_lse, int part_batch,
+                                  int part_stride, void* o, void* stream);
 
 /*
  * No counterpart in the reference. For callers that cannot allocate device
@@ -122,7 +128,8 @@ int sid_flash_decode_segments_fwd_noalloc(const void* q, const void* k_cache,
                                           int batch, int num_q_heads, int num_kv_heads,
                                           int head_dim, int64_t num_slots, int max_splits,
                                           int fixed_split_size, int segment_size,
-                                          int grid_slots, int variant, float sm_scale, void* o,
+                                          int grid_slots, int variant, const int32_t* wg_order,
+                                          float sm_scale, void* o,
                                           void* stream);
 
 /* Size of that scratch array in bytes (SID_DECODE_SCRATCH_BYTES). */

@@ -160,3 +160,75 @@ def test_long_segments_only_with_two_workgroups_per_cu():
     geom, _ = plan_variant([1024] * 255 + [1], 1024, 8, cu, 32, invariant=False)
     assert geom[1] == 256                                      # 511 workgroups
     assert plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=True) == (None, 0)
+
+
+def _walk_tokens(n, splits, fixed, seg):
+    """Token count of every partial slot of one request, walking its splits and segments."""
+    if n <= 0:
+        return []
+    if fixed:
+        s, chunk = -(-n // fixed), fixed
+    else:
+        s = min(splits, -(-n // 32))
+        chunk = -(-(-(-n // s)) // 32) * 32
+    sl = min(seg, chunk) if seg > 0 else chunk
+    sps = -(-chunk // sl)
+    out = []
+    for i in range(s):
+        a, b = i * chunk, min((i + 1) * chunk, n)
+        for j in range(sps):
+            st = a + j * sl
+            out.append(max(0, min(st + sl, b) - st))
+    return out
+
+
+@pytest.mark.parametrize("plan", [(1, 0, 256), (32, 0, 64), (4, 0, 128), (0, 256, 256), (2, 0, 512)])
+def test_segment_tokens_match_the_kernel_partition(plan):
+    """segment_tokens (the host mirror of the kernel's segment_range) gives every slot's token
+    count: the slot-by-slot walk of each request's splits and segments, zeros for padding
+    rows and for slots past a request's last segment."""
+    import numpy as np
+
+    from sid.kernels.decode_attention import segment_tokens
+    splits, fixed, seg = plan
+    rng = random.Random(7)
+    lens = [rng.randint(1, 5000) for _ in range(37)] + [1, 31, 32, 33, 255, 256, 257]
+    walks = [_walk_tokens(n, splits, fixed, seg) for n in lens]
+    slots = max(len(w) for w in walks) + 3
+    tok = segment_tokens(lens, len(lens) + 5, splits, fixed, seg, slots)
+    assert tok.shape == (slots, len(lens) + 5)
+    for b, w in enumerate(walks):
+        assert tok[:len(w), b].tolist() == w
+        assert not tok[len(w):, b].any()
+    assert not tok[:, len(lens):].any()
+    assert int(tok.sum()) == sum(lens)
+
+
+def test_workgroup_order_is_a_balanced_permutation():
+    """workgroup_order is a permutation of the grid (request << 12 | slot), heaviest segments
+    first in rounds of cu_count with every other full round of unequal segments reversed,
+    ties in the grid's own order (so a uniform batch keeps the grid's order)."""
+    import numpy as np
+
+    from sid.kernels.decode_attention import ORDER_SLOT_BITS, workgroup_order
+    rng = np.random.default_rng(3)
+    slots, rows, cu = 11, 50, 16
+    tok = rng.integers(0, 300, size=(slots, rows))
+    tok[rng.random((slots, rows)) < 0.3] = 0
+    order = workgroup_order(tok, cu)
+    b, y = order >> ORDER_SLOT_BITS, order & ((1 << ORDER_SLOT_BITS) - 1)
+    assert sorted((y * rows + b).tolist()) == list(range(slots * rows))
+    work = tok[y, b]
+    n = order.size
+    ranked = []
+    for k in range(0, n, cu):
+        chunk = work[k:k + cu].tolist()
+        rnd = k // cu
+        if rnd % 2 == 1 and k + cu <= n and len(set(chunk)) > 1:
+            chunk = chunk[::-1]
+        ranked += chunk
+    assert ranked == sorted(work.tolist(), reverse=True)
+    # equal work keeps the grid's order (request fastest), over several full rounds too
+    flat = np.full((4, 6), 7, dtype=np.int64)
+    assert workgroup_order(flat, 4).tolist() == [(b << ORDER_SLOT_BITS) | y
+                                                for y in range(4) for b in range(6)]

@@ -146,6 +146,46 @@ def test_long_segment_plans_vs_oracle(lens):
     assert_close_bf16(out, decode_attention_ref(q, k, v, indptr, idx, SCALE))
 
 
+@pytest.mark.parametrize("policy", ["heuristic", "fixed256", "seg64"])
+def test_workgroup_order_does_not_change_bits(policy):
+    """The heaviest-first workgroup order (wg_order) only moves segments between workgroups:
+    outputs are bitwise those of the grid's own order, for ragged batches with empty
+    requests, through the workspace and the allocation-free entry points (NaN-prefilled
+    workspaces: every partial the merge reads is written in the same call)."""
+    from sid.kernels.decode_attention import segment_tokens, workgroup_order
+    ext = _ext()
+    rng = np.random.default_rng(12)
+    lens = [int(x) for x in np.minimum(rng.lognormal(np.log(400), 1.0, 40), 6000).astype(int)]
+    lens[3] = 0
+    lens[17] = 1
+    q, k, v, indptr, idx = decode_inputs(lens, seed=13)
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    if policy == "fixed256":
+        ns, grid = plan_fixed(lens)
+        fixed, seg, slots = 256, 256, grid
+    else:
+        ns, grid = plan_heuristic(lens, cu, HKV, 32)
+        fixed, seg = 0, (256 if policy == "heuristic" else 64)
+        slots = _slots(lens, ns, fixed, seg)
+    tok = segment_tokens(lens, len(lens), grid, fixed, seg, slots)
+    order = torch.from_numpy(workgroup_order(tok, cu)).cuda()
+    print(f"policy={policy} slots={slots} busy={(tok > 0).sum()}", flush=True)
+    plain = _run(q, k, v, indptr, idx, ns, grid, fixed, seg=seg, slots=slots)
+    part_o = torch.full((len(lens), HQ, slots, D), float("nan"), device="cuda")
+    part_lse = torch.full((len(lens), HQ, slots), float("nan"), device="cuda")
+    o = torch.empty_like(q)
+    nst = torch.tensor(ns, dtype=torch.int32, device="cuda")
+    ext.flash_decode_fwd(q, k, v, indptr, idx, nst, grid, fixed, SCALE, part_o, part_lse, o,
+                         segment_size=seg, grid_slots=slots, wg_order=order)
+    assert torch.equal(o, plain)
+    o2 = torch.empty_like(q)
+    ext.flash_decode_fwd_noalloc(q, k, v, indptr, idx, nst, grid, fixed, SCALE, o2,
+                                 segment_size=seg, grid_slots=slots, wg_order=order)
+    assert torch.equal(o2, plain)
+    assert (o[3] == 0).all()
+    assert_close_bf16(o, decode_attention_ref(q, k, v, indptr, idx, SCALE))
+
+
 def test_direct_single_split_equals_two_stage():
     """Grid 1 writes o directly; a grid of 2 with every request on one split runs the
     merge pass. Both must give the same bits (merge of one split is the identity)."""
