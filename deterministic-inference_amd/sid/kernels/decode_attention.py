@@ -109,26 +109,23 @@ def nonempty_workgroups(lengths, splits: int, seg: int) -> int:
 # Stage-1 workgroup shapes (sid_flash_decode_segments_fwd `variant`): 0 = 4 waves x 4 tokens
 # per iteration, 1 = 4 x 1, 2 = 8 x 2, 3 = 4 x 2. The shape is part of the in-segment
 # reduction order. batch_invariant keeps 0 for every batch (results depend on the request
-# alone); nondet/dvr pick by the number of non-empty workgroups W against the CU count and by
-# how ragged the batch is, measured on 20 shapes (uniform and lognormal lengths, B = 1..256):
-# a full grid of at least two workgroups per CU is HBM-bound and runs best with the fewest
-# registers (1: config 3, 91.5 -> 88.9 us); fewer workgroups than CUs are bound by each
-# workgroup's chain of round trips (2: lognormal B = 64, 77.7 -> 60.1 us; B = 1, ctx 1024,
-# 13.3 -> 12.5 us); a grid at least half as full as its longest request would make it runs
-# best with 3 (config 2, 59.3 -> 56.1 us; uniform B = 48 x 2k, 73.6 -> 70.3 us); very ragged
-# batches with 0 (lognormal B = 128, 130.9 us against 142.0 with 3).
-def stage1_variant(workgroups: int, grid_workgroups: int, cu_count: int, invariant: bool) -> int:
-    """grid_workgroups: the non-empty workgroups if every request were as long as the longest
-    (workgroups / grid_workgroups < 1 measures how ragged the batch is)."""
+# alone); nondet/dvr pick by the number of non-empty workgroups W against the CU count.
+# Fewer workgroups than CUs are bound by each workgroup's chain of round trips: 8 x 2 (B = 1,
+# ctx 1024, 13.3 -> 12.5 us; lognormal B = 64 77.7 -> 60.1 us). One to two per CU: 4 x 2
+# (config 2, 59.3 -> 56.1 us). Two or more per CU are HBM-bound and run best with the fewest
+# registers: 4 x 1 (config 3, 91.5 -> 88.9 us). Ragged batches used to keep 4 x 4, which
+# copes best with CUs left idle at the end; with the heaviest-first workgroup order
+# (workgroup_order, used from W >= CUs) the W rule alone is as fast or faster on all 15
+# shapes measured (lognormal B = 256 154.2 -> 145.6 us, B = 128 84.3 -> 81.4 us).
+def stage1_variant(workgroups: int, cu_count: int, invariant: bool) -> int:
+    """The stage-1 workgroup shape for a plan with `workgroups` non-empty workgroups."""
     if invariant:
         return 0
-    if workgroups >= 2 * cu_count and workgroups >= 0.9 * grid_workgroups:
-        return 1
     if workgroups < cu_count:
         return 2
-    if workgroups >= 0.5 * grid_workgroups:
+    if workgroups < 2 * cu_count:
         return 3
-    return 0
+    return 1
 
 
 # Long segments for large batches: the longest of LONG_SEGMENTS that still gives every CU two
@@ -157,10 +154,7 @@ def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv
                 seg = long_seg
                 geom = (splits, seg, splits * max(1, _cdiv(chunk_max, seg)))
                 break
-    wg = nonempty_workgroups(lens, splits, seg)
-    # the workgroups if every request were as long as the longest (the batch's raggedness)
-    full = len(lens) * nonempty_workgroups([int(lens.max())], splits, seg) if lens.size else 0
-    return geom, stage1_variant(wg, full, cu_count, invariant=False)
+    return geom, stage1_variant(nonempty_workgroups(lens, splits, seg), cu_count, invariant=False)
 
 
 ORDER_SLOT_BITS = 12  # sid_flash_decode_segments_fwd wg_order entries: request << 12 | slot

@@ -129,12 +129,13 @@ def test_nonempty_workgroups_brute_force():
 
 def test_stage1_variant_rule():
     from sid.kernels.decode_attention import stage1_variant
-    assert stage1_variant(576, 576, 256, invariant=False) == 1     # full, >= 2 per CU
-    assert stage1_variant(576, 576, 256, invariant=True) == 0      # invariant: fixed shape
-    assert stage1_variant(230, 896, 256, invariant=False) == 2     # fewer than the CUs
-    assert stage1_variant(600, 2176, 256, invariant=False) == 0    # ragged, in between
-    assert stage1_variant(270, 512, 256, invariant=False) == 3     # half full, in between
-    assert stage1_variant(32, 32, 256, invariant=False) == 2
+    assert stage1_variant(576, 256, invariant=False) == 1     # >= 2 per CU
+    assert stage1_variant(512, 256, invariant=False) == 1
+    assert stage1_variant(576, 256, invariant=True) == 0      # invariant: fixed shape
+    assert stage1_variant(230, 256, invariant=False) == 2     # fewer than the CUs
+    assert stage1_variant(32, 256, invariant=False) == 2
+    assert stage1_variant(256, 256, invariant=False) == 3     # one to two per CU
+    assert stage1_variant(511, 256, invariant=False) == 3
 
 
 def test_long_segments_only_with_two_workgroups_per_cu():
