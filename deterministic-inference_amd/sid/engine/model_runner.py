@@ -20,8 +20,8 @@ from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_buc
                               build_decode_batch, gather_prev_tokens)
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
-from sid.kernels.decode_attention import (DecodeAttention, length_bucket, plan_variant,
-                                          segment_tokens, workgroup_order)
+from sid.kernels.decode_attention import (INVARIANT_VARIANT, DecodeAttention, length_bucket,
+                                          plan_variant, segment_tokens, workgroup_order)
 from sid.kernels.matmul_persistent import linear_sample_supported
 from sid.model.loader import build_model_config, load_weights, random_weights
 from sid.model.qwen3 import Qwen3Model
@@ -136,6 +136,8 @@ class ModelRunner:
         if self.graphs is None:
             assert prev_rows is None or not (prev_rows >= 0).any(), "a pending token needs graphs"
             fb = build_decode_batch(reqs, self.kv_cache, self.device, invariant)
+            if invariant:
+                fb.decode_variant = INVARIANT_VARIANT
             geom = None if invariant else self._pick_variant(fb, len(reqs), fb.max_seq_len)
             self._attach_order(fb, len(reqs), invariant, fb.max_seq_len, geom)
             return fb
@@ -151,7 +153,9 @@ class ModelRunner:
         bucket = length_bucket(fb.max_seq_len)
         fb.max_seq_len = bucket
         plan = None
-        if not invariant:
+        if invariant:
+            fb.decode_variant = INVARIANT_VARIANT
+        else:
             plan = self._pick_variant(fb, len(reqs), bucket)
         ordered = self._attach_order(fb, pad, invariant, bucket, plan)
         fb.graph_key = ("decode", pad, invariant, bucket, plan, fb.decode_variant, ordered)

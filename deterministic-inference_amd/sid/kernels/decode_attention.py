@@ -108,8 +108,11 @@ def nonempty_workgroups(lengths, splits: int, seg: int) -> int:
 
 # Stage-1 workgroup shapes (sid_flash_decode_segments_fwd `variant`): 0 = 4 waves x 4 tokens
 # per iteration, 1 = 4 x 1, 2 = 8 x 2, 3 = 4 x 2. The shape is part of the in-segment
-# reduction order. batch_invariant keeps 0 for every batch (results depend on the request
-# alone); nondet/dvr pick by the number of non-empty workgroups W against the CU count.
+# reduction order. batch_invariant uses one shape for every batch (results depend on the
+# request alone): 8 x 2, which with the heaviest-first order is the fastest fixed choice
+# (0.935 x the time of 4 x 4 over 11 shapes from one request to B = 256: small batches 10-15%
+# faster, config 3's shape 2.5%, lognormal B = 128 8%; B = 256 x 1024 0.4% slower). nondet/dvr
+# pick by the number of non-empty workgroups W against the CU count.
 # Fewer workgroups than CUs are bound by each workgroup's chain of round trips: 8 x 2 (B = 1,
 # ctx 1024, 13.3 -> 12.5 us; lognormal B = 64 77.7 -> 60.1 us). One to two per CU: 4 x 2
 # (config 2, 59.3 -> 56.1 us). Two or more per CU are HBM-bound and run best with the fewest
@@ -117,10 +120,13 @@ def nonempty_workgroups(lengths, splits: int, seg: int) -> int:
 # copes best with CUs left idle at the end; with the heaviest-first workgroup order
 # (workgroup_order, used from W >= CUs) the W rule alone is as fast or faster on all 15
 # shapes measured (lognormal B = 256 154.2 -> 145.6 us, B = 128 84.3 -> 81.4 us).
+INVARIANT_VARIANT = 2
+
+
 def stage1_variant(workgroups: int, cu_count: int, invariant: bool) -> int:
     """The stage-1 workgroup shape for a plan with `workgroups` non-empty workgroups."""
     if invariant:
-        return 0
+        return INVARIANT_VARIANT
     if workgroups < cu_count:
         return 2
     if workgroups < 2 * cu_count:
@@ -143,7 +149,7 @@ def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv
     the (possibly bucketed) bound the plan is built for. The geometry (grid splits, segment
     size, grid slots) is what DecodeAttention.forward runs when given it."""
     if invariant:
-        return None, 0
+        return None, INVARIANT_VARIANT
     lens = np.asarray(lengths, dtype=np.int64)
     geom = nondet_geometry(len(lens), max_len, num_kv_heads, cu_count, max_kv_splits)
     splits, seg, slots = geom
@@ -274,16 +280,20 @@ class DecodeAttention:
     def forward(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, seq_lens: torch.Tensor,
                 max_seq_len: int, sm_scale: float, invariant: bool,
-                policy_batch: int | None = None, variant: int = 0,
+                policy_batch: int | None = None, variant: int | None = None,
                 geometry: tuple | None = None,
                 wg_order: torch.Tensor | None = None) -> torch.Tensor:
         """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync).
         policy_batch: real requests among the B rows (the rest are empty padding); variant:
-        the stage-1 workgroup shape (stage1_variant; 0 in batch_invariant mode); geometry:
+        the stage-1 workgroup shape (stage1_variant; None: INVARIANT_VARIANT in batch_invariant
+        mode, else 0); geometry:
         plan_variant's nondet geometry for this batch (None: from the batch size and
         max_seq_len alone); wg_order: workgroup_order of this plan, on the device (None: the
         grid's own order)."""
-        assert not (invariant and variant), "batch_invariant mode keeps the default shape"
+        if variant is None:
+            variant = INVARIANT_VARIANT if invariant else 0
+        assert not invariant or variant == INVARIANT_VARIANT, \
+            "batch_invariant mode runs one fixed workgroup shape"
         bs = q.shape[0]
         assert bs <= self.part_o.shape[0], "decode batch exceeds workspace"
         # One plan per forward: every layer sees the same seq_lens tensor.

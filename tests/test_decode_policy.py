@@ -131,7 +131,8 @@ def test_stage1_variant_rule():
     from sid.kernels.decode_attention import stage1_variant
     assert stage1_variant(576, 256, invariant=False) == 1     # >= 2 per CU
     assert stage1_variant(512, 256, invariant=False) == 1
-    assert stage1_variant(576, 256, invariant=True) == 0      # invariant: fixed shape
+    assert stage1_variant(576, 256, invariant=True) == 2      # invariant: one fixed shape
+    assert stage1_variant(3, 256, invariant=True) == 2
     assert stage1_variant(230, 256, invariant=False) == 2     # fewer than the CUs
     assert stage1_variant(32, 256, invariant=False) == 2
     assert stage1_variant(256, 256, invariant=False) == 3     # one to two per CU
@@ -160,7 +161,7 @@ def test_long_segments_only_with_two_workgroups_per_cu():
     assert geom[1] == 256                                      # ragged B = 128: too few
     geom, _ = plan_variant([1024] * 255 + [1], 1024, 8, cu, 32, invariant=False)
     assert geom[1] == 256                                      # 511 workgroups
-    assert plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=True) == (None, 0)
+    assert plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=True) == (None, 2)
 
 
 def _walk_tokens(n, splits, fixed, seg):
