@@ -170,3 +170,16 @@ def test_argmax_first_index_and_nan():
     got = argmax_rows(x)
     assert got.tolist() == torch.argmax(x.cpu(), dim=-1).tolist()
     assert got[1] == 100 and got[2] == 0 and got[3] == 5000
+
+
+@pytest.mark.parametrize("cols", [33, 4001, 8192 * 4 + 3, 151936])
+def test_argmax_row_widths(cols):
+    """Every column path of the row loop: whole 8192-vector passes, the guarded last pass,
+    unaligned rows (odd widths) and the scalar tail; the maximum placed in each region."""
+    from sid.kernels.ops import argmax_rows
+    torch.manual_seed(cols)
+    x = torch.randn(6, cols, device="cuda")
+    for r, c in enumerate((0, cols // 3, cols - 5, cols - 1, min(cols - 1, 4 * 8192), 2)):
+        x[r, c] = 100.0
+    got = argmax_rows(x)
+    assert got.tolist() == torch.argmax(x.cpu(), dim=-1).tolist()
