@@ -262,7 +262,12 @@ constexpr int TT_KS = TT_K + 16;
 constexpr int TT_SUB_PER_CHUNK = KC / TT_K;
 
 // WM x WN waves; wave (wm, wn) owns MB x NB MFMA blocks = (16 MB) x (16 NB) outputs.
-template <int WM, int WN, int MB, int NB>
+// PF = 1: the next sub-tile is loaded into registers during the current one's MFMAs, and the
+// compiler schedules the loads among them (best when the grid fills the chip: the MFMAs
+// are the bound). PF = 2: a ring of two register buffers keeps two sub-tiles in flight,
+// issued at fixed points (best for grids of at most one workgroup per CU, where every
+// sub-tile's global-memory latency would otherwise be exposed). Same arithmetic either way.
+template <int WM, int WN, int MB, int NB, int PF>
 __global__ void __launch_bounds__(WM * WN * 64) linear_tiled_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ bias, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
@@ -304,21 +309,22 @@ __global__ void __launch_bounds__(WM * WN * 64) linear_tiled_kernel(
     bvec[i] = v & 7;
     wrow[i] = w + min<int64_t>(n0 + brow[i], N - 1) * K + bvec[i] * 8;
   }
-  bf16x8_v ra[LA], rb[LB];
-  auto load_sub = [&](int kt) {
+  static_assert(PF == 1 || PF == 2 || PF == 4, "PF must divide the 4 sub-tiles of a chunk");
+  bf16x8_v ra[PF][LA], rb[PF][LB];
+  auto load_sub = [&](int kt, bf16x8_v (&da)[LA], bf16x8_v (&db)[LB]) {
     const int64_t k0 = static_cast<int64_t>(kt) * TT_K;
 #pragma unroll
-    for (int i = 0; i < LA; ++i) ra[i] = ld_frag(xrow[i] + k0);
+    for (int i = 0; i < LA; ++i) da[i] = ld_frag(xrow[i] + k0);
 #pragma unroll
-    for (int i = 0; i < LB; ++i) rb[i] = ld_frag(wrow[i] + k0);
+    for (int i = 0; i < LB; ++i) db[i] = ld_frag(wrow[i] + k0);
   };
-  auto store_sub = [&](int buf) {
+  auto store_sub = [&](int buf, const bf16x8_v (&da)[LA], const bf16x8_v (&db)[LB]) {
 #pragma unroll
     for (int i = 0; i < LA; ++i)
-      *reinterpret_cast<bf16x8_v*>(&sa[buf][arow[i] * TT_KS + avec[i] * 8]) = ra[i];
+      *reinterpret_cast<bf16x8_v*>(&sa[buf][arow[i] * TT_KS + avec[i] * 8]) = da[i];
 #pragma unroll
     for (int i = 0; i < LB; ++i)
-      *reinterpret_cast<bf16x8_v*>(&sb[buf][brow[i] * TT_KS + bvec[i] * 8]) = rb[i];
+      *reinterpret_cast<bf16x8_v*>(&sb[buf][brow[i] * TT_KS + bvec[i] * 8]) = db[i];
   };
 
   f32x4_v acc[MB][NB], tot[MB][NB];
@@ -327,13 +333,8 @@ __global__ void __launch_bounds__(WM * WN * 64) linear_tiled_kernel(
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  const int nsub = static_cast<int>(K / TT_K);
-  load_sub(0);
-  store_sub(0);
-  __syncthreads();
-  for (int kt = 0; kt < nsub; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nsub) load_sub(kt + 1);
+  // One sub-tile's MFMAs out of LDS buffer `cur`, and the fold at the end of a chunk.
+  auto mma_sub = [&](int cur) {
 #pragma unroll
     for (int s = 0; s < TT_K / KSTEP; ++s) {
       bf16x8_v af[MB], bfv[NB];
@@ -352,25 +353,63 @@ __global__ void __launch_bounds__(WM * WN * 64) linear_tiled_kernel(
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mb], bfv[nb], acc[mb][nb], 0, 0, 0);
       }
     }
-    if (kt % TT_SUB_PER_CHUNK == TT_SUB_PER_CHUNK - 1) {  // chunk complete: fold, restart
-      const bool first = kt < TT_SUB_PER_CHUNK;
+  };
+  auto fold = [&](bool first) {  // chunk complete: fold, restart
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          if (first) {
-            tot[mb][nb] = acc[mb][nb];
-          } else {
+      for (int nb = 0; nb < NB; ++nb) {
+        if (first) {
+          tot[mb][nb] = acc[mb][nb];
+        } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) tot[mb][nb][i] += acc[mb][nb][i];
-          }
-          acc[mb][nb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+          for (int i = 0; i < 4; ++i) tot[mb][nb][i] += acc[mb][nb][i];
         }
+        acc[mb][nb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
       }
     }
-    if (kt + 1 < nsub) {
-      store_sub(cur ^ 1);
-      __syncthreads();
+  };
+
+  const int nsub = static_cast<int>(K / TT_K);  // a multiple of 4 (K is a multiple of 256)
+  if constexpr (PF == 1) {
+    load_sub(0, ra[0], rb[0]);
+    store_sub(0, ra[0], rb[0]);
+    __syncthreads();
+    for (int kt = 0; kt < nsub; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nsub) load_sub(kt + 1, ra[0], rb[0]);
+      mma_sub(cur);
+      if (kt % TT_SUB_PER_CHUNK == TT_SUB_PER_CHUNK - 1) fold(kt < TT_SUB_PER_CHUNK);
+      if (kt + 1 < nsub) {
+        store_sub(cur ^ 1, ra[0], rb[0]);
+        __syncthreads();
+      }
+    }
+  } else {
+    // One 256-wide chunk (4 sub-tiles) per outer iteration. Sub-tile t lives in register
+    // slot t % PF until it is stored to LDS buffer t & 1. The loads PF sub-tiles ahead are
+    // unconditional (indices clamped to the last sub-tile, whose repeats are stored but
+    // never read), so the loop is straight-line and each store waits only for its own
+    // slot's loads; a scheduling barrier keeps each batch of loads where it is issued.
+    load_sub(0, ra[0], rb[0]);
+    store_sub(0, ra[0], rb[0]);
+#pragma unroll
+    for (int p = 1; p <= PF; ++p) load_sub(min(p, nsub - 1), ra[p % PF], rb[p % PF]);
+    __syncthreads();
+    const int nch = nsub / TT_SUB_PER_CHUNK;
+    for (int c = 0; c < nch; ++c) {
+#pragma unroll
+      for (int j = 0; j < TT_SUB_PER_CHUNK; ++j) {
+        const int kt = c * TT_SUB_PER_CHUNK + j;
+        const int cur = j & 1;  // kt & 1
+        mma_sub(cur);
+        if (j == TT_SUB_PER_CHUNK - 1) fold(c == 0);
+        const int slot = (j + 1) % PF;  // sub-tile kt + 1 (4 c is a multiple of PF)
+        store_sub(cur ^ 1, ra[slot], rb[slot]);
+        __syncthreads();
+        load_sub(min(kt + 1 + PF, nsub - 1), ra[slot], rb[slot]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
@@ -398,12 +437,12 @@ __global__ void __launch_bounds__(WM * WN * 64) linear_tiled_kernel(
   }
 }
 
-template <int WM, int WN, int MB, int NB>
+template <int WM, int WN, int MB, int NB, int PF>
 void launch_tiled(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
                   int64_t n, int64_t k, int out_fp32, hipStream_t s) {
   constexpr int TM = WM * MB * 16, TN = WN * NB * 16;
   const dim3 grid((unsigned)((n + TN - 1) / TN), (unsigned)((m + TM - 1) / TM));
-  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB>), grid, dim3(WM * WN * 64), 0, s,
+  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB, PF>), grid, dim3(WM * WN * 64), 0, s,
                      (const bf16_t*)x, ldx, (const bf16_t*)w, (const bf16_t*)bias, y, m, n, k,
                      out_fp32);
 }
@@ -1265,9 +1304,13 @@ extern "C" int sid_linear(const void* x, int64_t ldx, const void* w, const void*
     SID_REQUIRE((m + 63) / 64 <= 65535, "linear: too many rows");
     const int64_t wide_tiles = ((m + 127) / 128) * ((n + 127) / 128);
     if (wide_tiles >= kTiledWideMinTiles) {
-      launch_tiled<4, 2, 2, 4>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
+      launch_tiled<4, 2, 2, 4, 1>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
+    } else if (((m + 127) / 128) * ((n + 63) / 64) <= stream_grid()) {
+      // At most one workgroup per CU: two sub-tiles in flight (measured, same bits: qkv
+      // M = 256 13.2 -> 11.2 us, o M = 2048 23.8 -> 18.6 us, down M = 2048 33.2 -> 24.9 us)
+      launch_tiled<4, 2, 2, 2, 2>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
     } else {
-      launch_tiled<4, 2, 2, 2>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
+      launch_tiled<4, 2, 2, 2, 1>(x, ldx, w, bias, y, m, n, k, out_fp32, s);
     }
     return check_launch("linear");
   }
