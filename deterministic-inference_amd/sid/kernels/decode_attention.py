@@ -17,7 +17,7 @@ partition, independent of the batch); nondet/dvr take the largest of 256/128/64 
 still gives 1.5 workgroups per CU for the batch's longest request, rounded up to a
 length bucket (so a HIP graph captured for a bucket computes the same plan), and
 plan_variant lengthens 256 to 512-2048 when the batch's real lengths still give two
-workgroups per CU. The stage-1 workgroup shape is picked with the plan (stage1_variant).
+workgroups per CU, 1.75 of them holding at least a quarter segment. The stage-1 workgroup shape is picked with the plan (stage1_variant).
 
 B in the policy is the number of real requests. A caller that pads its batch with empty
 requests (graph replay at a fixed size) passes the real count as ``policy_batch``, so
@@ -88,21 +88,24 @@ def nondet_geometry(batch: int, max_len: int, num_kv_heads: int, cu_count: int,
     return splits, seg, splits * max(1, _cdiv(chunk_max, seg))
 
 
-def nonempty_workgroups(lengths, splits: int, seg: int) -> int:
-    """Stage-1 workgroups of a nondet/dvr plan that hold tokens: per request of length n,
-    its min(splits, ceil(n/32)) splits of kv_per_split tokens, each cut into segments of at
-    most seg (host-side, from the requests' lengths)."""
+def nonempty_workgroups(lengths, splits: int, seg: int, min_tokens: int = 1) -> int:
+    """Stage-1 workgroups of a nondet/dvr plan that hold at least min_tokens tokens: per
+    request of length n, its min(splits, ceil(n/32)) splits of kv_per_split tokens, each cut
+    into segments of at most seg (host-side, from the requests' lengths)."""
     lens = np.asarray(lengths, dtype=np.int64)
     lens = lens[lens > 0]
     if lens.size == 0:
         return 0
+    min_tokens = max(int(min_tokens), 1)
     n = np.minimum(splits, -(-lens // 32))
     chunk = -(-(-(-lens // n)) // 32) * 32
     sl = np.minimum(seg, chunk)
     total = 0
     for s in range(int(n.max())):
-        part = np.clip(lens - s * chunk, 0, chunk)
-        total += int((-(-part // sl) * (s < n)).sum())
+        part = np.clip(lens - s * chunk, 0, chunk) * (s < n)
+        full = part // sl
+        tail = part - full * sl
+        total += int((full * (sl >= min_tokens)).sum() + (tail >= min_tokens).sum())
     return total
 
 
@@ -139,8 +142,13 @@ def stage1_variant(workgroups: int, cu_count: int, invariant: bool) -> int:
 # fewer partials, longer streams per workgroup). Measured: B = 256 x 1024 177.4 -> 166.3 us
 # (512); config-5-like lognormal B = 256 189.7 -> 177.6 us (512); B = 256 x 2048 360 -> 315
 # us (1024); B = 256 x 4096 722 -> 627 us (2048, 6.9 TB/s). Below two per CU they lose
-# (lognormal B = 128 with 512: 109 -> 146 us).
+# (lognormal B = 128 with 512: 109 -> 146 us). The workgroups must also carry work: at least
+# 1.75 per CU with a quarter segment or more. Lengths just past a multiple of the segment
+# otherwise pass with one full workgroup per CU plus a near-empty tail each (B = 256 x 1025:
+# 1024-token segments 223 us, 512-token 175 us; B = 256 x 2049: 439 -> 331 us; B = 256 x 520:
+# 119 -> 95 us), while config-5-like lognormal batches keep their plans.
 LONG_SEGMENTS = (2048, 1024, 512)
+LONG_SEGMENT_MIN_FRACTION = 4  # a workgroup carries work when it holds >= seg / 4 tokens
 
 
 def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv_splits: int,
@@ -155,7 +163,10 @@ def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv
     splits, seg, slots = geom
     if seg == SEGMENT_SIZES[0] and lens.size:
         for long_seg in LONG_SEGMENTS:
-            if nonempty_workgroups(lens, splits, long_seg) >= 2 * cu_count:
+            carrying = nonempty_workgroups(lens, splits, long_seg,
+                                           long_seg // LONG_SEGMENT_MIN_FRACTION)
+            if (nonempty_workgroups(lens, splits, long_seg) >= 2 * cu_count
+                    and 4 * carrying >= 7 * cu_count):
                 chunk_max = max(32, _cdiv(_cdiv(max_len, splits), 32) * 32)
                 seg = long_seg
                 geom = (splits, seg, splits * max(1, _cdiv(chunk_max, seg)))

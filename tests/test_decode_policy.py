@@ -141,8 +141,8 @@ def test_stage1_variant_rule():
 
 def test_long_segments_only_with_two_workgroups_per_cu():
     """plan_variant takes the longest of 2048/1024/512-token segments that still gives every CU
-    two non-empty workgroups (counted over the batch's real lengths), and keeps the
-    size-based rule otherwise."""
+    two non-empty workgroups (counted over the batch's real lengths), 1.75 of them holding a
+    quarter segment or more, and keeps the size-based rule otherwise."""
     import numpy as np
 
     from sid.kernels.decode_attention import plan_variant
@@ -162,6 +162,36 @@ def test_long_segments_only_with_two_workgroups_per_cu():
     geom, _ = plan_variant([1024] * 255 + [1], 1024, 8, cu, 32, invariant=False)
     assert geom[1] == 256                                      # 511 workgroups
     assert plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=True) == (None, 2)
+    # Lengths just past a segment multiple: 1024 + 1 tokens give 512 non-empty 1024-token
+    # workgroups, but only 256 of them carry work (the others hold one token each).
+    geom, _ = plan_variant([1025] * 256, 1025, 8, cu, 32, invariant=False)
+    assert geom[1] == 512 and geom[2] == 3
+    geom, _ = plan_variant([2049] * 256, 2049, 8, cu, 32, invariant=False)
+    assert geom[1] == 1024
+    geom, _ = plan_variant([520] * 256, 520, 8, cu, 32, invariant=False)
+    assert geom[1] == 256
+
+
+def test_workgroup_counts_match_the_partition():
+    """nonempty_workgroups(..., min_tokens) == the number of slots of segment_tokens (the
+    kernel's partition, itself checked against a walk of the splits) holding at least
+    min_tokens tokens."""
+    import numpy as np
+
+    from sid.kernels.decode_attention import nonempty_workgroups, segment_tokens
+    rng = np.random.default_rng(3)
+    for _ in range(300):
+        b = int(rng.integers(1, 80))
+        lens = rng.integers(0, 5000, b)
+        splits = int(rng.integers(1, 33))
+        seg = int(rng.choice([64, 128, 256, 512, 1024, 2048]))
+        mx = max(int(lens.max()), 1)
+        chunk_max = max(32, -(-(-(-mx // splits)) // 32) * 32)
+        slots = splits * max(1, -(-chunk_max // seg))
+        tok = segment_tokens(lens, b, splits, 0, seg, slots)
+        for min_tokens in (1, seg // 4, seg // 2, seg):
+            assert nonempty_workgroups(lens, splits, seg, min_tokens) == int(
+                (tok >= max(min_tokens, 1)).sum())
 
 
 def _walk_tokens(n, splits, fixed, seg):
