@@ -140,36 +140,53 @@ def test_stage1_variant_rule():
 
 
 def test_long_segments_only_with_two_workgroups_per_cu():
-    """plan_variant takes the longest of 2048/1024/512-token segments that still gives every CU
-    two non-empty workgroups (counted over the batch's real lengths), 1.75 of them holding a
-    quarter segment or more, and keeps the size-based rule otherwise."""
+    """For multi-split grids (fewer than 64 requests), plan_variant takes the longest of
+    2048/1024/512-token segments that still gives every CU two non-empty workgroups (counted
+    over the batch's real lengths), 1.75 of them holding a quarter segment or more, and
+    keeps the size-based rule otherwise."""
+    from sid.kernels.decode_attention import heuristic_splits, plan_variant
+    cu = 256
+    assert heuristic_splits(32, 8, cu, 32) == 2
+    geom, _ = plan_variant([16384] * 32, 16384, 8, cu, 32, invariant=False)
+    assert geom[:2] == (2, 1024)          # 32 x 2 splits x 8 segments = 512 workgroups
+    geom, _ = plan_variant([8192] * 32, 8192, 8, cu, 32, invariant=False)
+    assert geom[:2] == (2, 512)
+    geom, _ = plan_variant([8192] * 31 + [100], 8192, 8, cu, 32, invariant=False)
+    assert geom[1] == 256                 # 497 workgroups of 512 tokens
+    assert plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=True) == (None, 2)
+
+
+def test_wide_plans_for_single_split_batches():
+    """From 64 requests up (one split each) plan_variant takes the wide-workgroup plan: the
+    longest segment with >= 0.6 half-full workgroups per CU, a longest workgroup of at most
+    1/170 of the batch's tokens and (once every CU has one) balanced CUs; 8 x 2 below two
+    workgroups per CU, 4 x 1 from two; segments of 512+ at about one per CU halved into 4 x 1
+    when the halves fill every CU twice."""
     import numpy as np
 
-    from sid.kernels.decode_attention import plan_variant
+    from sid.kernels.decode_attention import _wide_plan, plan_variant
     cu = 256
-    geom, _ = plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=False)
-    assert geom[1] == 512 and geom[2] == 2                     # 512 workgroups = 2 per CU
-    geom, _ = plan_variant([4096] * 256, 4096, 8, cu, 32, invariant=False)
-    assert geom[1] == 2048 and geom[2] == 2                    # the longest that keeps 2 per CU
-    geom, _ = plan_variant([2048] * 256, 2048, 8, cu, 32, invariant=False)
-    assert geom[1] == 1024
-    geom, _ = plan_variant([2049] * 64, 2049, 8, cu, 32, invariant=False)
-    assert geom[1] == 256                                      # config 3: 320 < 512
-    rng = np.random.default_rng(5)
-    lens = (np.minimum(rng.lognormal(np.log(512), 0.8, 128).astype(int), 8192) + 200).tolist()
-    geom, _ = plan_variant(lens, max(lens), 8, cu, 32, invariant=False)
-    assert geom[1] == 256                                      # ragged B = 128: too few
-    geom, _ = plan_variant([1024] * 255 + [1], 1024, 8, cu, 32, invariant=False)
-    assert geom[1] == 256                                      # 511 workgroups
-    assert plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=True) == (None, 2)
-    # Lengths just past a segment multiple: 1024 + 1 tokens give 512 non-empty 1024-token
-    # workgroups, but only 256 of them carry work (the others hold one token each).
-    geom, _ = plan_variant([1025] * 256, 1025, 8, cu, 32, invariant=False)
-    assert geom[1] == 512 and geom[2] == 3
-    geom, _ = plan_variant([2049] * 256, 2049, 8, cu, 32, invariant=False)
-    assert geom[1] == 1024
-    geom, _ = plan_variant([520] * 256, 520, 8, cu, 32, invariant=False)
-    assert geom[1] == 256
+
+    def plan(lens):
+        geom, variant = plan_variant(lens, max(lens), 8, cu, 32, invariant=False)
+        assert geom[0] == 1 and geom[2] == -(-(-(-max(lens) // 32) * 32) // geom[1])
+        return geom[1], variant
+
+    assert plan([2049] * 64) == (256, 1)      # config 3: 512-token halves into 256 x 4 x 1
+    assert plan([1025] * 256) == (2048, 2)    # one 8 x 2 workgroup per request
+    assert plan([520] * 256) == (1024, 2)
+    assert plan([2049] * 96) == (1024, 2)     # 192 full 1024-token workgroups
+    assert plan([2049] * 128) == (512, 1)     # 256 x 1024 -> 512 x 512 of 4 x 1
+    assert plan([2049] * 256) == (1024, 1)
+    assert plan([4097] * 192) == (1024, 1)    # 2048: 384 workgroups leave CUs uneven
+    # Too little work for 0.6 half-full workgroups per CU at any size: the segment rules.
+    assert _wide_plan(np.array([100] * 64), cu) is None
+    assert plan([100] * 64) == (64, 2)
+    # A few requests far longer than the rest: their workgroups would set the time, so the
+    # segment is cut until the longest holds <= 1/170 of the tokens.
+    lens = [300] * 200 + [8192] * 4
+    seg, _ = plan(lens)
+    assert seg * 170 <= sum(lens) < 1024 * 170 and seg < 1024
 
 
 def test_workgroup_counts_match_the_partition():

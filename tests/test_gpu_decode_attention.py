@@ -125,12 +125,14 @@ def test_planned_decode_vs_oracle(invariant, lens):
     assert_close_bf16(out, decode_attention_ref(q, k, v, indptr, idx, SCALE))
 
 
-@pytest.mark.parametrize("lens", [[1024] * 256, [2048] * 256, [8192] * 64,
+@pytest.mark.parametrize("lens", [[1024] * 256, [2048] * 256, [8192] * 64, [1025] * 256,
+                                  [2049] * 96, [8192] * 32,
                                   [int(x) for x in (np.minimum(np.random.default_rng(3).lognormal(
                                       np.log(700), 0.8, 256), 8192) + 1).astype(int)]],
-                         ids=["b256x1024", "b256x2048", "b64x8192", "b256_lognormal"])
-def test_long_segment_plans_vs_oracle(lens):
-    """plan_variant's long segments (512/1024/2048 tokens for large batches) with the
+                         ids=["b256x1024", "b256x2048", "b64x8192", "b256x1025", "b96x2049",
+                              "b32x8192", "b256_lognormal"])
+def test_large_batch_plans_vs_oracle(lens):
+    """plan_variant's plans for large batches (wide 8 x 2 workgroups, long segments) with the
     workgroup shape it picks, run through DecodeAttention.forward, against the oracle."""
     from sid.kernels.decode_attention import DecodeAttention, plan_variant
     q, k, v, indptr, idx = decode_inputs(lens, seed=8)
