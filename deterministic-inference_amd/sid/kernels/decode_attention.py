@@ -15,9 +15,12 @@ MI355X addition: the kernel's workgroup reads all KV heads of a token range (who
 one workgroup each. batch_invariant uses seg = 256 = the split size (the reference's
 partition, independent of the batch); nondet/dvr take the largest of 256/128/64 that
 still gives 1.5 workgroups per CU for the batch's longest request, rounded up to a
-length bucket (so a HIP graph captured for a bucket computes the same plan), and
-plan_variant lengthens 256 to 512-2048 when the batch's real lengths still give two
-workgroups per CU, 1.75 of them holding at least a quarter segment. The stage-1 workgroup shape is picked with the plan (stage1_variant).
+length bucket (so a HIP graph captured for a bucket computes the same plan). From the
+batch's real lengths, plan_variant gives single-split grids (64 requests and more) wide
+8 x 2 workgroups of up to 2048 tokens when there is work for them (_wide_plan), and
+otherwise lengthens 256 to 512-2048 when the lengths still give two workgroups per CU,
+1.75 of them holding at least a quarter segment. The stage-1 workgroup shape is picked with
+the plan.
 
 B in the policy is the number of real requests. A caller that pads its batch with empty
 requests (graph replay at a fixed size) passes the real count as ``policy_batch``, so
