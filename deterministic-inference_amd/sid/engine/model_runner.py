@@ -149,8 +149,9 @@ class ModelRunner:
             gather_prev_tokens(static, prev_rows, prev_tokens)
         # The attention grid depends on the longest request (fixed-256 splits, or the
         # segment count of the heuristic splits): bucket it so a graph serves a range. The
-        # nondet plan follows the real request count, so it is part of the key.
-        bucket = length_bucket(fb.max_seq_len)
+        # nondet plan follows the real request count, so it is part of the key. No request
+        # is longer than max_seq_len, which also bounds the split workspace's slots.
+        bucket = min(length_bucket(fb.max_seq_len), max(self.cfg.max_seq_len, fb.max_seq_len))
         fb.max_seq_len = bucket
         plan = None
         if invariant:

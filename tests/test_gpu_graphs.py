@@ -92,3 +92,22 @@ def test_verify_graph_equals_eager():
     assert results[True][1] == results[False][1]
     for a, b in zip(results[True][0], results[False][0]):
         assert torch.equal(a, b)
+
+
+def test_decode_graph_near_max_seq_len():
+    """A request just past a length bucket near max_seq_len (8194 tokens, bucket 12288,
+    max_seq_len 9000): the graph's plan is bounded by max_seq_len, so its grid fits the
+    split workspace, and the graph replay equals the eager forward bitwise."""
+    outs = {}
+    for graphs in (False, True):
+        cfg = EngineConfig(mode=Mode.NONDET, kv_pool_tokens=9200, max_reqs=2, max_seq_len=9000,
+                           max_decode_batch=2, num_layers=2, seed=11, use_graphs=graphs)
+        runner = ModelRunner(cfg, "cuda")
+        reqs = _requests(runner, [8193])
+        fb = build_prefill_batch(reqs, runner.kv_cache, "cuda", invariant=False)
+        reqs[0].output_ids.append(int(runner.sample(fb, runner.forward(fb))[0]))
+        fb = runner.prepare_decode(reqs, False)
+        print(f"graphs={graphs} max_seq_len={fb.max_seq_len} geometry={fb.decode_geometry}",
+              flush=True)
+        outs[graphs] = runner.forward(fb).clone()
+    assert torch.equal(outs[True], outs[False])
