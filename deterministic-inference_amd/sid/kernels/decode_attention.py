@@ -18,9 +18,8 @@ still gives 1.5 workgroups per CU for the batch's longest request, rounded up to
 length bucket (so a HIP graph captured for a bucket computes the same plan). From the
 batch's real lengths, plan_variant gives single-split grids (64 requests and more) wide
 8 x 2 workgroups of up to 2048 tokens when there is work for them (_wide_plan), and
-otherwise lengthens 256 to 512-2048 when the lengths still give two workgroups per CU,
-1.75 of them holding at least a quarter segment. The stage-1 workgroup shape is picked with
-the plan.
+multi-split grids the longest of 512-64 tokens that still gives 0.75 half-full workgroups
+per CU (_multi_split_plan). The stage-1 workgroup shape is picked with the plan.
 
 B in the policy is the number of real requests. A caller that pads its batch with empty
 requests (graph replay at a fixed size) passes the real count as ``policy_batch``, so
@@ -140,20 +139,6 @@ def stage1_variant(workgroups: int, cu_count: int, invariant: bool) -> int:
     return 1
 
 
-# Long segments for large batches: the longest of LONG_SEGMENTS that still gives every CU two
-# non-empty workgroups (counted over the batch's actual lengths) beats 256 (fewer workgroups,
-# fewer partials, longer streams per workgroup). Measured: B = 256 x 1024 177.4 -> 166.3 us
-# (512); config-5-like lognormal B = 256 189.7 -> 177.6 us (512); B = 256 x 2048 360 -> 315
-# us (1024); B = 256 x 4096 722 -> 627 us (2048, 6.9 TB/s). Below two per CU they lose
-# (lognormal B = 128 with 512: 109 -> 146 us). The workgroups must also carry work: at least
-# 1.75 per CU with a quarter segment or more. Lengths just past a multiple of the segment
-# otherwise pass with one full workgroup per CU plus a near-empty tail each (B = 256 x 1025:
-# 1024-token segments 223 us, 512-token 175 us; B = 256 x 2049: 439 -> 331 us; B = 256 x 520:
-# 119 -> 95 us), while config-5-like lognormal batches keep their plans.
-LONG_SEGMENTS = (2048, 1024, 512)
-LONG_SEGMENT_MIN_FRACTION = 4  # a workgroup carries work when it holds >= seg / 4 tokens
-
-
 # Wide-workgroup plans for single-split grids (64 requests and more). An 8 x 2 workgroup
 # keeps four times the bytes of a 4 x 1 one in flight, so a few hundred of them already
 # stream at the chip's rate; then fewer, longer segments win (fewer partials, a shorter
@@ -212,31 +197,43 @@ def _wide_plan(lens: np.ndarray, cu_count: int):
     return None
 
 
+# Plans for multi-split grids (fewer than 64 requests), from the real lengths: the longest
+# of MULTI_SPLIT_SEGMENTS whose half-full workgroups number at least 0.75 per CU, with the
+# shape stage1_variant gives that count. The size-based segment counts every request as long
+# as the (bucketed) longest, so a few long requests among short ones left half the chip
+# idle: lognormal B = 32 2.53 -> 1.87 ms per step, B = 48 2.73 -> 2.25 ms. Measured on whole
+# steps (21 uniform shapes B = 1-48 x 512-8192, 8 lognormal batches, 15 fixed plans each):
+# 1.1% from the best plan of each shape on average, against 5.6% before.
+MULTI_SPLIT_SEGMENTS = (512, 256, 128, 64)
+MULTI_SPLIT_MIN_PER_CU = 0.75
+
+
+def _multi_split_plan(lens: np.ndarray, splits: int, cu_count: int):
+    for seg in MULTI_SPLIT_SEGMENTS:
+        carrying = nonempty_workgroups(lens, splits, seg, seg // 2)
+        if carrying >= MULTI_SPLIT_MIN_PER_CU * cu_count:
+            return seg, stage1_variant(carrying, cu_count, invariant=False)
+    return None
+
+
 def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv_splits: int,
                  invariant: bool) -> tuple:
     """(nondet geometry or None, stage-1 variant) for a batch of known lengths; max_len is
     the (possibly bucketed) bound the plan is built for. The geometry (grid splits, segment
-    size, grid slots) is what DecodeAttention.forward runs when given it."""
+    size, grid slots) is what DecodeAttention.forward runs when given it: the wide plan for
+    single-split grids, the multi-split plan otherwise, and the size-based segment (with the
+    shape for its non-empty workgroups) for batches too small for either."""
     if invariant:
         return None, INVARIANT_VARIANT
     lens = np.asarray(lengths, dtype=np.int64)
     geom = nondet_geometry(len(lens), max_len, num_kv_heads, cu_count, max_kv_splits)
     splits, seg, slots = geom
-    if splits == 1 and lens.size and int(lens.min()) > 0:
-        wide = _wide_plan(lens, cu_count)
-        if wide is not None:
-            chunk_max = max(32, _cdiv(max_len, 32) * 32)
-            return (1, wide[0], max(1, _cdiv(chunk_max, wide[0]))), wide[1]
-    if seg == SEGMENT_SIZES[0] and lens.size:
-        for long_seg in LONG_SEGMENTS:
-            carrying = nonempty_workgroups(lens, splits, long_seg,
-                                           long_seg // LONG_SEGMENT_MIN_FRACTION)
-            if (nonempty_workgroups(lens, splits, long_seg) >= 2 * cu_count
-                    and 4 * carrying >= 7 * cu_count):
-                chunk_max = max(32, _cdiv(_cdiv(max_len, splits), 32) * 32)
-                seg = long_seg
-                geom = (splits, seg, splits * max(1, _cdiv(chunk_max, seg)))
-                break
+    if lens.size and int(lens.min()) > 0:
+        pick = (_wide_plan(lens, cu_count) if splits == 1
+                else _multi_split_plan(lens, splits, cu_count))
+        if pick is not None:
+            chunk_max = max(32, _cdiv(_cdiv(max_len, splits), 32) * 32)
+            return (splits, pick[0], splits * max(1, _cdiv(chunk_max, pick[0]))), pick[1]
     return geom, stage1_variant(nonempty_workgroups(lens, splits, seg), cu_count, invariant=False)
 
 

@@ -139,21 +139,35 @@ def test_stage1_variant_rule():
     assert stage1_variant(511, 256, invariant=False) == 3
 
 
-def test_long_segments_only_with_two_workgroups_per_cu():
-    """For multi-split grids (fewer than 64 requests), plan_variant takes the longest of
-    2048/1024/512-token segments that still gives every CU two non-empty workgroups (counted
-    over the batch's real lengths), 1.75 of them holding a quarter segment or more, and
-    keeps the size-based rule otherwise."""
-    from sid.kernels.decode_attention import heuristic_splits, plan_variant
+def test_multi_split_plans():
+    """For multi-split grids (fewer than 64 requests) plan_variant takes the longest of
+    512/256/128/64-token segments with >= 0.75 half-full workgroups per CU, counted over the
+    batch's real lengths, and the shape stage1_variant gives that count; batches with less
+    work keep the size-based segment."""
+    import numpy as np
+
+    from sid.kernels.decode_attention import (heuristic_splits, nondet_geometry,
+                                              nonempty_workgroups, plan_variant)
     cu = 256
     assert heuristic_splits(32, 8, cu, 32) == 2
-    geom, _ = plan_variant([16384] * 32, 16384, 8, cu, 32, invariant=False)
-    assert geom[:2] == (2, 1024)          # 32 x 2 splits x 8 segments = 512 workgroups
-    geom, _ = plan_variant([8192] * 32, 8192, 8, cu, 32, invariant=False)
-    assert geom[:2] == (2, 512)
-    geom, _ = plan_variant([8192] * 31 + [100], 8192, 8, cu, 32, invariant=False)
-    assert geom[1] == 256                 # 497 workgroups of 512 tokens
-    assert plan_variant([1024] * 256, 1024, 8, cu, 32, invariant=True) == (None, 2)
+
+    def plan(lens):
+        geom, variant = plan_variant(lens, max(lens), 8, cu, 32, invariant=False)
+        return geom, variant
+
+    assert plan([8192] * 32) == ((2, 512, 16), 1)      # 32 x 2 x 8 = 512 workgroups
+    assert plan([2048] * 48) == ((2, 512, 4), 2)       # 192 full 512-token workgroups
+    assert plan([2048] * 24)[0][1] == 256              # 3 splits of 683: 216 workgroups
+    # a lognormal batch: the longest segment with 0.75 half-full workgroups per CU
+    rng = np.random.default_rng(7)
+    lens = (np.minimum(rng.lognormal(np.log(512), 0.8, 32), 8192) + 300).astype(int).tolist()
+    (splits, seg, _), variant = plan(lens)
+    assert splits == 2 and seg <= nondet_geometry(32, max(lens), 8, cu, 32)[1]
+    assert nonempty_workgroups(lens, 2, seg, seg // 2) >= 0.75 * cu
+    assert nonempty_workgroups(lens, 2, 2 * seg, seg) < 0.75 * cu
+    # one request of 1024 tokens (config 1): 32 splits of 32 tokens; the size-based plan
+    assert plan([1024]) == ((32, 64, 32), 2)
+    assert plan_variant([1024] * 4, 1024, 8, cu, 32, invariant=True) == (None, 2)
 
 
 def test_wide_plans_for_single_split_batches():

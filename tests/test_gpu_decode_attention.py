@@ -128,18 +128,20 @@ def test_planned_decode_vs_oracle(invariant, lens):
 @pytest.mark.parametrize("lens", [[1024] * 256, [2048] * 256, [8192] * 64, [1025] * 256,
                                   [2049] * 96, [8192] * 32,
                                   [int(x) for x in (np.minimum(np.random.default_rng(3).lognormal(
-                                      np.log(700), 0.8, 256), 8192) + 1).astype(int)]],
+                                      np.log(700), 0.8, 256), 8192) + 1).astype(int)],
+                                  [int(x) for x in (np.minimum(np.random.default_rng(4).lognormal(
+                                      np.log(512), 0.8, 32), 8192) + 300).astype(int)]],
                          ids=["b256x1024", "b256x2048", "b64x8192", "b256x1025", "b96x2049",
-                              "b32x8192", "b256_lognormal"])
-def test_large_batch_plans_vs_oracle(lens):
-    """plan_variant's plans for large batches (wide 8 x 2 workgroups, long segments) with the
-    workgroup shape it picks, run through DecodeAttention.forward, against the oracle."""
+                              "b32x8192", "b256_lognormal", "b32_lognormal"])
+def test_planned_geometries_vs_oracle(lens):
+    """plan_variant's plans from real lengths (wide 8 x 2 workgroups for single-split grids,
+    the multi-split plan below 64 requests) with the workgroup shape it picks, run through
+    DecodeAttention.forward, against the oracle."""
     from sid.kernels.decode_attention import DecodeAttention, plan_variant
     q, k, v, indptr, idx = decode_inputs(lens, seed=8)
     cu = torch.cuda.get_device_properties(0).multi_processor_count
     geom, variant = plan_variant(lens, max(lens), HKV, cu, 32, invariant=False)
     print(f"B={len(lens)} max={max(lens)} geometry={geom} variant={variant}", flush=True)
-    assert geom[1] >= 512
     attn = DecodeAttention(len(lens), HQ, HKV, D, 32, 256, 8192, "cuda")
     seq = torch.tensor(lens, dtype=torch.int32, device="cuda")
     out = attn.forward(q, k, v, indptr, idx, seq, max(lens), SCALE, False, variant=variant,
