@@ -82,7 +82,10 @@ def kept_mask_exact(p: np.ndarray, top_k: int, top_p: float) -> np.ndarray:
     """Keep-mask of one row under the exact rule (p: float32 probabilities)."""
     v = p.size
     order = np.lexsort((np.arange(v), -p.astype(np.float64)))  # p desc, index asc
-    q = np.floor(p.astype(np.float64)[order] * MASS_UNIT).astype(np.uint64)
+    # NaN probabilities (a +inf logit: inf - inf in the softmax) cast to unspecified
+    # masses; only the no-limit rule (every column kept) is pinned for such rows.
+    with np.errstate(invalid="ignore"):
+        q = np.floor(p.astype(np.float64)[order] * MASS_UNIT).astype(np.uint64)
     before = np.concatenate([[0], np.cumsum(q)[:-1]]).astype(np.uint64)
     keep_rank = np.ones(v, dtype=bool)
     if top_k > 0:
