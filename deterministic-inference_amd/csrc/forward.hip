@@ -28,9 +28,6 @@ bool split_for(int64_t t, int64_t n, int64_t wide_max) {
 }
 
 constexpr int64_t kAlign = 256;
-// Greedy rows up to this count take the lm_head with the fused argmax (one streaming pass
-// over the weights, no logits); more rows go through fp32 logits (tiled GEMM) + argmax.
-constexpr int64_t kFusedArgmaxMaxRows = 64;
 
 struct Carver {
   char* base;
@@ -128,9 +125,6 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
   const int64_t t = b->num_tokens;
   const int64_t r = b->sample_indices ? b->num_samples : t;
   SID_REQUIRE(r > 0, "qwen3_extend_forward: no sampled rows");
-  SID_REQUIRE(logits || r <= kFusedArgmaxMaxRows,
-              "qwen3_extend_forward: greedy over %lld rows needs a logits buffer",
-              (long long)r);
   const Layout l = plan(m, b, workspace);
   SID_REQUIRE(workspace && workspace_bytes >= l.total,
               "qwen3_extend_forward: workspace %lld bytes, need %lld",
@@ -205,11 +199,9 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
     SID_TRY(sid_gather_rows(l.x, b->sample_indices, l.rows, r, h, t, stream));
     rows = l.rows;
   }
-  if (greedy_tokens && r <= kFusedArgmaxMaxRows) {
+  if (greedy_tokens) {  // the greedy argmax fused into the lm_head (logits written if given)
     return sid_linear_argmax(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, l.argmax_ws,
                              l.argmax_ws_bytes, greedy_tokens, stream);
   }
-  SID_TRY(sid_linear(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, 1, stream));
-  if (greedy_tokens) return sid_argmax_rows(logits, m->vocab, greedy_tokens, r, m->vocab, stream);
-  return SID_OK;
+  return sid_linear(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, 1, stream);
 }

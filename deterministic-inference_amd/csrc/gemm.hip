@@ -243,6 +243,19 @@ __global__ void __launch_bounds__(NW * 64) linear_chunk_kernel(
   }
 }
 
+// Greedy argmax order over (value, column), torch's: larger value, then smaller index; NaN
+// above everything, first NaN wins. A total order, so a maximum over any split of the
+// columns into candidates, reduced in any order, is the same (value, column).
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v;
+  const bool bn = bv != bv;
+  if (vn || bn) {
+    if (vn && bn) return i < bi;
+    return vn;
+  }
+  return v > bv || (v == bv && i < bi);
+}
+
 // ---- large-M tiled GEMM (prefill) ---------------------------------------------------------
 //
 // 128 x 128 output tile per 4-wave workgroup (wave (wm, wn): 64 x 64 = 4 x 4 MFMA blocks),
@@ -267,11 +280,16 @@ constexpr int TT_SUB_PER_CHUNK = KC / TT_K;
 // are the bound). PF = 2: a ring of two register buffers keeps two sub-tiles in flight,
 // issued at fixed points (best for grids of at most one workgroup per CU, where every
 // sub-tile's global-memory latency would otherwise be exposed). Same arithmetic either way.
-template <int WM, int WN, int MB, int NB, int PF>
-__global__ void __launch_bounds__(WM * WN * 64) linear_tiled_kernel(
+//
+// AM (greedy lm_head): the epilogue also keeps each row's best (bf16-rounded logit, column)
+// over the tile's columns, in argmax_better's order, and writes it to
+// best_val / best_idx [blockIdx.x][M] for argmax_finalize_kernel; y may then be null (no
+// logits written).
+template <int WM, int WN, int MB, int NB, int PF, bool AM = false>
+__global__ void __launch_bounds__(WM * WN * 64, AM ? 4 : 1) linear_tiled_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ bias, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
-    int out_fp32) {
+    int out_fp32, float* __restrict__ best_val, int* __restrict__ best_idx) {
   constexpr int TM = WM * MB * 16;
   constexpr int TN = WN * NB * 16;
   constexpr int THREADS = WM * WN * 64;
@@ -414,37 +432,102 @@ __global__ void __launch_bounds__(WM * WN * 64) linear_tiled_kernel(
   }
 
   // Lane holds rows 16*mb + 4*g + i, column 16*nb + r of the wave's block.
+  if constexpr (!AM) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int64_t col = n0 + NB * 16 * wn + 16 * nb + r;
-    if (col >= N) continue;
-    const float bv = bias != nullptr ? bf16_to_f32(bias[col]) : 0.0f;
+    for (int nb = 0; nb < NB; ++nb) {
+      const int64_t col = n0 + NB * 16 * wn + 16 * nb + r;
+      if (col >= N) continue;
+      const float bv = bias != nullptr ? bf16_to_f32(bias[col]) : 0.0f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t row = m0 + MB * 16 * wm + 16 * mb + 4 * g + i;
+          if (row >= M) continue;
+          float v = tot[mb][nb][i];
+          if (bias != nullptr) v += bv;
+          if (out_fp32) {
+            static_cast<float*>(y)[row * N + col] = round_bf16(v);
+          } else {
+            static_cast<bf16_t*>(y)[row * N + col] = f32_to_bf16(v);
+          }
+        }
+      }
+    }
+  } else {
+    // Greedy epilogue, one row block at a time (few live registers: the kernel keeps its
+    // occupancy): each lane's best over its columns (logits written as fp32 when y is
+    // given), then over the 16 column lanes of each row, then over the WN waves of a row
+    // band through LDS (the x tile buffer, free once every wave is past its last MFMA).
+    float* s_v = reinterpret_cast<float*>(&sa[0][0]);
+    int* s_i = reinterpret_cast<int*>(s_v + WN * TM);
+    static_assert(2 * WN * TM * 4 <= TM * TT_KS * 2, "argmax scratch exceeds the x tile");
+    __syncthreads();
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t row = m0 + MB * 16 * wm + 16 * mb + 4 * g + i;
-        if (row >= M) continue;
-        float v = tot[mb][nb][i];
-        if (bias != nullptr) v += bv;
-        if (out_fp32) {
-          static_cast<float*>(y)[row * N + col] = round_bf16(v);
-        } else {
-          static_cast<bf16_t*>(y)[row * N + col] = f32_to_bf16(v);
+        float v = -INFINITY;
+        int ix = 0x7fffffff;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int64_t col = n0 + NB * 16 * wn + 16 * nb + r;
+          if (col >= N || row >= M) continue;
+          float t = tot[mb][nb][i];
+          if (bias != nullptr) t += bf16_to_f32(bias[col]);
+          const float vr = round_bf16(t);
+          if (y != nullptr) static_cast<float*>(y)[row * N + col] = vr;
+          if (argmax_better(vr, static_cast<int>(col), v, ix)) {
+            v = vr;
+            ix = static_cast<int>(col);
+          }
         }
+#pragma unroll
+        for (int mask = 1; mask < 16; mask <<= 1) {
+          const float ov = lane_xor(v, mask);
+          const int oi = __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, ix);
+          if (argmax_better(ov, oi, v, ix)) {
+            v = ov;
+            ix = oi;
+          }
+        }
+        if (r == 0) {
+          const int lr = MB * 16 * wm + 16 * mb + 4 * g + i;
+          s_v[wn * TM + lr] = v;
+          s_i[wn * TM + lr] = ix;
+        }
+      }
+    }
+    __syncthreads();
+    for (int lr = tid; lr < TM; lr += THREADS) {
+      float v = s_v[lr];
+      int ix = s_i[lr];
+#pragma unroll
+      for (int q = 1; q < WN; ++q) {
+        if (argmax_better(s_v[q * TM + lr], s_i[q * TM + lr], v, ix)) {
+          v = s_v[q * TM + lr];
+          ix = s_i[q * TM + lr];
+        }
+      }
+      const int64_t row = m0 + lr;
+      if (row < M) {
+        best_val[static_cast<int64_t>(blockIdx.x) * M + row] = v;
+        best_idx[static_cast<int64_t>(blockIdx.x) * M + row] = ix;
       }
     }
   }
 }
 
-template <int WM, int WN, int MB, int NB, int PF>
+template <int WM, int WN, int MB, int NB, int PF, bool AM = false>
 void launch_tiled(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
-                  int64_t n, int64_t k, int out_fp32, hipStream_t s) {
+                  int64_t n, int64_t k, int out_fp32, hipStream_t s, float* best_val = nullptr,
+                  int* best_idx = nullptr) {
   constexpr int TM = WM * MB * 16, TN = WN * NB * 16;
   const dim3 grid((unsigned)((n + TN - 1) / TN), (unsigned)((m + TM - 1) / TM));
-  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB, PF>), grid, dim3(WM * WN * 64), 0, s,
+  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB, PF, AM>), grid, dim3(WM * WN * 64), 0, s,
                      (const bf16_t*)x, ldx, (const bf16_t*)w, (const bf16_t*)bias, y, m, n, k,
-                     out_fp32);
+                     out_fp32, best_val, best_idx);
 }
 
 // sid_linear takes the tiled kernel from this many rows up: 8 waves (4 x 2), each 32 x 64
@@ -475,16 +558,6 @@ constexpr int WXS = WIDE_K + 8;
 // (torch's: larger value, then smaller index; NaN above everything, first NaN wins), so
 // the result does not depend on how the columns are split.
 constexpr int STREAM_WAVES = 8;
-
-__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
-  const bool vn = v != v;
-  const bool bn = bv != bv;
-  if (vn || bn) {
-    if (vn && bn) return i < bi;
-    return vn;
-  }
-  return v > bv || (v == bv && i < bi);
-}
 
 template <int MBS, bool ARGMAX>
 __global__ void __launch_bounds__(STREAM_WAVES * 64) linear_stream_kernel(
@@ -1343,9 +1416,21 @@ extern "C" int sid_linear_partials(const void* x, int64_t ldx, const void* w, fl
   return check_launch("linear_partials");
 }
 
+// sid_linear_argmax: up to one 64-row group streams the weights once (linear_stream_kernel,
+// one candidate per wave); more rows take the tiled GEMM with the argmax epilogue (one
+// candidate per 128-column tile, no logits needed: verify pass, 128 rows x 151936,
+// 101 us GEMM + 32 us argmax_rows before). Both reduce with argmax_finalize_kernel. The
+// workspace holds stream_grid() * STREAM_WAVES candidates per row, which bounds the tiled
+// path's column tiles.
+static bool argmax_streams(int64_t m, int64_t n, int64_t k) {
+  return m <= MROWS && stream_shape_ok(m, n, k);
+}
+
+static int64_t argmax_candidates() { return static_cast<int64_t>(stream_grid()) * STREAM_WAVES; }
+
 extern "C" int64_t sid_linear_argmax_workspace_bytes(int64_t m) {
-  if (m < 1 || m > kStreamMaxM) return 0;
-  return static_cast<int64_t>(stream_grid()) * STREAM_WAVES * m * (sizeof(float) + sizeof(int));
+  if (m < 1 || (m + MROWS - 1) / MROWS > 65535) return 0;
+  return argmax_candidates() * m * static_cast<int64_t>(sizeof(float) + sizeof(int));
 }
 
 extern "C" int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bias,
@@ -1357,23 +1442,31 @@ extern "C" int sid_linear_argmax(const void* x, int64_t ldx, const void* w, cons
   SID_REQUIRE(out_idx != nullptr && workspace != nullptr, "linear_argmax: null pointer");
   int rc = check_shapes(x, ldx, w, m, n, k, "linear_argmax");
   if (rc != SID_OK) return rc;
-  SID_REQUIRE(stream_shape_ok(m, n, k),
-              "linear_argmax: needs 1 <= M <= %d and K == %d (got M=%lld, K=%lld)", (int)kStreamMaxM, WIDE_K,
-              (long long)m, (long long)k);
   const int64_t need = sid_linear_argmax_workspace_bytes(m);
-  SID_REQUIRE(workspace_bytes >= need, "linear_argmax: workspace %lld bytes, need %lld",
+  SID_REQUIRE(need > 0 && workspace_bytes >= need, "linear_argmax: workspace %lld bytes, need %lld",
               (long long)workspace_bytes, (long long)need);
   SID_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
               "linear_argmax: workspace must be 16-byte aligned");
-  const int waves = stream_grid() * STREAM_WAVES;
+  const int64_t cands = argmax_candidates();
   float* bv = static_cast<float*>(workspace);
-  int* bi = reinterpret_cast<int*>(bv + static_cast<int64_t>(waves) * m);
+  int* bi = reinterpret_cast<int*>(bv + cands * m);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  launch_stream<true>(x, ldx, w, bias, logits, static_cast<int>(m), static_cast<int>(n), 1, bv, bi,
-                      s);
+  int used;
+  if (argmax_streams(m, n, k)) {
+    launch_stream<true>(x, ldx, w, bias, logits, static_cast<int>(m), static_cast<int>(n), 1, bv,
+                        bi, s);
+    used = static_cast<int>(cands);
+  } else {
+    const int64_t tiles = (n + 127) / 128;
+    SID_REQUIRE(tiles <= cands, "linear_argmax: N=%lld has more than %lld column tiles",
+                (long long)n, (long long)cands);
+    SID_REQUIRE((m + 127) / 128 <= 65535, "linear_argmax: too many rows");
+    launch_tiled<4, 2, 2, 4, 1, true>(x, ldx, w, bias, logits, m, n, k, 1, s, bv, bi);
+    used = static_cast<int>(tiles);
+  }
   rc = check_launch("linear_argmax");
   if (rc != SID_OK) return rc;
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(256), 0, s, bv, bi, waves,
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)m), dim3(256), 0, s, bv, bi, used,
                      static_cast<int>(m), out_idx);
   return check_launch("linear_argmax finalize");
 }

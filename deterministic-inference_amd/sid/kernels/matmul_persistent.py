@@ -84,14 +84,10 @@ def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 
 
 def linear_argmax_supported(m: int, k: int) -> bool:
-    """Shapes the fused lm_head + greedy argmax kernel takes (M <= 256, K = 1024)."""
-    return 1 <= m <= 256 and k == 1024
-
-
-def linear_argmax_preferred(m: int, k: int) -> bool:
-    """Where the fused kernel is the faster choice: one 64-row group (it streams the weights
-    once per group; more rows go through the tiled GEMM's logits + argmax_rows)."""
-    return 1 <= m <= 64 and k == 1024
+    """Shapes the fused lm_head + greedy argmax takes: any row count (up to 64 rows one
+    streaming pass over the weights, more rows the tiled GEMM with the argmax in its
+    epilogue; neither writes logits unless asked), K a multiple of 256."""
+    return m >= 1 and k > 0 and k % 256 == 0
 
 
 def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,

@@ -16,7 +16,6 @@ from sid.kernels.jit import load_ext
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 
-FUSED_ARGMAX_MAX_ROWS = 64  # csrc/forward.hip kFusedArgmaxMaxRows
 
 
 class Layer(ctypes.Structure):
@@ -94,9 +93,7 @@ class NativeQwen3:
         logits: Optional[torch.Tensor] = None
         tokens: Optional[torch.Tensor] = None
         if greedy:
-            tokens = torch.empty(r, dtype=torch.int64, device=dev)
-            if r > FUSED_ARGMAX_MAX_ROWS:  # the library needs a logits buffer past that
-                logits = torch.empty(r, self.vocab, dtype=torch.float32, device=dev)
+            tokens = torch.empty(r, dtype=torch.int64, device=dev)  # no logits written
         else:
             logits = torch.empty(r, self.vocab, dtype=torch.float32, device=dev)
         rc = lib.sid_qwen3_extend_forward(

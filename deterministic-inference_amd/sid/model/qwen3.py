@@ -15,7 +15,7 @@ import torch
 from sid.config import ModelConfig, decode_backend_kind
 from sid.engine.batch import ForwardBatch, ForwardMode
 from sid.kernels.extend_attention import extend_attention_fwd
-from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_preferred,
+from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_supported,
                                             linear_partials, linear_sample, linear_silu_mul,
                                             linear_silu_mul_preferred)
 from sid.kernels.ops import (argmax_rows, embedding, fused_add_rmsnorm_partials, gather_rows, qkv_post,
@@ -141,7 +141,7 @@ class Qwen3Model:
             return linear_sample(rows, self.w["lm_head"], fb.temperatures[:r], fb.seeds[:r],
                                  fb.sample_positions[:r])
         if greedy:
-            if linear_argmax_preferred(rows.shape[0], rows.shape[1]):
+            if linear_argmax_supported(rows.shape[0], rows.shape[1]):
                 return linear_argmax(rows, self.w["lm_head"])
             return argmax_rows(linear(rows, self.w["lm_head"], out_fp32=True))
         return linear(rows, self.w["lm_head"], out_fp32=True)

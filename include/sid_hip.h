@@ -304,8 +304,11 @@ int sid_sample_rows(const float* logits, int64_t ld, const float* temperatures,
  * and compared with sid_argmax_rows's order. Fuses the lm_head projection
  * (sid/model/qwen3.py:114-115) with the greedy branch of sample()
  * (sid/engine/sampler.py:38) for an all-greedy batch. logits may be NULL (not
- * written) or fp32 [M, N]. Needs 1 <= M <= 256, K == 1024; workspace of
- * sid_linear_argmax_workspace_bytes(M) bytes, 16-byte aligned.
+ * written) or fp32 [M, N]. Any M >= 1; K a multiple of 256. Up to 64 rows with
+ * K == 1024 stream the weights once; otherwise the tiled GEMM keeps one
+ * candidate per 128-column tile, so N <= 128 x 8 x (CU count) (1,048,576 on
+ * MI355X). Workspace of sid_linear_argmax_workspace_bytes(M) bytes, 16-byte
+ * aligned.
  */
 int64_t sid_linear_argmax_workspace_bytes(int64_t m);
 int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bias, float* logits,
@@ -324,7 +327,7 @@ int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bia
  * 4 * split_k_max_tokens tokens, N <= 4096 up to split_k_max_tokens, wider ones
  * below split_k_max_tokens (the results are the same either way). Outputs:
  * logits fp32 [R, vocab] and/or greedy_tokens int64 [R] (R = num_samples, or
- * num_tokens without sample_indices; greedy without logits needs R <= 64).
+ * num_tokens without sample_indices).
  */
 typedef struct {
   const void* input_ln;

@@ -100,17 +100,20 @@ def test_stream_lm_head_path_bitwise_matches_tiled(m):
     torch.testing.assert_close(full[:, :2048].cpu(), ref, atol=3e-2, rtol=2e-2)
 
 
-@pytest.mark.parametrize("m,n", [(1, 151936), (7, 151936), (33, 65536), (64, 151936), (64, 4096),
-                                 (128, 151936), (200, 65536)])
-def test_linear_argmax_matches_linear_then_argmax(m, n):
+@pytest.mark.parametrize("m,n,k", [(1, 151936, 1024), (7, 151936, 1024), (33, 65536, 1024),
+                                   (64, 151936, 1024), (64, 4096, 1024), (65, 151936, 1024),
+                                   (128, 151936, 1024), (200, 65536, 1024), (300, 151936, 1024),
+                                   (512, 151936, 1024), (100, 1088, 512), (3, 4096, 2048)])
+def test_linear_argmax_matches_linear_then_argmax(m, n, k):
     """Fused lm_head + greedy argmax == argmax_rows(linear(..., out_fp32=True)), and the
-    optional logits output equals linear's."""
+    optional logits output equals linear's: the streaming path (up to 64 rows, K = 1024)
+    and the tiled GEMM's argmax epilogue (more rows, other K, a ragged last column tile)."""
     from sid.kernels.matmul_persistent import linear, linear_argmax
     from sid.kernels.ops import argmax_rows
     torch.manual_seed(7 + m)
-    print(f"m={m} n={n}", flush=True)
-    x = torch.randn(m, 1024, device="cuda", dtype=torch.bfloat16)
-    w = (torch.randn(n, 1024, device="cuda") * 0.05).to(torch.bfloat16)
+    print(f"m={m} n={n} k={k}", flush=True)
+    x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(n, k, device="cuda") * 0.05).to(torch.bfloat16)
     logits = linear(x, w, out_fp32=True)
     want = argmax_rows(logits)
     assert torch.equal(linear_argmax(x, w), want)
@@ -119,13 +122,15 @@ def test_linear_argmax_matches_linear_then_argmax(m, n):
     assert torch.equal(lg, logits)
 
 
-def test_linear_argmax_ties_and_nan():
+@pytest.mark.parametrize("m", [4, 130])
+def test_linear_argmax_ties_and_nan(m):
     """Equal maxima -> first column; a NaN logit wins over every number, first NaN first
-    (torch.argmax semantics), also when the tied columns land in different waves."""
+    (torch.argmax semantics), also when the tied columns land in different waves (streaming
+    path) or column tiles (tiled path)."""
     from sid.kernels.matmul_persistent import linear_argmax
     torch.manual_seed(8)
     n = 151936
-    x = torch.randn(4, 1024, device="cuda", dtype=torch.bfloat16)
+    x = torch.randn(m, 1024, device="cuda", dtype=torch.bfloat16)
     w = (torch.randn(n, 1024, device="cuda") * 0.01).to(torch.bfloat16)
     hot = (x[0].float() / x[0].float().norm()).to(torch.bfloat16)
     for c in (150000, 70001, 70000, 123):   # identical rows: identical logits for every x
