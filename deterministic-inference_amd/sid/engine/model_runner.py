@@ -82,50 +82,67 @@ class ModelRunner:
             "kv_indices": z(g * (cfg.max_seq_len + cfg.dvr_window_size), torch.int32),
         }
 
-    def forward(self, fb: ForwardBatch, greedy: bool = False,
-                sample: bool = False) -> torch.Tensor:
+    def forward(self, fb: ForwardBatch, greedy: bool = False, sample: bool = False,
+                with_logits: bool = False):
         """Logits of the sampled rows, or (greedy=True) their greedy tokens, or (sample=True,
-        decode batches without top-k / top-p limits) their sampled tokens; rows of batch
-        padding are dropped."""
+        decode batches) the tokens the lm_head-fused sampler draws, with with_logits=True
+        together with the logits as (logits, tokens); rows of batch padding are dropped."""
         if self.graphs is not None and fb.graph_key is not None:
-            out = self.graphs.run(fb, greedy, sample)
+            out = self.graphs.run(fb, greedy, sample, with_logits)
         else:
-            out = self._forward_eager(fb, greedy, sample)
-        return out if fb.real_rows is None else out[:fb.real_rows]
+            out = self._forward_eager(fb, greedy, sample, with_logits)
+        if fb.real_rows is None:
+            return out
+        if isinstance(out, tuple):
+            return tuple(o[:fb.real_rows] for o in out)
+        return out[:fb.real_rows]
 
-    def _forward_eager(self, fb: ForwardBatch, greedy: bool = False,
-                       sample: bool = False) -> torch.Tensor:
+    def _forward_eager(self, fb: ForwardBatch, greedy: bool = False, sample: bool = False,
+                       with_logits: bool = False):
         fb.build_indices()
         return self.model.forward(fb, self.kv_cache, self.decode_attn,
                                   decode_backend=self.cfg.decode_backend, greedy=greedy,
-                                  sample=sample)
+                                  sample=sample, with_logits=with_logits)
+
+    def _invariant_fused(self) -> bool:
+        """batch_invariant mode's one choice per engine (never per batch) for its rows
+        without top-k / top-p limits: the lm_head-fused sampler when every decode batch fits
+        it (max_decode_batch <= 256). The fused sampler and the sampler kernel agree except at
+        float near-ties of the scores (their softmax sums run in different orders), so a
+        row's path must follow from the row alone."""
+        return linear_sample_supported(self.cfg.max_decode_batch, self.mcfg.hidden_size)
 
     def fused_sample(self, fb: ForwardBatch) -> bool:
         """Whether a decode batch without top-k / top-p limits draws its tokens inside the
-        lm_head (sid_linear_sample) instead of writing logits for the sampler kernel. The
-        two agree except at float near-ties of the scores (their softmax sums run in
-        different orders), so in batch_invariant mode the choice is one per engine, never
-        per batch: fused when every decode batch fits it (max_decode_batch <= 256). Elsewhere
-        by speed: fused up to 128 rows (it streams the weights once per 64 rows; measured at
-        T = 0.7: 1 row 74 vs 178 us, 64: 114 vs 205, 128: 205 vs 231, 256: 393 vs 329); dvr
-        commits only the verifier's tokens, so its decode rows may take either path."""
+        lm_head (sid_linear_sample) instead of writing logits for the sampler kernel.
+        batch_invariant: the engine's choice (_invariant_fused). Elsewhere by speed: fused up
+        to 128 rows (it streams the weights once per 64 rows; measured at T = 0.7: 1 row 74
+        vs 178 us, 64: 114 vs 205, 128: 205 vs 231, 256: 393 vs 329); dvr commits only the
+        verifier's tokens, so its decode rows may take either path."""
         if fb.mode != ForwardMode.DECODE or not fb.untruncated:
             return False
-        k = self.mcfg.hidden_size
         if fb.invariant:
-            return linear_sample_supported(self.cfg.max_decode_batch, k)
+            return self._invariant_fused()
         rows = fb.input_ids.shape[0]
-        return linear_sample_supported(rows, k) and rows <= 128
+        return linear_sample_supported(rows, self.mcfg.hidden_size) and rows <= 128
 
     def step(self, fb: ForwardBatch) -> torch.Tensor:
         """forward + sample -> int64 tokens [R]. An all-greedy batch takes the fused
         lm_head + argmax path, a decode batch the fused lm_head + sampler where
         fused_sample says so (no logits written); the rest writes the logits and runs the
-        sampler kernel over them."""
+        sampler kernel over them. A batch_invariant decode batch that mixes rows with and
+        without top-k / top-p limits, on an engine whose choice is the fused sampler, gets
+        both: the fused sampler's tokens for the rows without limits (as in any other batch),
+        the sampler kernel's for the others."""
         if fb.all_greedy:
             return self.forward(fb, greedy=True)
         if self.fused_sample(fb):
             return self.forward(fb, sample=True)
+        if fb.mode == ForwardMode.DECODE and fb.invariant and self._invariant_fused():
+            logits, fused = self.forward(fb, sample=True, with_logits=True)
+            r = logits.shape[0]
+            free = (fb.top_ks[:r] <= 0) & (fb.top_ps[:r] >= 1.0)
+            return torch.where(free, fused, self.sample(fb, logits))
         return self.sample(fb, self.forward(fb))
 
     def prepare_decode(self, reqs: list, invariant: bool, prev_rows=None,
@@ -239,11 +256,12 @@ class GraphCache:
                                           cfg.max_decode_batch * cfg.max_seq_len, runner.device,
                                           max_slots=runner.decode_attn.ws_splits)
 
-    def run(self, fb: ForwardBatch, greedy: bool = False, sample: bool = False) -> torch.Tensor:
-        key = (fb.graph_key, greedy, sample)
+    def run(self, fb: ForwardBatch, greedy: bool = False, sample: bool = False,
+            with_logits: bool = False):
+        key = (fb.graph_key, greedy, sample, with_logits)
         entry = self.graphs.get(key)
         if entry is None:
-            entry = self._capture(fb, greedy, sample)
+            entry = self._capture(fb, greedy, sample, with_logits)
             self.graphs[key] = entry
             while len(self.graphs) > self.max_graphs:
                 self.graphs.popitem(last=False)
@@ -253,7 +271,7 @@ class GraphCache:
         graph.replay()
         return out
 
-    def _capture(self, fb: ForwardBatch, greedy: bool, sample: bool):
+    def _capture(self, fb: ForwardBatch, greedy: bool, sample: bool, with_logits: bool = False):
         runner = self._runner()
         kind = fb.graph_key[0]
         if kind not in self._warm:
@@ -261,7 +279,7 @@ class GraphCache:
             # (library load, descriptors, torch's first-use work) happens outside a capture;
             # it computes exactly what the replay recomputes. Later captures of the kind run
             # the same host code and skip it.
-            runner._forward_eager(fb, greedy, sample)
+            runner._forward_eager(fb, greedy, sample, with_logits)
             self._warm.add(kind)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
@@ -274,7 +292,7 @@ class GraphCache:
         gc.disable()
         try:
             with torch.cuda.graph(graph, pool=self.pools[fb.graph_key[0]]):
-                out = runner._forward_eager(fb, greedy, sample)
+                out = runner._forward_eager(fb, greedy, sample, with_logits)
         finally:
             if was_enabled:
                 gc.enable()

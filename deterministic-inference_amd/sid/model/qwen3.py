@@ -89,12 +89,12 @@ class Qwen3Model:
     @torch.inference_mode()
     def forward(self, fb: ForwardBatch, kv_cache, decode_attn,
                 decode_backend: str = "cuda", greedy: bool = False,
-                sample: bool = False) -> torch.Tensor:
+                sample: bool = False, with_logits: bool = False):
         """fp32 logits [R, vocab] for the sampled rows (bf16-rounded values); with
         greedy=True, the greedy tokens int64 [R] instead (argmax of those logits, fused into
         the lm_head GEMM for decode-sized R); with sample=True (decode batches of at most 256
         rows, no top-k / top-p limit), the sampled tokens int64 [R], drawn inside the lm_head
-        GEMM without writing the logits.
+        GEMM without writing the logits (with_logits=True: (logits, those tokens)).
 
         Same op order as sid/model/qwen3.py:88-115; the residual add + RMSNorm that follows
         each o / down projection consumes the projection directly (fused), and the down
@@ -138,8 +138,11 @@ class Qwen3Model:
         rows = x if fb.sample_indices is None else gather_rows(x, fb.sample_indices)
         if sample:  # the sampler fused into the lm_head (rows without top-k / top-p)
             r = rows.shape[0]
-            return linear_sample(rows, self.w["lm_head"], fb.temperatures[:r], fb.seeds[:r],
-                                 fb.sample_positions[:r])
+            tokens = linear_sample(rows, self.w["lm_head"], fb.temperatures[:r], fb.seeds[:r],
+                                   fb.sample_positions[:r])
+            if with_logits:  # also the logits, for the rows that need the sampler kernel
+                return linear(rows, self.w["lm_head"], out_fp32=True), tokens
+            return tokens
         if greedy:
             if linear_argmax_supported(rows.shape[0], rows.shape[1]):
                 return linear_argmax(rows, self.w["lm_head"])

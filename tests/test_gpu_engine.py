@@ -64,6 +64,44 @@ def test_batch_invariant_identical_across_batch_widths():
     assert len({h for h, _ in out.values()}) == 1
 
 
+def test_batch_invariant_row_path_ignores_co_tenants_limits():
+    """batch_invariant, T = 0.7: a request without top-k / top-p limits draws every token
+    with the lm_head-fused sampler (the engine's choice at max_decode_batch <= 256) whether
+    its co-tenants have limits or not; the rows with limits use the sampler kernel. The two
+    paths can disagree at float near-ties, so the path must follow from the row alone."""
+    from sid.engine.model_runner import ModelRunner
+    eng = _engine(Mode.BATCH_INVARIANT)
+    calls = []
+    orig = ModelRunner.forward
+
+    def spy(self, fb, greedy=False, sample=False, with_logits=False):
+        if fb.mode.name == "DECODE":
+            calls.append((sample, with_logits))
+        return orig(self, fb, greedy, sample, with_logits)
+
+    watched = _prompts(1, 101)[0]
+    fillers = _prompts(5, 201)
+    free = SamplingParams(max_new_tokens=40, temperature=0.7, seed=99, ignore_eos=True)
+    tokens = {}
+    ModelRunner.forward = spy
+    try:
+        for limits in ("none", "top_k", "top_p"):
+            params = [free] + [SamplingParams(
+                max_new_tokens=40, temperature=0.7, seed=5 + i, ignore_eos=True,
+                top_k=20 if limits == "top_k" else -1,
+                top_p=0.9 if limits == "top_p" else 1.0) for i in range(len(fillers))]
+            calls.clear()
+            tokens[limits] = eng.generate([watched] + fillers, params)[0].token_ids
+            decode_calls = set(calls)
+            if limits == "none":
+                assert decode_calls == {(True, False)}, decode_calls
+            else:
+                assert decode_calls == {(True, True)}, decode_calls
+    finally:
+        ModelRunner.forward = orig
+    assert tokens["none"] == tokens["top_k"] == tokens["top_p"]
+
+
 def test_engine_step_api_and_release():
     eng = _engine(Mode.DVR)
     free0 = eng.kv.free_count

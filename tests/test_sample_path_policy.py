@@ -1,7 +1,9 @@
 """Which decode batches draw their tokens inside the lm_head (ModelRunner.fused_sample), on
 the host: nothing here launches a kernel. The fused and the logits + sampler paths agree
 except at float near-ties, so in batch_invariant mode the choice must not depend on the
-batch (one answer per engine), while nondet/dvr pick the faster path by row count."""
+batch (one answer per engine; a batch mixing rows with and without top-k / top-p limits
+still takes the fused path for the latter, tests/test_gpu_engine.py), while nondet/dvr
+pick the faster path by row count."""
 
 from __future__ import annotations
 
@@ -15,8 +17,10 @@ from sid.engine.model_runner import ModelRunner
 
 
 def _runner(max_decode_batch):
-    return SimpleNamespace(cfg=SimpleNamespace(max_decode_batch=max_decode_batch),
-                           mcfg=SimpleNamespace(hidden_size=1024))
+    r = SimpleNamespace(cfg=SimpleNamespace(max_decode_batch=max_decode_batch),
+                        mcfg=SimpleNamespace(hidden_size=1024))
+    r._invariant_fused = lambda: ModelRunner._invariant_fused(r)
+    return r
 
 
 def _fb(rows, invariant, untruncated=True, mode=ForwardMode.DECODE):
