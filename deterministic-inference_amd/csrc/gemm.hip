@@ -285,7 +285,13 @@ constexpr int TT_SUB_PER_CHUNK = KC / TT_K;
 // over the tile's columns, in argmax_better's order, and writes it to
 // best_val / best_idx [blockIdx.x][M] for argmax_finalize_kernel; y may then be null (no
 // logits written).
-template <int WM, int WN, int MB, int NB, int PF, bool AM = false>
+//
+// SW (gate_up + SwiGLU, weights [gate rows | up rows] of inter rows each): the tile's first
+// NB/2 column blocks of each wave are gate rows and the last NB/2 the up rows of the same
+// inter columns, so a lane holds both values of its outputs; the epilogue writes
+// act[row][c] = silu_mul1(gate, up) of the bf16-rounded projections ([M, inter], the bits of
+// sid_silu_mul over sid_linear's output) and no projection.
+template <int WM, int WN, int MB, int NB, int PF, bool AM = false, bool SW = false>
 __global__ void __launch_bounds__(WM * WN * 64, AM ? 4 : 1) linear_tiled_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ bias, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
@@ -325,7 +331,16 @@ __global__ void __launch_bounds__(WM * WN * 64, AM ? 4 : 1) linear_tiled_kernel(
     const int v = tid + THREADS * i;
     brow[i] = v >> 3;
     bvec[i] = v & 7;
-    wrow[i] = w + min<int64_t>(n0 + brow[i], N - 1) * K + bvec[i] * 8;
+    int64_t wr = n0 + brow[i];
+    if constexpr (SW) {  // LDS row j = wave column block's row: gate or up row of column c
+      static_assert(NB % 2 == 0, "SwiGLU tiles pair gate and up column blocks");
+      const int jw = brow[i] / (NB * 16);
+      const int jb = (brow[i] / 16) % NB;
+      const int64_t c = blockIdx.x * (TN / 2) + jw * (NB / 2) * 16 + (jb % (NB / 2)) * 16 +
+                        (brow[i] % 16);
+      wr = jb < NB / 2 ? c : N / 2 + c;
+    }
+    wrow[i] = w + min<int64_t>(wr, N - 1) * K + bvec[i] * 8;
   }
   static_assert(PF == 1 || PF == 2 || PF == 4, "PF must divide the 4 sub-tiles of a chunk");
   bf16x8_v ra[PF][LA], rb[PF][LB];
@@ -432,7 +447,24 @@ __global__ void __launch_bounds__(WM * WN * 64, AM ? 4 : 1) linear_tiled_kernel(
   }
 
   // Lane holds rows 16*mb + 4*g + i, column 16*nb + r of the wave's block.
-  if constexpr (!AM) {
+  if constexpr (SW) {
+    const int64_t inter = N / 2;
+#pragma unroll
+    for (int nb = 0; nb < NB / 2; ++nb) {
+      const int64_t col = blockIdx.x * (TN / 2) + wn * (NB / 2) * 16 + 16 * nb + r;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t row = m0 + MB * 16 * wm + 16 * mb + 4 * g + i;
+          if (row >= M) continue;
+          const float gv = round_bf16(tot[mb][nb][i]);
+          const float uv = round_bf16(tot[mb][nb + NB / 2][i]);
+          static_cast<bf16_t*>(y)[row * inter + col] = f32_to_bf16(silu_mul1(gv, uv));
+        }
+      }
+    }
+  } else if constexpr (!AM) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const int64_t col = n0 + NB * 16 * wn + 16 * nb + r;
@@ -519,13 +551,13 @@ __global__ void __launch_bounds__(WM * WN * 64, AM ? 4 : 1) linear_tiled_kernel(
   }
 }
 
-template <int WM, int WN, int MB, int NB, int PF, bool AM = false>
+template <int WM, int WN, int MB, int NB, int PF, bool AM = false, bool SW = false>
 void launch_tiled(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
                   int64_t n, int64_t k, int out_fp32, hipStream_t s, float* best_val = nullptr,
                   int* best_idx = nullptr) {
   constexpr int TM = WM * MB * 16, TN = WN * NB * 16;
   const dim3 grid((unsigned)((n + TN - 1) / TN), (unsigned)((m + TM - 1) / TM));
-  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB, PF, AM>), grid, dim3(WM * WN * 64), 0, s,
+  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB, PF, AM, SW>), grid, dim3(WM * WN * 64), 0, s,
                      (const bf16_t*)x, ldx, (const bf16_t*)w, (const bf16_t*)bias, y, m, n, k,
                      out_fp32, best_val, best_idx);
 }
@@ -1559,6 +1591,21 @@ extern "C" int sid_linear_silu_mul(const void* x, const void* w, void* out, int6
                   reinterpret_cast<uintptr_t>(out) % 4 == 0,
               "linear_silu_mul: misaligned operand");
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (m >= kTiledMinM && inter % 64 == 0) {
+    // Prefill-sized M: the tiled GEMM with the SwiGLU epilogue, in sid_linear's tile shapes
+    // (grid over the 2 * inter projection columns; the [M, 2 * inter] projection is never
+    // written). Measured against sid_linear + sid_silu_mul, same bits.
+    SID_REQUIRE((m + 127) / 128 <= 65535, "linear_silu_mul: too many rows");
+    const int64_t n = 2 * inter;
+    if (((m + 127) / 128) * ((n + 127) / 128) >= kTiledWideMinTiles) {
+      launch_tiled<4, 2, 2, 4, 1, false, true>(x, k, w, nullptr, out, m, n, k, 0, s);
+    } else if (((m + 127) / 128) * ((n + 63) / 64) <= stream_grid()) {
+      launch_tiled<4, 2, 2, 2, 2, false, true>(x, k, w, nullptr, out, m, n, k, 0, s);
+    } else {
+      launch_tiled<4, 2, 2, 2, 1, false, true>(x, k, w, nullptr, out, m, n, k, 0, s);
+    }
+    return check_launch("linear_silu_mul");
+  }
   const int mbs = m >= MROWS ? 4 : static_cast<int>((m + 15) / 16);
   // Two column blocks per wave halve the x read per output (M = 64, I = 3072, weights from
   // HBM: 12.3 -> 9.3 us); an I that is not a multiple of 16 takes one block per wave.

@@ -68,11 +68,12 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor,
 # graph-timed pair -> fused: M=1 8.0 -> 5.2 us, M=32 9.9 -> 6.8, M=64 12.5 -> 9.3,
 # M=128 16.0 -> 14.6, M=192 19.3 -> 19.8).
 LINEAR_SILU_MAX_ROWS = 128
+LINEAR_SILU_TILED_MIN_ROWS = 256  # from here: the tiled GEMM with the SwiGLU epilogue
 
 
 def linear_silu_mul_preferred(m: int, k: int) -> bool:
     """Shapes where linear_silu_mul is used for the MLP's first half (K = 1024)."""
-    return 1 <= m <= LINEAR_SILU_MAX_ROWS and k == 1024
+    return (1 <= m <= LINEAR_SILU_MAX_ROWS or m >= LINEAR_SILU_TILED_MIN_ROWS) and k == 1024
 
 
 def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

@@ -245,10 +245,13 @@ int sid_silu_mul_partials(const float* partials, int nchunks, void* out, int64_t
  * bf16(bf16(silu(g)) * u) with g = row j and u = row I + j of
  * x @ w^T (x bf16 [M, K] contiguous, w bf16 [2I, K]), both in sid_linear's
  * reduction order and rounding. Bit-identical to sid_linear_partials followed
- * by sid_silu_mul_partials. K must be 1024; I a multiple of 8; x and w
- * 16-byte aligned. out bf16 [M, I].
+ * by sid_silu_mul_partials (and to sid_linear followed by sid_silu_mul).
+ * K must be 1024; I a multiple of 8; x and w 16-byte aligned. out bf16 [M, I].
+ * From M = 256 (with I a multiple of 64) it runs as the tiled prefill GEMM
+ * with the SwiGLU applied in its epilogue; the [M, 2I] projection is never
+ * written.
  * Replaces sid/model/qwen3.py:84-85 (gate_up = F.linear(...);
- * F.silu(gate) * up) for decode-sized batches.
+ * F.silu(gate) * up) for decode-sized batches and prefill.
  */
 int sid_linear_silu_mul(const void* x, const void* w, void* out, int64_t m, int64_t k,
                         int64_t inter, void* stream);

@@ -83,11 +83,13 @@ def test_silu_mul_partials_matches_unfused(t):
     assert torch.equal(silu_mul_partials(linear_partials(x, w)), silu_mul(linear(x, w)))
 
 
-@pytest.mark.parametrize("t", [1, 5, 16, 33, 64, 65, 128, 200, 256])
-@pytest.mark.parametrize("inter", [3072, 96])
+@pytest.mark.parametrize("t", [1, 5, 16, 33, 64, 65, 128, 200, 256, 300, 1000, 2048])
+@pytest.mark.parametrize("inter", [3072, 192, 96])
 def test_linear_silu_mul_matches_unfused(t, inter):
     """gate_up projection + SwiGLU in one launch == linear_partials + silu_mul_partials (and
-    == linear + silu_mul), bit for bit, on full and ragged 64-row groups."""
+    == linear + silu_mul), bit for bit, on full and ragged 64-row groups; from 256 rows the
+    tiled GEMM with the SwiGLU epilogue in each of its tile shapes (inter 96 keeps the small-M
+    kernel)."""
     from sid.kernels.matmul_persistent import linear, linear_partials, linear_silu_mul
     from sid.kernels.ops import silu_mul, silu_mul_partials
     print(f"linear_silu_mul t={t} inter={inter}", flush=True)
