@@ -11,11 +11,6 @@
 namespace sid {
 namespace {
 
-// Rows up to which the gate_up projection and SwiGLU run as sid_linear_silu_mul's small-M
-// kernel (the same bits as the split-K pair; faster up to here on MI355X, slower beyond),
-// and from which they run as its tiled form (the tiled GEMM with the SwiGLU epilogue).
-constexpr int64_t kLinearSiluMaxRows = 128;
-constexpr int64_t kLinearSiluTiledMinRows = 256;
 
 // Whether a projection of t rows and n output columns takes the split-K path (the same bits
 // either way). Narrow outputs (n <= 2048: o, down) have few output tiles, so split-K keeps
@@ -175,9 +170,9 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
       SID_TRY(sid_linear(l.attn, ao, lw.o, nullptr, l.x, t, h, ao, 0, stream));
       SID_TRY(sid_fused_add_rmsnorm(l.x, l.resid, lw.post_ln, t, h, eps, stream));
     }
-    // act = silu(gate) * up (one launch, except for 129-255 rows)
-    if ((t <= kLinearSiluMaxRows || t >= kLinearSiluTiledMinRows) && h == 1024 &&
-        inter % 64 == 0) {
+    // act = silu(gate) * up in one launch (K = 1024 shapes; the split-K or direct GEMM +
+    // silu_mul pair otherwise)
+    if (h == 1024 && inter % 64 == 0) {
       SID_TRY(sid_linear_silu_mul(l.x, lw.gate_up, l.act, t, h, inter, stream));
     } else if (split_gu) {
       SID_TRY(sid_linear_partials(l.x, h, lw.gate_up, part, t, 2 * inter, h, stream));

@@ -569,6 +569,8 @@ void launch_tiled(const void* x, int64_t ldx, const void* w, const void* bias, v
 // sets in AGPRs at one wave per SIMD and reached 13%.)
 constexpr int64_t kTiledMinM = 256;
 constexpr int64_t kTiledWideMinTiles = 512;
+// sid_linear_silu_mul takes the tiled form from this many rows up.
+constexpr int64_t kLinearSiluTiledMinM = 96;
 
 // K of the streaming kernel below, its chunk count and LDS row stride of staged x.
 constexpr int WIDE_K = 1024;
@@ -1591,10 +1593,13 @@ extern "C" int sid_linear_silu_mul(const void* x, const void* w, void* out, int6
                   reinterpret_cast<uintptr_t>(out) % 4 == 0,
               "linear_silu_mul: misaligned operand");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (m >= kTiledMinM && inter % 64 == 0) {
-    // Prefill-sized M: the tiled GEMM with the SwiGLU epilogue, in sid_linear's tile shapes
+  if (m >= kLinearSiluTiledMinM && inter % 64 == 0) {
+    // From 96 rows: the tiled GEMM with the SwiGLU epilogue, in sid_linear's tile shapes
     // (grid over the 2 * inter projection columns; the [M, 2 * inter] projection is never
-    // written). Measured against sid_linear + sid_silu_mul, same bits.
+    // written). Same bits as the kernel below and as sid_linear + sid_silu_mul. Measured
+    // (I = 3072, weights from HBM, graph-timed): M = 64 11.9 us vs 9.8 for the kernel below,
+    // M = 96 12.4 vs 13.6, M = 128 12.8 vs 15.6, M = 192 12.5 vs 20.7; against sid_linear +
+    // sid_silu_mul M = 256 11.0 vs 15.1 us, M = 2048 38.4 vs 48.2, M = 8192 143 vs 171.
     SID_REQUIRE((m + 127) / 128 <= 65535, "linear_silu_mul: too many rows");
     const int64_t n = 2 * inter;
     if (((m + 127) / 128) * ((n + 127) / 128) >= kTiledWideMinTiles) {

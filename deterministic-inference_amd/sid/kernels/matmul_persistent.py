@@ -61,19 +61,15 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor,
     return out
 
 
-# Rows up to which the fused gate_up + SwiGLU kernel replaces linear_partials +
-# silu_mul_partials. Every workgroup reads its rows' whole x (K = 1024) for 16 output
-# columns, twice the x traffic of the split-K kernel per weight byte, against which it saves
-# a launch and the fp32 partials' round trip (MI355X, gate_up 6144 x 1024, weights from HBM,
-# graph-timed pair -> fused: M=1 8.0 -> 5.2 us, M=32 9.9 -> 6.8, M=64 12.5 -> 9.3,
-# M=128 16.0 -> 14.6, M=192 19.3 -> 19.8).
-LINEAR_SILU_MAX_ROWS = 128
-LINEAR_SILU_TILED_MIN_ROWS = 256  # from here: the tiled GEMM with the SwiGLU epilogue
-
-
+# sid_linear_silu_mul (gate_up projection + SwiGLU in one launch, no projection written)
+# serves every row count at K = 1024: up to 95 rows a kernel in which every workgroup reads
+# its rows' whole x for 16 output columns (against the split-K pair it saves a launch and the
+# fp32 partials' round trip: M=1 8.0 -> 5.2 us, M=32 9.9 -> 6.8, M=64 12.5 -> 9.3), from 96
+# rows the tiled GEMM with the SwiGLU in its epilogue (M=128 15.6 -> 12.8 us, M=192
+# 20.7 -> 12.5, M=2048 48.2 -> 38.4 against linear + silu_mul). Same bits everywhere.
 def linear_silu_mul_preferred(m: int, k: int) -> bool:
     """Shapes where linear_silu_mul is used for the MLP's first half (K = 1024)."""
-    return (1 <= m <= LINEAR_SILU_MAX_ROWS or m >= LINEAR_SILU_TILED_MIN_ROWS) and k == 1024
+    return m >= 1 and k == 1024
 
 
 def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

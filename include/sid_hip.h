@@ -247,7 +247,7 @@ int sid_silu_mul_partials(const float* partials, int nchunks, void* out, int64_t
  * reduction order and rounding. Bit-identical to sid_linear_partials followed
  * by sid_silu_mul_partials (and to sid_linear followed by sid_silu_mul).
  * K must be 1024; I a multiple of 8; x and w 16-byte aligned. out bf16 [M, I].
- * From M = 256 (with I a multiple of 64) it runs as the tiled prefill GEMM
+ * From M = 96 (with I a multiple of 64) it runs as the tiled prefill GEMM
  * with the SwiGLU applied in its epilogue; the [M, 2I] projection is never
  * written.
  * Replaces sid/model/qwen3.py:84-85 (gate_up = F.linear(...);
