@@ -14,13 +14,13 @@ namespace {
 
 // Whether a projection of t rows and n output columns takes the split-K path (the same bits
 // either way). Narrow outputs (n <= 2048: o, down) have few output tiles, so split-K keeps
-// the chip busy up to 4x `wide_max` rows; n <= 4096 (qkv) up to `wide_max`; wider ones
-// (gate_up) below `wide_max`, where the tiled direct GEMM takes over. (MI355X, fused consumers included: down at 512 rows 21.2 us
-// split vs 34.9 direct, o 18.6 vs 24.8; qkv at 384 rows 13.7 vs 13.2; gate_up at 256 rows
-// 21.6 vs 17.2.)
+// the chip busy up to 3x `wide_max` rows; n <= 4096 (qkv) below 5/8 of it; wider ones below
+// `wide_max`; beyond, the tiled direct GEMM is faster. (MI355X, weights from HBM, fused
+// consumers included, split vs direct: o at 512 rows 18.9 vs 20.1 us, at 1024 27.6 vs 23.4;
+// down 21.8 vs 28.6, 36.8 vs 31.2; qkv at 128 rows 14.5 vs 15.8, at 192 17.9 vs 15.8.)
 bool split_for(int64_t t, int64_t n, int64_t wide_max) {
-  if (n <= 2048) return t <= 4 * wide_max;
-  if (n <= 4096) return t <= wide_max;
+  if (n <= 2048) return t <= 3 * wide_max;
+  if (n <= 4096) return t < 5 * wide_max / 8;
   return t < wide_max;
 }
 

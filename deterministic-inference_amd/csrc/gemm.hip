@@ -566,8 +566,10 @@ void launch_tiled(const void* x, int64_t ldx, const void* w, const void* bias, v
 // outputs (a 128 x 128 tile), or 32 x 32 (128 x 64) when 128 x 128 tiles would leave fewer
 // than two workgroups per CU. (Measured on prefill shapes: 25-29% of the bf16 MFMA peak at
 // M >= 2048 vs 8% for the 64-row-group kernel; 4 waves of 64 x 64 held both accumulator
-// sets in AGPRs at one wave per SIMD and reached 13%.)
-constexpr int64_t kTiledMinM = 256;
+// sets in AGPRs at one wave per SIMD and reached 13%. From 64 rows it also beats the 64-row-
+// group kernel on the decode shapes, weights from HBM, consumer included: qkv at 128 rows
+// 15.8 vs 22.1 us, o 19.3 vs 33.0, down 28.1 vs 47.3.)
+constexpr int64_t kTiledMinM = 64;
 constexpr int64_t kTiledWideMinTiles = 512;
 // sid_linear_silu_mul takes the tiled form from this many rows up.
 constexpr int64_t kLinearSiluTiledMinM = 96;

@@ -24,22 +24,22 @@ from sid.kernels.rmsnorm import fused_add_rmsnorm, rmsnorm
 from sid.kernels.rope import RotaryEmbedding
 
 
-# Split-K projections (chunk partials folded by the consuming fused kernel) or direct GEMMs:
-# both give identical bits, so this is a speed choice per projection shape. Outputs of
-# N <= 2048 columns (o, down: few output tiles) split up to 4 x SPLIT_K_MAX_TOKENS rows,
-# N <= 4096 (qkv) up to SPLIT_K_MAX_TOKENS, wider ones (gate_up) below it (at and above it
-# the tiled direct GEMM is faster). The native executor applies the same rule
-# (sid_qwen3_model.split_k_max_tokens). MI355X, consumers included: down at 512 rows 21.2 us
-# split vs 34.9 direct, o 18.6 vs 24.8; qkv at 384 rows 13.7 vs 13.2; gate_up at 256 rows
-# 21.6 vs 17.2.
+# Split-K projections (chunk partials folded by the consuming fused kernel) or direct GEMMs
+# (the tiled kernel from 64 rows): both give identical bits, so this is a speed choice per
+# projection shape. With W = SPLIT_K_MAX_TOKENS: outputs of N <= 2048 columns (o, down: few
+# output tiles) split up to 3 W rows, N <= 4096 (qkv) below 5 W / 8, wider ones below W.
+# The native executor applies the same rule (sid_qwen3_model.split_k_max_tokens). MI355X,
+# weights from HBM, consumers included (split vs direct, us): o at 512 rows 18.9 vs 20.1,
+# at 1024 27.6 vs 23.4; down 21.8 vs 28.6, 36.8 vs 31.2; qkv at 128 rows 14.5 vs 15.8, at
+# 192 17.9 vs 15.8, at 256 20.7 vs 16.2.
 SPLIT_K_MAX_TOKENS = 256
 
 
 def split_k_preferred(rows: int, n: int, wide_max: int = SPLIT_K_MAX_TOKENS) -> bool:
     if n <= 2048:
-        return rows <= 4 * wide_max
+        return rows <= 3 * wide_max
     if n <= 4096:
-        return rows <= wide_max
+        return rows < 5 * wide_max // 8
     return rows < wide_max
 
 

@@ -49,7 +49,7 @@ def test_next_rows_skip_stopped_requests():
 
 def test_split_k_rule():
     w = SPLIT_K_MAX_TOKENS
-    assert split_k_preferred(4 * w, 1024) and not split_k_preferred(4 * w + 1, 1024)
-    assert split_k_preferred(w, 4096) and not split_k_preferred(w + 1, 4096)
+    assert split_k_preferred(3 * w, 1024) and not split_k_preferred(3 * w + 1, 1024)
+    assert split_k_preferred(5 * w // 8 - 1, 4096) and not split_k_preferred(5 * w // 8, 4096)
     assert split_k_preferred(w - 1, 6144) and not split_k_preferred(w, 6144)
     assert not split_k_preferred(1, 1024, wide_max=0)
