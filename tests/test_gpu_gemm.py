@@ -149,9 +149,9 @@ def test_linear_argmax_ties_and_nan(m):
 @pytest.mark.parametrize("m,n,k", [(256, 1024, 1024), (300, 1024, 2048), (1000, 6144, 1024),
                                    (2048, 4096, 1024), (777, 192, 512), (4100, 1024, 3072)])
 def test_tiled_large_m_bitwise_matches_row_group_kernel(m, n, k):
-    """M >= 256 takes the LDS-tiled MFMA kernel (128 x 128 or 128 x 64 tiles); its bits
-    equal the 64-row-group kernel's on row slices (M < 256 there), with bias, both output
-    dtypes, ragged M and N tails."""
+    """M >= 64 takes the LDS-tiled MFMA kernel (128 x 128 or 128 x 64 tiles); its bits
+    equal the 64-row-group kernel's on row slices of fewer than 64 rows, and its own on a
+    129-row slice, with bias, both output dtypes, ragged M and N tails."""
     from sid.kernels.matmul_persistent import linear
     torch.manual_seed(m + n)
     print(f"m={m} n={n} k={k}", flush=True)
@@ -160,7 +160,7 @@ def test_tiled_large_m_bitwise_matches_row_group_kernel(m, n, k):
     b = torch.randn(n, device="cuda", dtype=torch.bfloat16)
     for bias in (None, b):
         full = linear(x, w, bias)
-        for lo, hi in ((0, 100), (m - 67, m), (m // 2, m // 2 + 129)):
+        for lo, hi in ((0, 63), (m - 33, m), (m // 2, m // 2 + 129)):
             assert torch.equal(full[lo:hi], linear(x[lo:hi].contiguous(), w, bias)), (lo, hi)
     f32 = linear(x, w, out_fp32=True)
     assert torch.equal(f32.to(torch.bfloat16), linear(x, w))
