@@ -15,9 +15,10 @@
 //     256-wide chunk of 64 columns per 4-wave workgroup, x chunk staged in LDS, weights
 //     streamed straight into MFMA B operands; writes partials[c][m][n], which the consumer
 //     kernel folds in chunk order (norm_rope.hip). No cross-workgroup synchronisation.
-//   * linear_kernel: direct y for M < 256 in 64-row groups, every chunk of a column tile
+//   * linear_kernel: direct y for M < 64 in one row group, every chunk of a column tile
 //     in one workgroup with the next chunk's operands prefetched during the MFMAs;
-//   * linear_tiled_kernel: direct y for M >= 256 (prefill), LDS-tiled 128 x 128 / 128 x 64;
+//   * linear_tiled_kernel: direct y for M >= 64 (prefill, and decode / verify rows past the
+//     split-K cuts), LDS-tiled 128 x 128 / 128 x 64; also gate_up with the SwiGLU epilogue;
 //   * linear_stream_kernel: lm_head-shaped N (persistent grid, x staged once per CU), with
 //     an optional fused greedy argmax.
 #include "common.h"
