@@ -34,12 +34,18 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16, round to nearest even; a NaN stays a NaN with the quiet bit set (the top
+// payload bits kept). gfx950's v_cvt_pk_bf16_f32 does exactly this: it matched the integer
+// formulation ((u + 0x7fff + lsb) >> 16; NaN: (u >> 16) | 0x40) on 4M random bit patterns
+// including every NaN class, so the one-instruction form is used.
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_hw{lo, hi}), bf16x2_hw));
+}
+
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<bf16_t>(u >> 16);
+  return static_cast<bf16_t>(cvt_pk_bf16(f, 0.0f));
 }
 
 // Round an fp32 value to the nearest bf16 and return it as fp32.
@@ -55,18 +61,8 @@ __device__ __forceinline__ float silu_mul1(float g, float u) {
   return s * u;
 }
 
-// Two finite fp32 values to packed bf16 (round to nearest even) with the hardware
-// conversion (v_cvt_pk_bf16_f32): no NaN test, so no branch; for finite inputs the bits are
-// pack_bf16x2's.
-typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
-typedef float f32x2_hw __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_bf16x2_finite(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_hw{lo, hi}), bf16x2_hw));
-}
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
-}
+// Two fp32 values to packed bf16 (f32_to_bf16 of each).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return cvt_pk_bf16(lo, hi); }
 
 // DPP lane exchanges inside a row of 16 lanes. The control words are the
 // GCN/CDNA DPP encodings: quad_perm [1,0,3,2] swaps neighbours, quad_perm

@@ -1,0 +1,589 @@
+// The decode step's projections with their neighbours fused in (decode-sized M: a batch of
+// single-token rows). Per layer the chain is
+//
+//   q, K/V cache  <- sid_rmsnorm_qkv_post(r)          input RMSNorm + qkv projection +
+//                                                      q/k-norm + RoPE + cache write
+//   o             <- decode attention(q)
+//   residual, r   <- sid_linear_residual(o, W_o)       o projection + residual add
+//   act           <- sid_rmsnorm_linear_silu_mul(r)    post RMSNorm + gate_up + SwiGLU
+//   residual, r   <- sid_linear_residual(act, W_down)  down projection + residual add
+//
+// where r is the fp32 sum residual + projection (the value sid/kernels/rmsnorm.py:27-42
+// normalises; the bf16 residual is its rounding). Five launches per layer instead of eight,
+// and no fp32 split-K partials in memory.
+//
+// Bits: every projection keeps sid_linear's reduction order (256-wide chunks, each
+// accumulated from zero by 8 v_mfma_f32_16x16x32_bf16 k-steps in increasing k with the same
+// operand layout, chunks left-folded in increasing order, one rounding to bf16), every
+// RMSNorm rmsnorm_kernel's order for a 64-lane row (lane j owns the 8-element vectors
+// j + 64 i, sequential fmaf, xor butterfly), and the q/k-norm + RoPE and the SwiGLU go
+// through the same helpers as qkv_post_kernel and silu_mul_kernel. So the chain's outputs
+// are bit-identical to the unfused sequence sid_linear -> sid_fused_add_rmsnorm ->
+// sid_linear_silu_mul -> ... (checked by the GPU tests), and M-invariant like it.
+//
+// Shape of the work (MI355X: every one of these kernels moves 4-13 MB, i.e. a few us at
+// HBM rate, so what counts is one memory round trip per workgroup): each workgroup issues
+// all of its global loads (weights straight into MFMA B fragments, activations) before its
+// first MFMA, and owns a whole column tile over the whole K, so nothing but the outputs is
+// written. Workgroups that share a weight tile (the row groups of one column tile) are
+// numbered so they land on the same XCD (workgroups are dealt round-robin over the 8 XCDs
+// in id order) and share its L2.
+#include "common.h"
+#include "rowmath.h"
+
+namespace sid {
+namespace {
+
+constexpr int KC = 256;     // chunk width of the canonical reduction order
+constexpr int KSTEP = 32;   // MFMA 16x16x32 k-step
+constexpr int NSTEP = KC / KSTEP;
+
+__device__ __forceinline__ bf16x8_v ld_frag(const bf16_t* p) {
+  return *reinterpret_cast<const bf16x8_v*>(p);
+}
+
+// Workgroup id -> (column tile, row group) with the R row groups of a tile on one XCD
+// (ids congruent mod 8) when the tile count is a multiple of 8.
+__device__ __forceinline__ void xcd_tile(int id, int ntiles, int R, int& tile, int& rg) {
+  if ((ntiles & 7) == 0) {
+    tile = (id & 7) + 8 * ((id >> 3) / R);
+    rg = (id >> 3) % R;
+  } else {
+    tile = id / R;
+    rg = id % R;
+  }
+}
+
+// ---- MFMA operand tiles ---------------------------------------------------------------------
+//
+// The canonical operand layout puts row r, elements 32 s + 8 g .. +7 of a chunk in lane
+// r + 16 g of k-step register s. Loaded straight from memory that is 16 rows x 64 bytes per
+// instruction with neighbouring lanes in different rows, which the memory pipeline serves
+// poorly (measured on MI355X: a 4 MB projection 2x slower than whole-line reads). So a
+// 16-row x 256-element chunk tile is loaded with neighbouring lanes on neighbouring 16-byte
+// pieces (instruction i: rows 2i, 2i + 1, 512 bytes each), and each wave transposes its own
+// tiles through a private 8 KB LDS scratch: the pieces are stored XOR-swizzled
+// (piece c of row r at slot c ^ (r & 15)) so both the stores and the fragment reads are
+// free of bank conflicts. Same values in the same registers as the direct load.
+struct Tile {
+  u32x4_v v[8];
+};
+
+// Issue the loads of a tile; row_ptr(i) (i < 16) gives row i's first element of the chunk.
+template <typename RowPtr>
+__device__ __forceinline__ void tile_load_rows(Tile& t, RowPtr row_ptr, int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bf16_t* p = row_ptr(2 * i + (lane >> 5));
+    t.v[i] = *reinterpret_cast<const u32x4_v*>(p + 8 * (lane & 31));
+  }
+}
+
+// Rows row0 .. row0 + 15 of a matrix with row stride ld (rows past `last` clamped to it; the
+// caller drops their results), elements k0 .. k0 + 255.
+__device__ __forceinline__ void tile_load(Tile& t, const bf16_t* __restrict__ p, int64_t ld,
+                                          int row0, int last, int64_t k0, int lane) {
+  tile_load_rows(t, [&](int i) { return p + static_cast<int64_t>(min(row0 + i, last)) * ld + k0; },
+                 lane);
+}
+
+// Tile -> the 8 k-step fragments, through the wave's LDS scratch (8 KB). LDS operations of a
+// wave complete in order, so a scratch can be reused for the next tile right away.
+__device__ __forceinline__ void tile_frags(const Tile& t, char* scratch, bf16x8_v (&f)[NSTEP],
+                                           int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 2 * i + (lane >> 5);
+    *reinterpret_cast<u32x4_v*>(scratch + row * 512 + 16 * ((lane & 31) ^ (row & 15))) = t.v[i];
+  }
+  const int r = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s)
+    f[s] = *reinterpret_cast<const bf16x8_v*>(scratch + r * 512 + 16 * ((4 * s + g) ^ r));
+}
+
+// ---- the fp32 residual sum r32 -------------------------------------------------------------
+//
+// r32 rows are stored in the RMSNorm lane order so a 64-lane norm reads them with whole-line
+// loads: element 8 v + e of a row (v = j + 64 i: lane j's i-th 8-element vector; e < 8) sits
+// at i * 512 + (e >> 2) * 256 + 4 j + (e & 3).
+__device__ __forceinline__ int r32_pos(int col) {
+  const int v = col >> 3, e = col & 7;
+  return (v >> 6) * 512 + (e >> 2) * 256 + 4 * (v & 63) + (e & 3);
+}
+
+// ---- RMSNorm of a row into the MFMA A tile --------------------------------------------------
+//
+// One wave per row, hidden = 512 PL: lane j holds the 8-element vectors j + 64 i (i < PL)
+// (rmsnorm_kernel's layout for 64 lanes per row). F32: the row is an r32 row; otherwise
+// bf16 in column order. Loads and arithmetic are split so a kernel can issue the loads with
+// its weight loads.
+template <int PL, bool F32>
+__device__ __forceinline__ void norm_row_load(const void* __restrict__ src, int64_t row, int j,
+                                              float (&v)[PL][8]) {
+  constexpr int H = 512 * PL;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    if constexpr (F32) {
+      const float* p = static_cast<const float*>(src) + row * H + 512 * i + 4 * j;
+      const float4 a = *reinterpret_cast<const float4*>(p);
+      const float4 b = *reinterpret_cast<const float4*>(p + 256);
+      v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+      v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+    } else {
+      load8(*reinterpret_cast<const uint4*>(static_cast<const bf16_t*>(src) + row * H +
+                                            8 * (j + 64 * i)),
+            v[i]);
+    }
+  }
+}
+
+// rmsnorm(v) * w rounded to bf16 (rmsnorm_kernel's bits): y[i] = lane j's 8-element vector
+// j + 64 i of the output row, packed.
+template <int PL>
+__device__ __forceinline__ void norm_w_load(const uint4* __restrict__ w, int j, uint4 (&wv)[PL]) {
+#pragma unroll
+  for (int i = 0; i < PL; ++i) wv[i] = w[j + 64 * i];
+}
+
+template <int PL>
+__device__ __forceinline__ void norm_row_apply(const float (&v)[PL][8], int j,
+                                               const uint4 (&wv)[PL], float eps,
+                                               uint4 (&y)[PL]) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) ss = sumsq8(v[i], ss);
+  ss = group_sum64(ss);
+  const float rstd = rms_rstd(ss, 512 * PL, eps);
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    float wf[8], o[8];
+    load8(wv[i], wf);
+    rms_apply8(v[i], rstd, wf, o);
+    y[i] = store8(o);
+  }
+}
+
+// The same, written to row `row` of an A tile in LDS: 16-byte piece p of the row at
+// tile + row * 2 H bytes + 16 (p ^ (row & 15)), the layout a_frag reads (no padding, no bank
+// conflicts).
+template <int PL>
+__device__ __forceinline__ void norm_row_store(const float (&v)[PL][8], int j,
+                                               const uint4 (&wv)[PL], float eps,
+                                               char* tile, int row) {
+  uint4 y[PL];
+  norm_row_apply<PL>(v, j, wv, eps, y);
+#pragma unroll
+  for (int i = 0; i < PL; ++i)
+    *reinterpret_cast<uint4*>(tile + row * (1024 * PL) + 16 * ((j + 64 * i) ^ (row & 15))) = y[i];
+}
+
+// A fragment of k-step s of chunk c from such a tile (row r of row block mb, part g).
+template <int PL>
+__device__ __forceinline__ bf16x8_v a_frag(const char* tile, int row, int c, int s, int g) {
+  const int p = 32 * c + 4 * s + g;
+  return *reinterpret_cast<const bf16x8_v*>(tile + row * (1024 * PL) + 16 * (p ^ (row & 15)));
+}
+
+// ---- projection + residual add ------------------------------------------------------------
+//
+// y = x w^T for a 16-row x 16-column tile over K = 256 NCH: wave c loads chunk c of the x
+// rows and of the w rows (all loads issued before the MFMAs) and accumulates it from zero;
+// the chunk sums meet in LDS and are folded c0 + c1 + ... in order; then
+// r = residual + bf16(y) (fp32), residual = bf16(r), r32 = r (in r32 order).
+template <int NCH>
+__global__ void __launch_bounds__(NCH * 64) linear_residual_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
+    bf16_t* __restrict__ residual, float* __restrict__ r32, int M, int N, int R) {
+  constexpr int64_t K = static_cast<int64_t>(NCH) * KC;
+  constexpr int SS = 17;  // LDS row stride of a chunk tile (floats)
+  __shared__ float sacc[NCH][16 * SS];
+  __shared__ __align__(16) char scratch[NCH][8192];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int tile, rg;
+  xcd_tile(blockIdx.x, N / 16, R, tile, rg);
+  const int n0 = tile * 16;
+  const int m0 = rg * 16;
+  const int64_t k0 = static_cast<int64_t>(wave) * KC;
+  Tile xt, wt;
+  tile_load(xt, x, ldx, m0, M - 1, k0, lane);  // rows >= M clamped, their sums dropped
+  tile_load(wt, w, K, n0, N - 1, k0, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  bf16x8_v xf[NSTEP], wf[NSTEP];
+  tile_frags(xt, scratch[wave], xf, lane);
+  tile_frags(wt, scratch[wave], wf, lane);
+  f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[s], wf[s], acc, 0, 0, 0);
+  // Lane holds rows 4 g + i of column r.
+  const int r = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sacc[wave][(4 * g + i) * SS + r] = acc[i];
+  __syncthreads();
+  const int erow = threadIdx.x >> 4;
+  const int ecol = threadIdx.x & 15;
+  if (threadIdx.x >= 256 || m0 + erow >= M) return;
+  const int64_t off = static_cast<int64_t>(m0 + erow) * N + n0 + ecol;
+  const bf16_t res = residual[off];
+  float tot = sacc[0][erow * SS + ecol];
+#pragma unroll
+  for (int c = 1; c < NCH; ++c) tot += sacc[c][erow * SS + ecol];
+  const float rr = bf16_to_f32(res) + round_bf16(tot);
+  residual[off] = f32_to_bf16(rr);
+  r32[static_cast<int64_t>(m0 + erow) * N + r32_pos(n0 + ecol)] = rr;
+}
+
+// ---- RMSNorm + gate_up projection + SwiGLU ------------------------------------------------
+//
+// act[m, j] = bf16(bf16(silu(g)) * u), g / u the gate / up projections of
+// x = bf16(rmsnorm(src) * norm_w). A workgroup owns 16 MBS rows and 8 NB gate columns (with
+// their up columns); in MFMA column block nb, rows 0-7 are gate rows j0 + 8 nb.. of w and
+// rows 8-15 the matching up rows inter + j0 + 8 nb.. (linear_silu_kernel's layout). Its
+// NCH x NB waves are (chunk, column block) pairs. Every wave issues its weight tile's loads
+// and its rows' loads, normalises its rows into the shared A tile, transposes its weight
+// tile; then every wave runs its chunk's MFMAs for all row blocks, and the chunk sums are
+// folded in order in LDS (aliasing the transposition scratch, dead by then).
+template <int PL, bool F32, int MBS, int NB>
+__global__ void __launch_bounds__(2 * PL * NB * 64) norm_silu_kernel(
+    const void* __restrict__ src, const uint4* __restrict__ norm_w, float eps,
+    const bf16_t* __restrict__ w, bf16_t* __restrict__ out, int M, int inter, int R) {
+  constexpr int NCH = 2 * PL;
+  constexpr int H = 512 * PL;
+  constexpr int NW = NCH * NB;
+  constexpr int ROWS = 16 * MBS;
+  constexpr int SS = 16 * NB + 1;    // LDS row stride of a chunk-sum tile (floats)
+  constexpr int RPW = (ROWS + NW - 1) / NW;
+  constexpr int SCRATCH = NW * 8192;
+  constexpr int SACC = NCH * ROWS * SS * 4;
+  __shared__ __align__(16) char sx[ROWS * 2 * H];
+  __shared__ __align__(16) char spool[SCRATCH > SACC ? SCRATCH : SACC];
+  float (*sacc)[ROWS * SS] = reinterpret_cast<float (*)[ROWS * SS]>(spool);
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int c = wave % NCH;
+  const int nb = wave / NCH;
+  int tile, rg;
+  xcd_tile(blockIdx.x, inter / (8 * NB), R, tile, rg);
+  const int j0 = tile * 8 * NB;
+  const int m0 = rg * ROWS;
+
+  // Norm weights and activation rows first: the norm waits only for them.
+  uint4 nw[PL];
+  norm_w_load<PL>(norm_w, lane, nw);
+  float v[RPW][PL][8];
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int row = wave + NW * q;
+    if (row < ROWS) norm_row_load<PL, F32>(src, min(m0 + row, M - 1), lane, v[q]);
+  }
+  Tile wt;
+  tile_load_rows(wt, [&](int i) {
+    const int64_t wr = i < 8 ? j0 + 8 * nb + i : inter + j0 + 8 * nb + (i - 8);
+    return w + wr * H + static_cast<int64_t>(c) * KC;
+  }, lane);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int row = wave + NW * q;
+    if (row < ROWS) norm_row_store<PL>(v[q], lane, nw, eps, sx, row);
+  }
+  bf16x8_v wf[NSTEP];
+  tile_frags(wt, spool + wave * 8192, wf, lane);
+  __syncthreads();
+  f32x4_v acc[MBS];
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) acc[mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+#pragma unroll
+    for (int mb = 0; mb < MBS; ++mb)
+      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_frag<PL>(sx, 16 * mb + r, c, s, g),
+                                                        wf[s], acc[mb], 0, 0, 0);
+  }
+  __syncthreads();  // every wave is done with its scratch before the chunk sums reuse it
+#pragma unroll
+  for (int mb = 0; mb < MBS; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sacc[c][(16 * mb + 4 * g + i) * SS + 16 * nb + r] = acc[mb][i];
+  }
+  __syncthreads();
+  // ROWS x 8 NB outputs, two adjacent gate columns per thread.
+  for (int o = threadIdx.x; o < ROWS * 4 * NB; o += NW * 64) {
+    const int row = o / (4 * NB);
+    const int q = o % (4 * NB);
+    const int b = q >> 2;
+    const int col = 2 * (q & 3);
+    if (m0 + row >= M) continue;
+    const int base = row * SS + 16 * b + col;
+    float y[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float gs = sacc[0][base + e];
+      float us = sacc[0][base + 8 + e];
+#pragma unroll
+      for (int k = 1; k < NCH; ++k) {
+        gs += sacc[k][base + e];
+        us += sacc[k][base + 8 + e];
+      }
+      y[e] = silu_mul1(round_bf16(gs), round_bf16(us));
+    }
+    *reinterpret_cast<uint32_t*>(out + static_cast<int64_t>(m0 + row) * inter + j0 + 8 * b + col) =
+        pack_bf16x2(y[0], y[1]);
+  }
+}
+
+// ---- RMSNorm + qkv projection + q/k-norm + RoPE + KV-cache write -----------------------
+//
+// A workgroup owns one head (128 projection columns: a q, k or v head) of 16 rows. Its 8
+// waves are the head's 16-column blocks; wave b holds its block's weights for every chunk
+// (all loads issued first, with the rows the workgroup normalises into LDS), accumulates
+// chunk by chunk and folds in registers. The bf16-rounded head then goes through
+// qkv_post_kernel's epilogue: q / k heads per-head RMSNorm + RoPE (16 lanes per row), q to
+// q_out, k and v to the pools at slots[row] (negative or out-of-range slots skipped).
+constexpr int QD = 128;
+
+template <int PL, bool F32>
+__global__ void __launch_bounds__(512) norm_qkv_kernel(
+    const void* __restrict__ src, const uint4* __restrict__ norm_w, float eps,
+    const bf16_t* __restrict__ w, int M, int num_q_heads, int num_kv_heads, int R,
+    const uint4* __restrict__ q_norm, const uint4* __restrict__ k_norm,
+    const int64_t* __restrict__ positions, const float* __restrict__ cos_sin,
+    int64_t max_positions, const int64_t* __restrict__ slots, uint4* __restrict__ q_out,
+    uint4* __restrict__ k_cache, uint4* __restrict__ v_cache, int64_t num_slots) {
+  constexpr int NCH = 2 * PL;
+  constexpr int H = 512 * PL;
+  constexpr int YS = QD + 4;
+  __shared__ __align__(16) char sx[16 * 2 * H];
+  __shared__ __align__(16) char scratch[8][8192];
+  __shared__ __align__(16) float sy[16 * YS];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int heads = num_q_heads + 2 * num_kv_heads;
+  int head, rg;
+  xcd_tile(blockIdx.x, heads, R, head, rg);
+  const int m0 = rg * 16;
+
+  // Epilogue operands first (thread t < 256: row t / 16, head lanes t % 16), then the norm
+  // weights and rows, then the weight tiles: each wait covers only what it needs.
+  const int row = threadIdx.x >> 4;
+  const int j = threadIdx.x & 15;
+  const int64_t t = min(m0 + row, M - 1);
+  const bool valid = threadIdx.x < 256 && m0 + row < M;
+  const bool is_v = head >= num_q_heads + num_kv_heads;
+  const bool is_q = head < num_q_heads;
+  int64_t slot = -1;
+  QkRopeIn in;
+  if (threadIdx.x < 256) {
+    slot = slots[t];
+    if (!is_v) qk_rope_load(in, j, is_q ? q_norm : k_norm, positions[t], cos_sin, max_positions);
+  }
+  uint4 nw[PL];
+  norm_w_load<PL>(norm_w, lane, nw);
+  float v[2][PL][8];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) norm_row_load<PL, F32>(src, min(m0 + wave + 8 * q, M - 1), lane, v[q]);
+  Tile wt[NCH];
+  {
+    const bf16_t* wp = w + static_cast<int64_t>(head * QD + 16 * wave) * H;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) tile_load(wt[c], wp, H, 0, 15, static_cast<int64_t>(c) * KC, lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) norm_row_store<PL>(v[q], lane, nw, eps, sx, wave + 8 * q);
+  __syncthreads();
+  f32x4_v tot;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    bf16x8_v wf[NSTEP];
+    tile_frags(wt[c], scratch[wave], wf, lane);
+    f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_frag<PL>(sx, r, c, s, g), wf[s], acc, 0, 0, 0);
+    if (c == 0) {
+      tot = acc;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tot[i] += acc[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sy[(4 * g + i) * YS + 16 * wave + r] = round_bf16(tot[i]);
+  __syncthreads();
+  if (threadIdx.x >= 256) return;
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = sy[row * YS + 8 * j + e];
+  const bool slot_ok = valid && slot >= 0 && slot < num_slots;
+  const int kv_row = 16 * num_kv_heads;  // uint4 per pool row
+  if (is_v) {
+    if (slot_ok) v_cache[slot * kv_row + (head - num_q_heads - num_kv_heads) * 16 + j] = store8(y);
+    return;
+  }
+  float o[8];
+  qk_head_norm_rope(y, j, in, eps, o);
+  if (is_q) {
+    if (valid) q_out[(t * num_q_heads + head) * 16 + j] = store8(o);
+  } else if (slot_ok) {
+    k_cache[slot * kv_row + (head - num_q_heads) * 16 + j] = store8(o);
+  }
+}
+
+// ---- RMSNorm of fp32 rows (the final norm of the chain) ------------------------------------
+template <int PL>
+__global__ void __launch_bounds__(256) rmsnorm_f32_kernel(const float* __restrict__ x,
+                                                          const uint4* __restrict__ w,
+                                                          bf16_t* __restrict__ out, int M,
+                                                          float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  uint4 nw[PL];
+  norm_w_load<PL>(w, lane, nw);
+  float v[PL][8];
+  norm_row_load<PL, true>(x, min(row, M - 1), lane, v);
+  if (row >= M) return;  // whole waves
+  uint4 y[PL];
+  norm_row_apply<PL>(v, lane, nw, eps, y);
+  uint4* o = reinterpret_cast<uint4*>(out + static_cast<int64_t>(row) * 512 * PL);
+#pragma unroll
+  for (int i = 0; i < PL; ++i) o[lane + 64 * i] = y[i];
+}
+
+}  // namespace
+}  // namespace sid
+
+using namespace sid;
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+extern "C" int sid_linear_residual(const void* x, int64_t ldx, const void* w, void* residual,
+                                   float* r32, int64_t m, int64_t n, int64_t k, void* stream) {
+  SID_REQUIRE(m >= 0 && n >= 0 && k >= 0, "linear_residual: negative size");
+  if (m == 0 || n == 0) return SID_OK;
+  SID_REQUIRE(x && w && residual && r32, "linear_residual: null pointer");
+  SID_REQUIRE(n % 512 == 0, "linear_residual: N=%lld must be a multiple of 512", (long long)n);
+  SID_REQUIRE(k == 1024 || k == 2048 || k == 3072 || k == 4096,
+              "linear_residual: K=%lld must be 1024, 2048, 3072 or 4096", (long long)k);
+  SID_REQUIRE(ldx >= k && ldx % 64 == 0, "linear_residual: row stride %lld must be >= K and a multiple of 64", (long long)ldx);
+  SID_REQUIRE(aligned16(x) && aligned16(w), "linear_residual: operands must be 16-byte aligned");
+  const int64_t R = (m + 15) / 16;
+  SID_REQUIRE(R * (n / 16) < (1ll << 31), "linear_residual: too large");
+  const dim3 grid((unsigned)(R * (n / 16)));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto go = [&](auto kern, int nch) {
+    hipLaunchKernelGGL(kern, grid, dim3(nch * 64), 0, s, (const bf16_t*)x, ldx, (const bf16_t*)w,
+                       (bf16_t*)residual, r32, (int)m, (int)n, (int)R);
+  };
+  switch (k) {
+    case 1024: go(linear_residual_kernel<4>, 4); break;
+    case 2048: go(linear_residual_kernel<8>, 8); break;
+    case 3072: go(linear_residual_kernel<12>, 12); break;
+    default: go(linear_residual_kernel<16>, 16); break;
+  }
+  return check_launch("linear_residual");
+}
+
+extern "C" int sid_rmsnorm_linear_silu_mul(const void* src, int src_fp32, const void* norm_w,
+                                           float eps, const void* w, void* out, int64_t m,
+                                           int64_t hidden, int64_t inter, void* stream) {
+  SID_REQUIRE(m >= 0 && hidden >= 0 && inter >= 0, "rmsnorm_linear_silu_mul: negative size");
+  if (m == 0 || inter == 0) return SID_OK;
+  SID_REQUIRE(src && norm_w && w && out, "rmsnorm_linear_silu_mul: null pointer");
+  SID_REQUIRE(hidden == 512 || hidden == 1024,
+              "rmsnorm_linear_silu_mul: hidden %lld must be 512 or 1024", (long long)hidden);
+  SID_REQUIRE(inter % 24 == 0, "rmsnorm_linear_silu_mul: intermediate %lld not a multiple of 24",
+              (long long)inter);
+  SID_REQUIRE(aligned16(src) && aligned16(norm_w) && aligned16(w) &&
+                  (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+              "rmsnorm_linear_silu_mul: misaligned operand");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int mbs = m <= 16 ? 1 : 2;
+  const int64_t R = (m + 16 * mbs - 1) / (16 * mbs);
+  const int64_t tiles = inter / 24;
+  SID_REQUIRE(R * tiles < (1ll << 31), "rmsnorm_linear_silu_mul: too large");
+  const dim3 grid((unsigned)(R * tiles));
+  auto go = [&](auto kern, int pl) {
+    hipLaunchKernelGGL(kern, grid, dim3(2 * pl * 3 * 64), 0, s, src, (const uint4*)norm_w, eps,
+                       (const bf16_t*)w, (bf16_t*)out, (int)m, (int)inter, (int)R);
+  };
+  const int pl = static_cast<int>(hidden / 512);
+  const bool f = src_fp32 != 0;
+#define SID_NS(PL, F, MB) go(norm_silu_kernel<PL, F, MB, 3>, PL)
+  if (pl == 1) {
+    if (f) { if (mbs == 1) SID_NS(1, true, 1); else SID_NS(1, true, 2); }
+    else { if (mbs == 1) SID_NS(1, false, 1); else SID_NS(1, false, 2); }
+  } else {
+    if (f) { if (mbs == 1) SID_NS(2, true, 1); else SID_NS(2, true, 2); }
+    else { if (mbs == 1) SID_NS(2, false, 1); else SID_NS(2, false, 2); }
+  }
+#undef SID_NS
+  return check_launch("rmsnorm_linear_silu_mul");
+}
+
+extern "C" int sid_rmsnorm_qkv_post(const void* src, int src_fp32, const void* norm_w, float eps,
+                                    const void* w_qkv, int64_t m, int64_t hidden,
+                                    int num_q_heads, int num_kv_heads, int head_dim,
+                                    const void* q_norm, const void* k_norm,
+                                    const int64_t* positions, const float* cos_sin,
+                                    int64_t max_positions, const int64_t* slots, void* q_out,
+                                    void* k_cache, void* v_cache, int64_t num_slots,
+                                    void* stream) {
+  SID_REQUIRE(m >= 0 && hidden >= 0, "rmsnorm_qkv_post: negative size");
+  if (m == 0) return SID_OK;
+  SID_REQUIRE(src && norm_w && w_qkv && q_norm && k_norm && positions && cos_sin && slots &&
+                  q_out && k_cache && v_cache,
+              "rmsnorm_qkv_post: null pointer");
+  SID_REQUIRE(head_dim == QD, "rmsnorm_qkv_post: head_dim must be %d, got %d", QD, head_dim);
+  SID_REQUIRE(num_q_heads > 0 && num_kv_heads > 0, "rmsnorm_qkv_post: bad head counts");
+  SID_REQUIRE(hidden == 512 || hidden == 1024,
+              "rmsnorm_qkv_post: hidden %lld must be 512 or 1024", (long long)hidden);
+  SID_REQUIRE(num_slots > 0, "rmsnorm_qkv_post: empty KV pool");
+  SID_REQUIRE(aligned16(src) && aligned16(norm_w) && aligned16(w_qkv) && aligned16(q_out) &&
+                  aligned16(k_cache) && aligned16(v_cache),
+              "rmsnorm_qkv_post: operands must be 16-byte aligned");
+  const int64_t R = (m + 15) / 16;
+  const int heads = num_q_heads + 2 * num_kv_heads;
+  SID_REQUIRE(R * heads < (1ll << 31), "rmsnorm_qkv_post: too large");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(R * heads));
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, src, (const uint4*)norm_w, eps,
+                       (const bf16_t*)w_qkv, (int)m, num_q_heads, num_kv_heads, (int)R,
+                       (const uint4*)q_norm, (const uint4*)k_norm, positions, cos_sin,
+                       max_positions, slots, (uint4*)q_out, (uint4*)k_cache, (uint4*)v_cache,
+                       num_slots);
+  };
+  if (hidden == 512) {
+    if (src_fp32) go(norm_qkv_kernel<1, true>); else go(norm_qkv_kernel<1, false>);
+  } else {
+    if (src_fp32) go(norm_qkv_kernel<2, true>); else go(norm_qkv_kernel<2, false>);
+  }
+  return check_launch("rmsnorm_qkv_post");
+}
+
+extern "C" int sid_rmsnorm_f32(const float* x, const void* w, void* out, int64_t rows,
+                               int hidden, float eps, void* stream) {
+  SID_REQUIRE(rows >= 0, "rmsnorm_f32: negative rows");
+  if (rows == 0) return SID_OK;
+  SID_REQUIRE(x && w && out, "rmsnorm_f32: null pointer");
+  SID_REQUIRE(hidden == 512 || hidden == 1024 || hidden == 2048,
+              "rmsnorm_f32: hidden %d must be 512, 1024 or 2048", hidden);
+  SID_REQUIRE(aligned16(x) && aligned16(w) && aligned16(out), "rmsnorm_f32: misaligned operand");
+  SID_REQUIRE((rows + 3) / 4 < (1ll << 31), "rmsnorm_f32: too many rows");
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (hidden) {
+    case 512: hipLaunchKernelGGL(rmsnorm_f32_kernel<1>, grid, dim3(256), 0, s, x, (const uint4*)w, (bf16_t*)out, (int)rows, eps); break;
+    case 1024: hipLaunchKernelGGL(rmsnorm_f32_kernel<2>, grid, dim3(256), 0, s, x, (const uint4*)w, (bf16_t*)out, (int)rows, eps); break;
+    default: hipLaunchKernelGGL(rmsnorm_f32_kernel<4>, grid, dim3(256), 0, s, x, (const uint4*)w, (bf16_t*)out, (int)rows, eps); break;
+  }
+  return check_launch("rmsnorm_f32");
+}

@@ -228,10 +228,10 @@ __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     uint4 u;  // p is finite (exp of a finite difference, or 0)
-    u.x = pack_bf16x2_finite(s[8 * kb + 0], s[8 * kb + 1]);
-    u.y = pack_bf16x2_finite(s[8 * kb + 2], s[8 * kb + 3]);
-    u.z = pack_bf16x2_finite(s[8 * kb + 4], s[8 * kb + 5]);
-    u.w = pack_bf16x2_finite(s[8 * kb + 6], s[8 * kb + 7]);
+    u.x = pack_bf16x2(s[8 * kb + 0], s[8 * kb + 1]);
+    u.y = pack_bf16x2(s[8 * kb + 2], s[8 * kb + 3]);
+    u.z = pack_bf16x2(s[8 * kb + 4], s[8 * kb + 5]);
+    u.w = pack_bf16x2(s[8 * kb + 6], s[8 * kb + 7]);
     pf[kb] = __builtin_bit_cast(bf16x8_v, u);
   }
 #pragma unroll

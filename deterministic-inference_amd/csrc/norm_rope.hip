@@ -13,23 +13,12 @@
 // kernels share goes through the same helpers with explicit fmaf, so the
 // fused and unfused paths also agree bit for bit after the first rounding.
 #include "common.h"
+#include "rowmath.h"
 
 #include <cmath>
 
 namespace sid {
 namespace {
-
-__device__ __forceinline__ void load8(const uint4& u, float (&f)[8]) {
-  f[0] = bf16_lo(u.x); f[1] = bf16_hi(u.x);
-  f[2] = bf16_lo(u.y); f[3] = bf16_hi(u.y);
-  f[4] = bf16_lo(u.z); f[5] = bf16_hi(u.z);
-  f[6] = bf16_lo(u.w); f[7] = bf16_hi(u.w);
-}
-
-__device__ __forceinline__ uint4 store8(const float (&f)[8]) {
-  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                    pack_bf16x2(f[6], f[7]));
-}
 
 // An activation row: a bf16 matrix [rows, ld], or GEMM chunk partials
 // fp32 [nchunks][rows][ld] folded in chunk order and rounded to bf16.
@@ -97,36 +86,6 @@ __host__ void dispatch_nch(const RowSrc& src, F&& fn) {
     case 16: return fn.template operator()<16>();
     default: return fn.template operator()<-1>();
   }
-}
-
-// ---- shared arithmetic --------------------------------------------------------------
-
-__device__ __forceinline__ float sumsq8(const float (&v)[8], float acc) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc = fmaf(v[e], v[e], acc);
-  return acc;
-}
-
-// Xor butterfly over an aligned group of `lpr` lanes (identical bits in every lane).
-__device__ __forceinline__ float group_sum(float v, int lpr) {
-  for (int mask = 1; mask < lpr; mask <<= 1) v += lane_xor(v, mask);
-  return v;
-}
-
-__device__ __forceinline__ float rms_rstd(float sumsq, int hidden, float eps) {
-  return 1.0f / sqrtf(sumsq / static_cast<float>(hidden) + eps);
-}
-
-__device__ __forceinline__ void rms_apply8(const float (&v)[8], float rstd, const float (&w)[8],
-                                           float (&y)[8]) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = (v[e] * rstd) * w[e];
-}
-
-// NeoX rotate-half on one (x1, x2) = (x[i], x[i + D/2]) pair.
-__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float& o1, float& o2) {
-  o1 = fmaf(x1, c, -(x2 * s));
-  o2 = fmaf(x2, c, x1 * s);
 }
 
 // ---- RMSNorm ----------------------------------------------------------------------------
@@ -371,35 +330,10 @@ __global__ void __launch_bounds__(128) qkv_post_kernel(
     return;  // v heads occupy whole blocks' tail groups; no cross-lane op follows for them
   }
   const bool is_q = hh < num_q_heads;
-  float wf[8], y[8];
-  load8((is_q ? q_norm : k_norm)[j], wf);
-  const float ss = group_sum(sumsq8(v, 0.0f), 16);
-  rms_apply8(v, rms_rstd(ss, QD, eps), wf, y);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = round_bf16(y[e]);
-
-  const int64_t pos = positions[t];
+  QkRopeIn in;
+  qk_rope_load(in, j, is_q ? q_norm : k_norm, positions[t], cos_sin, max_positions);
   float o[8];
-  if (pos >= 0 && pos < max_positions) {
-    const float* cs = cos_sin + pos * QD;
-    const int ri = 8 * (j & 7);  // rotary index of this lane's first element
-    const bool first_half = j < 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float partner = dpp<DPP_ROW_ROR8>(y[e]);
-      float o1, o2;
-      if (first_half) {
-        rope_pair(y[e], partner, cs[ri + e], cs[QD / 2 + ri + e], o1, o2);
-        o[e] = o1;
-      } else {
-        rope_pair(partner, y[e], cs[ri + e], cs[QD / 2 + ri + e], o1, o2);
-        o[e] = o2;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = y[e];
-  }
+  qk_head_norm_rope(v, j, in, eps, o);
   if (!valid) return;
   if (is_q) {
     q_out[(t * num_q_heads + hh) * 16 + j] = store8(o);

@@ -1,0 +1,139 @@
+// Row arithmetic shared by the norm / RoPE kernels and the GEMMs that fuse them
+// (norm_rope.hip, decode_chain.hip): every kernel that computes an RMSNorm, a q/k-norm or a
+// rotary pair goes through these helpers, so fused and unfused paths give the same bits.
+#pragma once
+
+#include "common.h"
+
+namespace sid {
+
+__device__ __forceinline__ void load8(const uint4& u, float (&f)[8]) {
+  f[0] = bf16_lo(u.x); f[1] = bf16_hi(u.x);
+  f[2] = bf16_lo(u.y); f[3] = bf16_hi(u.y);
+  f[4] = bf16_lo(u.z); f[5] = bf16_hi(u.z);
+  f[6] = bf16_lo(u.w); f[7] = bf16_hi(u.w);
+}
+
+__device__ __forceinline__ uint4 store8(const float (&f)[8]) {
+  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                    pack_bf16x2(f[6], f[7]));
+}
+
+// ---- shared arithmetic --------------------------------------------------------------
+
+__device__ __forceinline__ float sumsq8(const float (&v)[8], float acc) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = fmaf(v[e], v[e], acc);
+  return acc;
+}
+
+// Xor butterfly over an aligned group of `lpr` lanes (identical bits in every lane).
+__device__ __forceinline__ float group_sum(float v, int lpr) {
+  for (int mask = 1; mask < lpr; mask <<= 1) v += lane_xor(v, mask);
+  return v;
+}
+
+// group_sum(v, 64) with the same bits, without LDS round trips: the xor-1 / xor-2 steps are
+// DPP quad permutations; after them a quad holds one value, so the xor-4 partner can be any
+// lane of the other quad (DPP half-mirror); xor-8 is DPP row_ror:8; after that each 16-lane
+// row holds one value R_k, and the last two butterfly steps give (R0 + R1) + (R2 + R3) in
+// every lane (IEEE addition is commutative, so every lane's sum has the same bits).
+__device__ __forceinline__ float group_sum64(float v) {
+  v += dpp<DPP_QUAD_XOR1>(v);
+  v += dpp<DPP_QUAD_XOR2>(v);
+  v += dpp<DPP_HALF_MIRROR>(v);
+  v += dpp<DPP_ROW_ROR8>(v);
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
+__device__ __forceinline__ float rms_rstd(float sumsq, int hidden, float eps) {
+  return 1.0f / sqrtf(sumsq / static_cast<float>(hidden) + eps);
+}
+
+__device__ __forceinline__ void rms_apply8(const float (&v)[8], float rstd, const float (&w)[8],
+                                           float (&y)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = (v[e] * rstd) * w[e];
+}
+
+// NeoX rotate-half on one (x1, x2) = (x[i], x[i + D/2]) pair.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float& o1, float& o2) {
+  o1 = fmaf(x1, c, -(x2 * s));
+  o2 = fmaf(x2, c, x1 * s);
+}
+
+// One q or k head of the fused QKV epilogue, held by an aligned group of 16 lanes (lane j:
+// dims 8j..8j+7 of the head, head_dim 128): per-head RMSNorm with weight w (rmsnorm's lane
+// layout for hidden 128: sequential fmaf over the lane's 8 dims, xor butterfly over the 16
+// lanes), rounded to bf16, then NeoX RoPE at `pos` (the rotate-half partner of lane j is
+// lane j ^ 8, one DPP row_ror:8 away) from the fp32 [cos(64) | sin(64)] table row; a
+// position outside the table leaves the normed values. Every lane of the 16 must be active.
+// group_sum(v, 16) with the same bits, all in DPP (see group_sum64).
+__device__ __forceinline__ float group_sum16(float v) {
+  v += dpp<DPP_QUAD_XOR1>(v);
+  v += dpp<DPP_QUAD_XOR2>(v);
+  v += dpp<DPP_HALF_MIRROR>(v);
+  v += dpp<DPP_ROW_ROR8>(v);
+  return v;
+}
+
+// The per-lane operands of qk_head_norm_rope that come from memory, so a kernel can load
+// them ahead of the values: the norm weights of the lane's 8 dims, and cos / sin of their
+// rotary indices at the row's position (rot false: position outside the table).
+struct QkRopeIn {
+  float w[8], c[8], s[8];
+  bool rot;
+};
+
+__device__ __forceinline__ void qk_rope_load(QkRopeIn& in, int j, const uint4* __restrict__ w,
+                                             int64_t pos, const float* __restrict__ cos_sin,
+                                             int64_t max_positions) {
+  constexpr int D = 128;
+  load8(w[j], in.w);
+  in.rot = pos >= 0 && pos < max_positions;
+  const float* cs = cos_sin + (in.rot ? pos : 0) * D + 8 * (j & 7);
+  const float4 c0 = *reinterpret_cast<const float4*>(cs);
+  const float4 c1 = *reinterpret_cast<const float4*>(cs + 4);
+  const float4 s0 = *reinterpret_cast<const float4*>(cs + D / 2);
+  const float4 s1 = *reinterpret_cast<const float4*>(cs + D / 2 + 4);
+  in.c[0] = c0.x; in.c[1] = c0.y; in.c[2] = c0.z; in.c[3] = c0.w;
+  in.c[4] = c1.x; in.c[5] = c1.y; in.c[6] = c1.z; in.c[7] = c1.w;
+  in.s[0] = s0.x; in.s[1] = s0.y; in.s[2] = s0.z; in.s[3] = s0.w;
+  in.s[4] = s1.x; in.s[5] = s1.y; in.s[6] = s1.z; in.s[7] = s1.w;
+}
+
+// One q or k head of the fused QKV epilogue, held by an aligned group of 16 lanes (lane j:
+// dims 8j..8j+7 of the head, head_dim 128): per-head RMSNorm with weight w (rmsnorm's lane
+// layout for hidden 128: sequential fmaf over the lane's 8 dims, xor butterfly over the 16
+// lanes), rounded to bf16, then NeoX RoPE (the rotate-half partner of lane j is lane j ^ 8,
+// one DPP row_ror:8 away) with the fp32 [cos(64) | sin(64)] table row of the position; a
+// position outside the table leaves the normed values. Every lane of the 16 must be active.
+__device__ __forceinline__ void qk_head_norm_rope(const float (&v)[8], int j, const QkRopeIn& in,
+                                                  float eps, float (&o)[8]) {
+  constexpr int D = 128;
+  float y[8];
+  const float ss = group_sum16(sumsq8(v, 0.0f));
+  rms_apply8(v, rms_rstd(ss, D, eps), in.w, y);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = round_bf16(y[e]);
+  const bool first_half = j < 8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float partner = dpp<DPP_ROW_ROR8>(y[e]);
+    float o1, o2;
+    if (first_half) {
+      rope_pair(y[e], partner, in.c[e], in.s[e], o1, o2);
+      o[e] = o1;
+    } else {
+      rope_pair(partner, y[e], in.c[e], in.s[e], o1, o2);
+      o[e] = o2;
+    }
+    if (!in.rot) o[e] = y[e];
+  }
+}
+
+}  // namespace sid

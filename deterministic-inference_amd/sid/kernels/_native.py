@@ -47,13 +47,18 @@ _SIGNATURES = {
     "sid_linear_sample": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i32,
                           _vp],
     "sid_linear_argmax": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
+    "sid_linear_residual": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "sid_rmsnorm_linear_silu_mul": [_vp, _i32, _vp, _f32, _vp, _vp, _i64, _i64, _i64, _vp],
+    "sid_rmsnorm_qkv_post": [_vp, _i32, _vp, _f32, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp,
+                             _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp],
+    "sid_rmsnorm_f32": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
 }
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
             "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes",
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward",
             "sid_flash_decode_noalloc_scratch_bytes", "sid_linear_sample_workspace_bytes",
             *_SIGNATURES)
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -372,6 +377,74 @@ class NativeLib:
                    q_norm.data_ptr(), k_norm.data_ptr(), float(eps), positions.data_ptr(),
                    cos_sin.data_ptr(), cos_sin.shape[0], slots.data_ptr(), q_out.data_ptr(),
                    k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0], _stream(q_out))
+
+    def linear_residual(self, x, w, residual, r32) -> None:
+        """residual, r32 <- r = residual + bf16(x @ w^T) (fp32 r; residual = bf16(r))."""
+        m, k, n = self._linear_check(x, w)
+        _gpu(residual, "residual", torch.bfloat16)
+        _gpu(r32, "r32", torch.float32)
+        _check(tuple(residual.shape) == (m, n) and tuple(r32.shape) == (m, n),
+               "residual / r32 must be [M, N]")
+        self._call("sid_linear_residual", x.data_ptr(), x.stride(0), w.data_ptr(),
+                   residual.data_ptr(), r32.data_ptr(), m, n, k, _stream(r32))
+
+    @staticmethod
+    def _norm_src(src):
+        _check(src.is_cuda and src.dim() == 2 and src.is_contiguous()
+               and src.dtype in (torch.float32, torch.bfloat16),
+               "norm source must be a contiguous fp32 or bf16 [M, hidden] GPU tensor")
+        return int(src.dtype == torch.float32)
+
+    def rmsnorm_linear_silu_mul(self, src, norm_w, eps: float, w, out) -> None:
+        """out <- silu_mul(bf16(rmsnorm(src) * norm_w) @ w^T), w = [gate rows | up rows]."""
+        f32 = self._norm_src(src)
+        _gpu(norm_w, "norm weight", torch.bfloat16)
+        _gpu(w, "weight", torch.bfloat16)
+        _gpu(out, "out", torch.bfloat16)
+        m, hidden = src.shape
+        _check(w.dim() == 2 and w.shape[1] == hidden and w.shape[0] % 2 == 0
+               and norm_w.numel() == hidden, "rmsnorm_linear_silu_mul shapes")
+        inter = w.shape[0] // 2
+        _check(tuple(out.shape) == (m, inter), "out must be [M, I]")
+        self._call("sid_rmsnorm_linear_silu_mul", src.data_ptr(), f32, norm_w.data_ptr(),
+                   float(eps), w.data_ptr(), out.data_ptr(), m, hidden, inter, _stream(out))
+
+    def rmsnorm_qkv_post(self, src, norm_w, eps: float, w, q_norm, k_norm, positions, cos_sin,
+                         slots, q_out, k_cache, v_cache) -> None:
+        """qkv_post over bf16(rmsnorm(src) * norm_w) @ w^T (one launch)."""
+        f32 = self._norm_src(src)
+        m, hidden = src.shape
+        _gpu(norm_w, "norm weight", torch.bfloat16)
+        _gpu(w, "weight", torch.bfloat16)
+        _gpu(q_out, "q_out", torch.bfloat16)
+        _check(q_out.dim() == 3 and q_out.shape[0] == m, "q_out must be [M, HQ, D]")
+        hq, d = q_out.shape[1], q_out.shape[2]
+        for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+            _gpu(c, name, torch.bfloat16)
+            _check(c.dim() == 3 and c.shape[2] == d, f"{name} must be [S, HKV, D]")
+        hkv = k_cache.shape[1]
+        _check(w.dim() == 2 and w.shape[0] == (hq + 2 * hkv) * d and w.shape[1] == hidden
+               and norm_w.numel() == hidden, "qkv weight must be [(HQ + 2*HKV) * D, hidden]")
+        _gpu(q_norm, "q_norm", torch.bfloat16)
+        _gpu(k_norm, "k_norm", torch.bfloat16)
+        _gpu(positions, "positions", torch.int64)
+        _gpu(slots, "slots", torch.int64)
+        _gpu(cos_sin, "cos_sin", torch.float32)
+        _check(positions.numel() == m and slots.numel() == m, "positions/slots must have M entries")
+        self._call("sid_rmsnorm_qkv_post", src.data_ptr(), f32, norm_w.data_ptr(), float(eps),
+                   w.data_ptr(), m, hidden, hq, hkv, d, q_norm.data_ptr(), k_norm.data_ptr(),
+                   positions.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0], slots.data_ptr(),
+                   q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+                   _stream(q_out))
+
+    def rmsnorm_f32(self, x, w, out, eps: float) -> None:
+        """out <- bf16(rmsnorm(x) * w) for fp32 rows x (rmsnorm's bits)."""
+        _gpu(x, "x", torch.float32)
+        _gpu(w, "weight", torch.bfloat16)
+        _gpu(out, "out", torch.bfloat16)
+        _check(x.dim() == 2 and out.shape == x.shape and w.numel() == x.shape[1], "rmsnorm_f32 shapes")
+        self._call("sid_rmsnorm_f32", x.data_ptr(), w.data_ptr(), out.data_ptr(), x.shape[0],
+                   x.shape[1], float(eps), _stream(out))
 
     def linear_silu_mul(self, x, w, out) -> None:
         _gpu(x, "x", torch.bfloat16)

@@ -74,3 +74,64 @@ def qkv_post(qkv_or_partials: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.
     load_ext().qkv_post(None if partial else qkv_or_partials, qkv_or_partials if partial else None,
                         q_norm, k_norm, eps, positions, cos_sin, slots, q, k_cache, v_cache)
     return q
+
+
+# ---- the decode-step chain (csrc/decode_chain.hip) -----------------------------------------
+
+def r32_positions(hidden: int) -> torch.Tensor:
+    """Where column c of an r32 row is stored (int64 [hidden]): the RMSNorm lane order of
+    csrc/decode_chain.hip (element 8 v + e, v = j + 64 i, at i*512 + (e//4)*256 + 4 j + e%4),
+    so `r32[:, r32_positions(h)]` is the row in column order."""
+    col = torch.arange(hidden)
+    v, e = col >> 3, col & 7
+    return (v >> 6) * 512 + (e >> 2) * 256 + 4 * (v & 63) + (e & 3)
+
+
+def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+                    r32: torch.Tensor) -> None:
+    """In place: r = residual + bf16(x @ weight^T) (fp32), residual = bf16(r), r32 = r stored
+    in the RMSNorm lane order (r32_positions): the projection plus the residual half of
+    fused_add_rmsnorm (sid/kernels/rmsnorm.py:27-42)."""
+    load_ext().linear_residual(x, weight, residual, r32)
+
+
+def rmsnorm_linear_silu_mul(src: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                            weight: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up of bf16(rmsnorm(src) * norm_w) @ weight^T; src an r32 (fp32, lane
+    order) or bf16 rows in column order, [T, H]."""
+    out = torch.empty(src.shape[0], weight.shape[0] // 2, dtype=torch.bfloat16, device=src.device)
+    load_ext().rmsnorm_linear_silu_mul(src, norm_w, eps, weight, out)
+    return out
+
+
+def rmsnorm_qkv_post(src: torch.Tensor, norm_w: torch.Tensor, eps: float, weight: torch.Tensor,
+                     q_norm: torch.Tensor, k_norm: torch.Tensor, positions: torch.Tensor,
+                     cos_sin: torch.Tensor, slots: torch.Tensor, k_cache: torch.Tensor,
+                     v_cache: torch.Tensor, num_q_heads: int) -> torch.Tensor:
+    """qkv_post of the qkv projection of bf16(rmsnorm(src) * norm_w); returns q [T, HQ, D]."""
+    d = k_cache.shape[2]
+    q = torch.empty(src.shape[0], num_q_heads, d, dtype=torch.bfloat16, device=src.device)
+    load_ext().rmsnorm_qkv_post(src, norm_w, eps, weight, q_norm, k_norm, positions, cos_sin,
+                                slots, q, k_cache, v_cache)
+    return q
+
+
+def rmsnorm_f32(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """bf16(rmsnorm(x) * weight) for r32 rows (fp32 in the lane order of r32_positions);
+    sid.kernels.rmsnorm.rmsnorm's bits on the same values."""
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    load_ext().rmsnorm_f32(x, weight, out, eps)
+    return out
+
+
+def decode_chain_supported(rows: int, hidden: int, intermediate: int, q_size: int,
+                           head_dim: int) -> bool:
+    """Whether the fused decode chain serves this model shape (rows: decode batch size)."""
+    return (1 <= rows <= DECODE_CHAIN_MAX_ROWS and hidden in (512, 1024) and head_dim == 128
+            and intermediate % 24 == 0 and intermediate % 256 == 0
+            and q_size % 256 == 0 and q_size <= 4096 and intermediate <= 4096 and hidden % 128 == 0)
+
+
+# Decode batches up to this many rows take the fused chain; larger ones the split-K /
+# tiled projections with separate norms (identical bits either way).
+DECODE_CHAIN_MAX_ROWS = 256

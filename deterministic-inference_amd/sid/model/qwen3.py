@@ -18,8 +18,10 @@ from sid.kernels.extend_attention import extend_attention_fwd
 from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_supported,
                                             linear_partials, linear_sample, linear_silu_mul,
                                             linear_silu_mul_preferred)
-from sid.kernels.ops import (argmax_rows, embedding, fused_add_rmsnorm_partials, gather_rows, qkv_post,
-                             silu_mul, silu_mul_partials)
+from sid.kernels.ops import (argmax_rows, decode_chain_supported, embedding,
+                             fused_add_rmsnorm_partials, gather_rows, linear_residual, qkv_post,
+                             rmsnorm_f32, rmsnorm_linear_silu_mul, rmsnorm_qkv_post, silu_mul,
+                             silu_mul_partials)
 from sid.kernels.rmsnorm import fused_add_rmsnorm, rmsnorm
 from sid.kernels.rope import RotaryEmbedding
 
@@ -56,6 +58,9 @@ class Qwen3Model:
         # forward); False keeps the op-by-op Python driver below (identical bits).
         self.native_extend = True
         self._native = None
+        # Decode batches run the fused five-launch layer chain (identical bits); False keeps
+        # the split-K projections with separate norm kernels.
+        self.decode_chain = True
 
     def set_batch_invariant(self, enabled: bool) -> None:
         # Every GEMM here already reduces in an M-independent order (see
@@ -72,6 +77,14 @@ class Qwen3Model:
         proj = linear_partials(x, lw["qkv"]) if split else linear(x, lw["qkv"])
         q = qkv_post(proj, lw["q_norm"], lw["k_norm"], cfg.rms_norm_eps, fb.positions,
                      self.rope.cos_sin, fb.out_slots, k_pool, v_pool, cfg.num_q_heads)
+        return self._attend(layer_idx, q, fb, kv_cache, decode_attn, decode_backend)
+
+    def _attend(self, layer_idx: int, q: torch.Tensor, fb: ForwardBatch, kv_cache, decode_attn,
+                decode_backend: str) -> torch.Tensor:
+        """Attention of q [T, HQ, D] over the pool (this step's K/V already written)."""
+        cfg = self.cfg
+        t = q.shape[0]
+        k_pool, v_pool = kv_cache.layer(layer_idx)
         if fb.mode == ForwardMode.DECODE and decode_backend == "hip":
             o = decode_attn.forward(q, k_pool, v_pool, fb.kv_indptr, fb.kv_indices, fb.seq_lens,
                                     fb.max_seq_len, self.sm_scale, invariant=fb.invariant,
@@ -80,11 +93,35 @@ class Qwen3Model:
         else:
             qo = fb.qo_indptr
             if qo is None:  # decode through the extend kernel: one query per request
-                qo = torch.arange(t + 1, dtype=torch.int32, device=x.device)
+                qo = torch.arange(t + 1, dtype=torch.int32, device=q.device)
             o = extend_attention_fwd(q, k_pool, v_pool, qo, fb.kv_indptr, fb.kv_indices,
                                      max(fb.max_extend_len, 1), self.sm_scale,
                                      max_kv_len=fb.max_kv_len or fb.max_seq_len or None)
         return o.view(t, cfg.q_size)
+
+    def _decode_chain(self, fb: ForwardBatch, kv_cache, decode_attn,
+                      decode_backend: str) -> torch.Tensor:
+        """The decoder stack of a decode batch as five fused launches per layer
+        (csrc/decode_chain.hip); returns the final-normed hidden rows. Same bits as the
+        unfused sequence in forward()."""
+        cfg = self.cfg
+        eps = cfg.rms_norm_eps
+        layers = self.w["layers"]
+        residual = embedding(fb.input_ids, self.w["embed"])
+        r32 = torch.empty(residual.shape, dtype=torch.float32, device=residual.device)
+        src = residual  # layer 0 normalises the embedding rows themselves
+        for i in range(cfg.num_layers):
+            lw = layers[i]
+            k_pool, v_pool = kv_cache.layer(i)
+            q = rmsnorm_qkv_post(src, lw["input_ln"], eps, lw["qkv"], lw["q_norm"], lw["k_norm"],
+                                 fb.positions, self.rope.cos_sin, fb.out_slots, k_pool, v_pool,
+                                 cfg.num_q_heads)
+            o = self._attend(i, q, fb, kv_cache, decode_attn, decode_backend)
+            linear_residual(o, lw["o"], residual, r32)
+            act = rmsnorm_linear_silu_mul(r32, lw["post_ln"], eps, lw["gate_up"])
+            linear_residual(act, lw["down"], residual, r32)
+            src = r32
+        return rmsnorm_f32(r32, self.w["norm"], eps)
 
     @torch.inference_mode()
     def forward(self, fb: ForwardBatch, kv_cache, decode_attn,
@@ -113,6 +150,10 @@ class Qwen3Model:
         split_gu = split_k_preferred(t, 2 * cfg.intermediate_size)
         split_down = split_k_preferred(t, h)
         decode_attn.reset_plan()
+        if self.decode_chain and fb.mode == ForwardMode.DECODE and decode_chain_supported(
+                t, h, cfg.intermediate_size, cfg.q_size, cfg.head_dim):
+            x = self._decode_chain(fb, kv_cache, decode_attn, decode_backend)
+            return self._head(x, fb, greedy, sample, with_logits)
         residual = embedding(fb.input_ids, self.w["embed"])
         x = rmsnorm(residual, layers[0]["input_ln"], eps)
         for i in range(cfg.num_layers):
@@ -135,6 +176,11 @@ class Qwen3Model:
                                                          residual, next_w, eps)
             else:
                 x, residual = fused_add_rmsnorm(linear(act, lw["down"]), residual, next_w, eps)
+        return self._head(x, fb, greedy, sample, with_logits)
+
+    def _head(self, x: torch.Tensor, fb: ForwardBatch, greedy: bool, sample: bool,
+              with_logits: bool):
+        """lm_head (tied) on the sampled rows of the final-normed hidden states x."""
         rows = x if fb.sample_indices is None else gather_rows(x, fb.sample_indices)
         if sample:  # the sampler fused into the lm_head (rows without top-k / top-p)
             r = rows.shape[0]

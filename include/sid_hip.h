@@ -274,6 +274,56 @@ int sid_qkv_post(const void* qkv, const float* partials, int nchunks, int64_t nu
                  void* v_cache, int64_t num_slots, void* stream);
 
 /*
+ * Decode-step chain: the projections of a Qwen3 layer with their neighbours
+ * fused in, for decode-sized M (sid/model/qwen3.py:43-86 for one token per
+ * request). Each output is bit-identical to the unfused sequence of the
+ * entry points above (same reduction orders), so they are a speed choice.
+ *
+ * sid_linear_residual: y = x w^T (x bf16 [M, K] with row stride ldx, w bf16
+ * [N, K]), then r = residual + bf16(y) in fp32, residual = bf16(r) (bf16
+ * [M, N], in place) and r32 = r (fp32 [M, N]). Replaces self.o_proj /
+ * self.down_proj + fused_add_rmsnorm's residual half (sid/model/qwen3.py:80,
+ * 86; sid/kernels/rmsnorm.py:27-42); r32 is the value that add-norm
+ * normalises. N a multiple of 128; K in {1024, 2048, 3072, 4096}.
+ */
+int sid_linear_residual(const void* x, int64_t ldx, const void* w, void* residual, float* r32,
+                        int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
+ * sid_rmsnorm_linear_silu_mul: out = silu(g) * u (sid_linear_silu_mul's bits)
+ * of x = bf16(rmsnorm(src) * norm_w), src fp32 [M, hidden] (src_fp32 != 0:
+ * an r32 from sid_linear_residual) or bf16; w = [gate rows | up rows]
+ * bf16 [2I, hidden]; out bf16 [M, I]. Replaces the rmsnorm half of
+ * fused_add_rmsnorm + gate_up_proj + silu * up (sid/model/qwen3.py:84-85).
+ * hidden in {512, 1024}; I a multiple of 24.
+ */
+int sid_rmsnorm_linear_silu_mul(const void* src, int src_fp32, const void* norm_w, float eps,
+                                const void* w, void* out, int64_t m, int64_t hidden,
+                                int64_t inter, void* stream);
+
+/*
+ * sid_rmsnorm_qkv_post: sid_qkv_post over the projection of
+ * x = bf16(rmsnorm(src) * norm_w) by w_qkv bf16 [(HQ + 2 HKV) D, hidden]
+ * (src as above). Replaces the input rmsnorm / fused_add_rmsnorm + qkv_proj +
+ * q/k-norm + RoPE + reshape_and_cache (sid/model/qwen3.py:49-61, 99-106).
+ * hidden in {512, 1024}; D must be 128.
+ */
+int sid_rmsnorm_qkv_post(const void* src, int src_fp32, const void* norm_w, float eps,
+                         const void* w_qkv, int64_t m, int64_t hidden, int num_q_heads,
+                         int num_kv_heads, int head_dim, const void* q_norm, const void* k_norm,
+                         const int64_t* positions, const float* cos_sin, int64_t max_positions,
+                         const int64_t* slots, void* q_out, void* k_cache, void* v_cache,
+                         int64_t num_slots, void* stream);
+
+/*
+ * sid_rmsnorm_f32: out = bf16(rmsnorm(x) * w) for fp32 rows x [rows, hidden]
+ * (the final norm of the chain, sid/model/qwen3.py:111, on an r32); the bits
+ * of sid_rmsnorm on the same values. hidden in {512, 1024, 2048}.
+ */
+int sid_rmsnorm_f32(const float* x, const void* w, void* out, int64_t rows, int hidden,
+                    float eps, void* stream);
+
+/*
  * out[i] = table[idx[i]] for bf16 rows of row_elems elements (row_elems a
  * multiple of 8). Indices outside [0, table_rows) produce a zero row.
  * Used for the embedding lookup (sid/model/qwen3.py:93) and the sampled-row
