@@ -54,54 +54,55 @@ __device__ __forceinline__ void xcd_tile(int id, int ntiles, int R, int& tile, i
   }
 }
 
-// ---- MFMA operand tiles ---------------------------------------------------------------------
+// ---- MFMA operands ------------------------------------------------------------------------
 //
-// The canonical operand layout puts row r, elements 32 s + 8 g .. +7 of a chunk in lane
-// r + 16 g of k-step register s. Loaded straight from memory that is 16 rows x 64 bytes per
-// instruction with neighbouring lanes in different rows, which the memory pipeline serves
-// poorly (measured on MI355X: a 4 MB projection 2x slower than whole-line reads). So a
-// 16-row x 256-element chunk tile is loaded with neighbouring lanes on neighbouring 16-byte
-// pieces (instruction i: rows 2i, 2i + 1, 512 bytes each), and each wave transposes its own
-// tiles through a private 8 KB LDS scratch: the pieces are stored XOR-swizzled
-// (piece c of row r at slot c ^ (r & 15)) so both the stores and the fragment reads are
-// free of bank conflicts. Same values in the same registers as the direct load.
-struct Tile {
-  u32x4_v v[8];
-};
+// The canonical operand layout puts row r, elements 32 s + 8 g .. +7 of a 256-wide chunk in
+// lane r + 16 g of k-step register s. Read straight from a row-major matrix that is 16 rows
+// x 64 bytes per instruction with neighbouring lanes in different rows, which the memory
+// pipeline serves at about half the rate of whole-line reads (measured on MI355X). So:
+//
+// * Weights are used in a fragment-packed copy (made once at load time, see
+//   sid_pack_decode_weights): for 16-row block b and chunk c, the 8 KB of its fragments are
+//   stored in register order, [b][c][s][lane][8], and a wave loads its operand with eight
+//   contiguous 1 KB reads straight into registers.
+// * Activation tiles (16 rows x one chunk, 8 KB) are staged by each wave in a private LDS
+//   region with global_load_lds (1 KB per instruction, the 16-byte pieces XOR-swizzled:
+//   piece c of row r at slot c ^ (r & 15)) and read back as fragments without bank
+//   conflicts.
+// Same values in the same registers as the direct loads, so the same bits.
+__device__ __forceinline__ void packed_load(bf16x8_v (&f)[NSTEP], const bf16_t* __restrict__ wp,
+                                            int64_t block, int c, int nch, int lane) {
+  const bf16_t* p = wp + ((block * nch + c) * NSTEP) * 512 + 8 * lane;
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) f[s] = ld_frag(p + 512 * s);
+}
 
-// Issue the loads of a tile; row_ptr(i) (i < 16) gives row i's first element of the chunk.
-template <typename RowPtr>
-__device__ __forceinline__ void tile_load_rows(Tile& t, RowPtr row_ptr, int lane) {
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Stage rows row0 .. row0 + 15 (rows past `last` clamped to it; the caller drops their
+// results), elements k0 .. k0 + 255, of a row-major bf16 matrix into the wave's 8 KB region.
+__device__ __forceinline__ void stage_tile(char* region, const bf16_t* __restrict__ p, int64_t ld,
+                                           int row0, int last, int64_t k0, int lane) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const bf16_t* p = row_ptr(2 * i + (lane >> 5));
-    t.v[i] = *reinterpret_cast<const u32x4_v*>(p + 8 * (lane & 31));
+    const int piece = 64 * i + lane;
+    const int row = piece >> 5;
+    const int c = (piece & 31) ^ (row & 15);
+    const bf16_t* g = p + static_cast<int64_t>(min(row0 + row, last)) * ld + k0 + 8 * c;
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(region + 1024 * i), 16, 0, 0);
   }
 }
 
-// Rows row0 .. row0 + 15 of a matrix with row stride ld (rows past `last` clamped to it; the
-// caller drops their results), elements k0 .. k0 + 255.
-__device__ __forceinline__ void tile_load(Tile& t, const bf16_t* __restrict__ p, int64_t ld,
-                                          int row0, int last, int64_t k0, int lane) {
-  tile_load_rows(t, [&](int i) { return p + static_cast<int64_t>(min(row0 + i, last)) * ld + k0; },
-                 lane);
-}
-
-// Tile -> the 8 k-step fragments, through the wave's LDS scratch (8 KB). LDS operations of a
-// wave complete in order, so a scratch can be reused for the next tile right away.
-__device__ __forceinline__ void tile_frags(const Tile& t, char* scratch, bf16x8_v (&f)[NSTEP],
-                                           int lane) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 2 * i + (lane >> 5);
-    *reinterpret_cast<u32x4_v*>(scratch + row * 512 + 16 * ((lane & 31) ^ (row & 15))) = t.v[i];
-  }
+__device__ __forceinline__ void staged_frags(bf16x8_v (&f)[NSTEP], const char* region, int lane) {
   const int r = lane & 15;
   const int g = lane >> 4;
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s)
-    f[s] = *reinterpret_cast<const bf16x8_v*>(scratch + r * 512 + 16 * ((4 * s + g) ^ r));
+    f[s] = *reinterpret_cast<const bf16x8_v*>(region + r * 512 + 16 * ((4 * s + g) ^ r));
 }
+
+// Waits until this wave's outstanding global loads (global_load_lds included) are done.
+__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---- the fp32 residual sum r32 -------------------------------------------------------------
 //
@@ -188,32 +189,28 @@ __device__ __forceinline__ bf16x8_v a_frag(const char* tile, int row, int c, int
 
 // ---- projection + residual add ------------------------------------------------------------
 //
-// y = x w^T for a 16-row x 16-column tile over K = 256 NCH: wave c loads chunk c of the x
-// rows and of the w rows (all loads issued before the MFMAs) and accumulates it from zero;
-// the chunk sums meet in LDS and are folded c0 + c1 + ... in order; then
-// r = residual + bf16(y) (fp32), residual = bf16(r), r32 = r (in r32 order).
+// y = x w^T for a 16-row x 16-column tile over K = 256 NCH: wave c stages chunk c of the x
+// rows and loads chunk c of the packed w block, then accumulates it from zero; the chunk
+// sums meet in LDS and are folded c0 + c1 + ... in order; then r = residual + bf16(y)
+// (fp32), residual = bf16(r), r32 = r (in r32 order).
 template <int NCH>
 __global__ void __launch_bounds__(NCH * 64) linear_residual_kernel(
-    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
+    const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ wpk,
     bf16_t* __restrict__ residual, float* __restrict__ r32, int M, int N, int R) {
-  constexpr int64_t K = static_cast<int64_t>(NCH) * KC;
   constexpr int SS = 17;  // LDS row stride of a chunk tile (floats)
   __shared__ float sacc[NCH][16 * SS];
-  __shared__ __align__(16) char scratch[NCH][8192];
+  __shared__ __align__(16) char stage[NCH][8192];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   int tile, rg;
   xcd_tile(blockIdx.x, N / 16, R, tile, rg);
   const int n0 = tile * 16;
   const int m0 = rg * 16;
-  const int64_t k0 = static_cast<int64_t>(wave) * KC;
-  Tile xt, wt;
-  tile_load(xt, x, ldx, m0, M - 1, k0, lane);  // rows >= M clamped, their sums dropped
-  tile_load(wt, w, K, n0, N - 1, k0, lane);
-  __builtin_amdgcn_sched_barrier(0);
+  stage_tile(stage[wave], x, ldx, m0, M - 1, static_cast<int64_t>(wave) * KC, lane);
   bf16x8_v xf[NSTEP], wf[NSTEP];
-  tile_frags(xt, scratch[wave], xf, lane);
-  tile_frags(wt, scratch[wave], wf, lane);
+  packed_load(wf, wpk, tile, wave, NCH, lane);
+  wait_loads();
+  staged_frags(xf, stage[wave], lane);
   f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[s], wf[s], acc, 0, 0, 0);
@@ -256,11 +253,8 @@ __global__ void __launch_bounds__(2 * PL * NB * 64) norm_silu_kernel(
   constexpr int ROWS = 16 * MBS;
   constexpr int SS = 16 * NB + 1;    // LDS row stride of a chunk-sum tile (floats)
   constexpr int RPW = (ROWS + NW - 1) / NW;
-  constexpr int SCRATCH = NW * 8192;
-  constexpr int SACC = NCH * ROWS * SS * 4;
   __shared__ __align__(16) char sx[ROWS * 2 * H];
-  __shared__ __align__(16) char spool[SCRATCH > SACC ? SCRATCH : SACC];
-  float (*sacc)[ROWS * SS] = reinterpret_cast<float (*)[ROWS * SS]>(spool);
+  __shared__ float sacc[NCH][ROWS * SS];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
@@ -281,19 +275,14 @@ __global__ void __launch_bounds__(2 * PL * NB * 64) norm_silu_kernel(
     const int row = wave + NW * q;
     if (row < ROWS) norm_row_load<PL, F32>(src, min(m0 + row, M - 1), lane, v[q]);
   }
-  Tile wt;
-  tile_load_rows(wt, [&](int i) {
-    const int64_t wr = i < 8 ? j0 + 8 * nb + i : inter + j0 + 8 * nb + (i - 8);
-    return w + wr * H + static_cast<int64_t>(c) * KC;
-  }, lane);
+  bf16x8_v wf[NSTEP];
+  packed_load(wf, w, static_cast<int64_t>(tile) * NB + nb, c, NCH, lane);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int q = 0; q < RPW; ++q) {
     const int row = wave + NW * q;
     if (row < ROWS) norm_row_store<PL>(v[q], lane, nw, eps, sx, row);
   }
-  bf16x8_v wf[NSTEP];
-  tile_frags(wt, spool + wave * 8192, wf, lane);
   __syncthreads();
   f32x4_v acc[MBS];
 #pragma unroll
@@ -305,7 +294,6 @@ __global__ void __launch_bounds__(2 * PL * NB * 64) norm_silu_kernel(
       acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_frag<PL>(sx, 16 * mb + r, c, s, g),
                                                         wf[s], acc[mb], 0, 0, 0);
   }
-  __syncthreads();  // every wave is done with its scratch before the chunk sums reuse it
 #pragma unroll
   for (int mb = 0; mb < MBS; ++mb) {
 #pragma unroll
@@ -359,7 +347,6 @@ __global__ void __launch_bounds__(512) norm_qkv_kernel(
   constexpr int H = 512 * PL;
   constexpr int YS = QD + 4;
   __shared__ __align__(16) char sx[16 * 2 * H];
-  __shared__ __align__(16) char scratch[8][8192];
   __shared__ __align__(16) float sy[16 * YS];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -378,23 +365,25 @@ __global__ void __launch_bounds__(512) norm_qkv_kernel(
   const bool valid = threadIdx.x < 256 && m0 + row < M;
   const bool is_v = head >= num_q_heads + num_kv_heads;
   const bool is_q = head < num_q_heads;
-  int64_t slot = -1;
-  QkRopeIn in;
+  int64_t slot = -1, pos = -1;
   if (threadIdx.x < 256) {
     slot = slots[t];
-    if (!is_v) qk_rope_load(in, j, is_q ? q_norm : k_norm, positions[t], cos_sin, max_positions);
+    pos = positions[t];
   }
   uint4 nw[PL];
   norm_w_load<PL>(norm_w, lane, nw);
   float v[2][PL][8];
 #pragma unroll
   for (int q = 0; q < 2; ++q) norm_row_load<PL, F32>(src, min(m0 + wave + 8 * q, M - 1), lane, v[q]);
-  Tile wt[NCH];
-  {
-    const bf16_t* wp = w + static_cast<int64_t>(head * QD + 16 * wave) * H;
+  bf16x8_v wf[NCH][NSTEP];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) tile_load(wt[c], wp, H, 0, 15, static_cast<int64_t>(c) * KC, lane);
-  }
+  for (int c = 0; c < NCH; ++c) packed_load(wf[c], w, static_cast<int64_t>(head) * 8 + wave, c, NCH, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  // The rotary table row depends on the position: its loads go out once that one is back,
+  // with everything issued after it still in flight.
+  QkRopeIn in;
+  if (threadIdx.x < 256 && !is_v)
+    qk_rope_load(in, j, is_q ? q_norm : k_norm, pos, cos_sin, max_positions);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int q = 0; q < 2; ++q) norm_row_store<PL>(v[q], lane, nw, eps, sx, wave + 8 * q);
@@ -402,12 +391,10 @@ __global__ void __launch_bounds__(512) norm_qkv_kernel(
   f32x4_v tot;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    bf16x8_v wf[NSTEP];
-    tile_frags(wt[c], scratch[wave], wf, lane);
     f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_frag<PL>(sx, r, c, s, g), wf[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_frag<PL>(sx, r, c, s, g), wf[c][s], acc, 0, 0, 0);
     if (c == 0) {
       tot = acc;
     } else {
@@ -435,6 +422,28 @@ __global__ void __launch_bounds__(512) norm_qkv_kernel(
   } else if (slot_ok) {
     k_cache[slot * kv_row + (head - num_q_heads) * 16 + j] = store8(o);
   }
+}
+
+// ---- weight packing ------------------------------------------------------------------------
+//
+// packed[b][c][s][lane] (16 bytes each) = row(b, lane & 15), elements 256 c + 32 s + 8 (lane >> 4)
+// .. +7 of w, where row(b, r) = 16 b + r, or for a gate_up weight [gate rows | up rows] of
+// `inter` rows each: gate row 8 b + r for r < 8, up row inter + 8 b + r - 8 (one 16-byte piece
+// per thread).
+__global__ void __launch_bounds__(256) pack_weight_kernel(const uint4* __restrict__ w,
+                                                          uint4* __restrict__ packed, int64_t n,
+                                                          int64_t k, int64_t inter) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t nch = k / KC;
+  if (i >= n * k / 8) return;
+  const int lane = static_cast<int>(i & 63);
+  const int s = static_cast<int>((i >> 6) & 7);
+  const int64_t bc = i >> 9;
+  const int64_t c = bc % nch;
+  const int64_t b = bc / nch;
+  const int r = lane & 15;
+  const int64_t row = inter > 0 ? (r < 8 ? 8 * b + r : inter + 8 * b + (r - 8)) : 16 * b + r;
+  packed[i] = w[(row * k + c * KC + 32 * s + 8 * (lane >> 4)) / 8];
 }
 
 // ---- RMSNorm of fp32 rows (the final norm of the chain) ------------------------------------
@@ -472,7 +481,7 @@ extern "C" int sid_linear_residual(const void* x, int64_t ldx, const void* w, vo
   SID_REQUIRE(n % 512 == 0, "linear_residual: N=%lld must be a multiple of 512", (long long)n);
   SID_REQUIRE(k == 1024 || k == 2048 || k == 3072 || k == 4096,
               "linear_residual: K=%lld must be 1024, 2048, 3072 or 4096", (long long)k);
-  SID_REQUIRE(ldx >= k && ldx % 64 == 0, "linear_residual: row stride %lld must be >= K and a multiple of 64", (long long)ldx);
+  SID_REQUIRE(ldx >= k && ldx % 8 == 0, "linear_residual: row stride %lld must be >= K and a multiple of 8", (long long)ldx);
   SID_REQUIRE(aligned16(x) && aligned16(w), "linear_residual: operands must be 16-byte aligned");
   const int64_t R = (m + 15) / 16;
   SID_REQUIRE(R * (n / 16) < (1ll << 31), "linear_residual: too large");
@@ -567,6 +576,22 @@ extern "C" int sid_rmsnorm_qkv_post(const void* src, int src_fp32, const void* n
     if (src_fp32) go(norm_qkv_kernel<2, true>); else go(norm_qkv_kernel<2, false>);
   }
   return check_launch("rmsnorm_qkv_post");
+}
+
+extern "C" int sid_pack_decode_weight(const void* w, void* packed, int64_t n, int64_t k,
+                                      int gate_up, void* stream) {
+  SID_REQUIRE(n >= 0 && k >= 0, "pack_decode_weight: negative size");
+  if (n == 0 || k == 0) return SID_OK;
+  SID_REQUIRE(w && packed && w != packed, "pack_decode_weight: null or aliased pointer");
+  SID_REQUIRE(k % KC == 0, "pack_decode_weight: K=%lld must be a multiple of 256", (long long)k);
+  SID_REQUIRE(n % 16 == 0, "pack_decode_weight: N=%lld must be a multiple of 16", (long long)n);
+  SID_REQUIRE(aligned16(w) && aligned16(packed), "pack_decode_weight: misaligned operand");
+  const int64_t pieces = n * k / 8;
+  SID_REQUIRE((pieces + 255) / 256 < (1ll << 31), "pack_decode_weight: too large");
+  hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), (const uint4*)w, (uint4*)packed, n, k,
+                     gate_up ? n / 2 : int64_t(0));
+  return check_launch("pack_decode_weight");
 }
 
 extern "C" int sid_rmsnorm_f32(const float* x, const void* w, void* out, int64_t rows,

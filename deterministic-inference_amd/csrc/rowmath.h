@@ -66,12 +66,6 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
   o2 = fmaf(x2, c, x1 * s);
 }
 
-// One q or k head of the fused QKV epilogue, held by an aligned group of 16 lanes (lane j:
-// dims 8j..8j+7 of the head, head_dim 128): per-head RMSNorm with weight w (rmsnorm's lane
-// layout for hidden 128: sequential fmaf over the lane's 8 dims, xor butterfly over the 16
-// lanes), rounded to bf16, then NeoX RoPE at `pos` (the rotate-half partner of lane j is
-// lane j ^ 8, one DPP row_ror:8 away) from the fp32 [cos(64) | sin(64)] table row; a
-// position outside the table leaves the normed values. Every lane of the 16 must be active.
 // group_sum(v, 16) with the same bits, all in DPP (see group_sum64).
 __device__ __forceinline__ float group_sum16(float v) {
   v += dpp<DPP_QUAD_XOR1>(v);
@@ -83,9 +77,12 @@ __device__ __forceinline__ float group_sum16(float v) {
 
 // The per-lane operands of qk_head_norm_rope that come from memory, so a kernel can load
 // them ahead of the values: the norm weights of the lane's 8 dims, and cos / sin of their
-// rotary indices at the row's position (rot false: position outside the table).
+// rotary indices at the row's position (rot false: position outside the table). Loads
+// only: the values are converted where they are used, so waiting for them never waits for
+// loads issued after these.
 struct QkRopeIn {
-  float w[8], c[8], s[8];
+  uint4 w;            // 8 bf16 norm weights
+  float4 c[2], s[2];  // cos / sin of the lane's 8 rotary indices
   bool rot;
 };
 
@@ -93,17 +90,13 @@ __device__ __forceinline__ void qk_rope_load(QkRopeIn& in, int j, const uint4* _
                                              int64_t pos, const float* __restrict__ cos_sin,
                                              int64_t max_positions) {
   constexpr int D = 128;
-  load8(w[j], in.w);
+  in.w = w[j];
   in.rot = pos >= 0 && pos < max_positions;
   const float* cs = cos_sin + (in.rot ? pos : 0) * D + 8 * (j & 7);
-  const float4 c0 = *reinterpret_cast<const float4*>(cs);
-  const float4 c1 = *reinterpret_cast<const float4*>(cs + 4);
-  const float4 s0 = *reinterpret_cast<const float4*>(cs + D / 2);
-  const float4 s1 = *reinterpret_cast<const float4*>(cs + D / 2 + 4);
-  in.c[0] = c0.x; in.c[1] = c0.y; in.c[2] = c0.z; in.c[3] = c0.w;
-  in.c[4] = c1.x; in.c[5] = c1.y; in.c[6] = c1.z; in.c[7] = c1.w;
-  in.s[0] = s0.x; in.s[1] = s0.y; in.s[2] = s0.z; in.s[3] = s0.w;
-  in.s[4] = s1.x; in.s[5] = s1.y; in.s[6] = s1.z; in.s[7] = s1.w;
+  in.c[0] = *reinterpret_cast<const float4*>(cs);
+  in.c[1] = *reinterpret_cast<const float4*>(cs + 4);
+  in.s[0] = *reinterpret_cast<const float4*>(cs + D / 2);
+  in.s[1] = *reinterpret_cast<const float4*>(cs + D / 2 + 4);
 }
 
 // One q or k head of the fused QKV epilogue, held by an aligned group of 16 lanes (lane j:
@@ -115,9 +108,14 @@ __device__ __forceinline__ void qk_rope_load(QkRopeIn& in, int j, const uint4* _
 __device__ __forceinline__ void qk_head_norm_rope(const float (&v)[8], int j, const QkRopeIn& in,
                                                   float eps, float (&o)[8]) {
   constexpr int D = 128;
-  float y[8];
+  float wf[8], y[8];
+  load8(in.w, wf);
+  const float c[8] = {in.c[0].x, in.c[0].y, in.c[0].z, in.c[0].w,
+                      in.c[1].x, in.c[1].y, in.c[1].z, in.c[1].w};
+  const float sn[8] = {in.s[0].x, in.s[0].y, in.s[0].z, in.s[0].w,
+                       in.s[1].x, in.s[1].y, in.s[1].z, in.s[1].w};
   const float ss = group_sum16(sumsq8(v, 0.0f));
-  rms_apply8(v, rms_rstd(ss, D, eps), in.w, y);
+  rms_apply8(v, rms_rstd(ss, D, eps), wf, y);
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = round_bf16(y[e]);
   const bool first_half = j < 8;
@@ -126,10 +124,10 @@ __device__ __forceinline__ void qk_head_norm_rope(const float (&v)[8], int j, co
     const float partner = dpp<DPP_ROW_ROR8>(y[e]);
     float o1, o2;
     if (first_half) {
-      rope_pair(y[e], partner, in.c[e], in.s[e], o1, o2);
+      rope_pair(y[e], partner, c[e], sn[e], o1, o2);
       o[e] = o1;
     } else {
-      rope_pair(partner, y[e], in.c[e], in.s[e], o1, o2);
+      rope_pair(partner, y[e], c[e], sn[e], o1, o2);
       o[e] = o2;
     }
     if (!in.rot) o[e] = y[e];

@@ -52,6 +52,7 @@ _SIGNATURES = {
     "sid_rmsnorm_qkv_post": [_vp, _i32, _vp, _f32, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp,
                              _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp],
     "sid_rmsnorm_f32": [_vp, _vp, _vp, _i64, _i32, _f32, _vp],
+    "sid_pack_decode_weight": [_vp, _vp, _i64, _i64, _i32, _vp],
 }
 EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace_bytes",
             "sid_linear_argmax_workspace_bytes", "sid_sample_workspace_bytes",
@@ -436,6 +437,14 @@ class NativeLib:
                    positions.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0], slots.data_ptr(),
                    q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
                    _stream(q_out))
+
+    def pack_decode_weight(self, w, packed, gate_up: bool) -> None:
+        """packed <- w [N, K] in the fragment-packed order of the decode-chain kernels."""
+        _gpu(w, "weight", torch.bfloat16)
+        _gpu(packed, "packed", torch.bfloat16)
+        _check(w.dim() == 2 and packed.shape == w.shape, "packed must have the weight's shape")
+        self._call("sid_pack_decode_weight", w.data_ptr(), packed.data_ptr(), w.shape[0],
+                   w.shape[1], int(gate_up), _stream(packed))
 
     def rmsnorm_f32(self, x, w, out, eps: float) -> None:
         """out <- bf16(rmsnorm(x) * w) for fp32 rows x (rmsnorm's bits)."""

@@ -87,18 +87,27 @@ def r32_positions(hidden: int) -> torch.Tensor:
     return (v >> 6) * 512 + (e >> 2) * 256 + 4 * (v & 63) + (e & 3)
 
 
-def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+def pack_decode_weight(weight: torch.Tensor, gate_up: bool = False) -> torch.Tensor:
+    """The fragment-packed copy of a [N, K] projection weight that the decode-chain kernels
+    read (same shape and values, another order; gate_up: [gate rows | up rows])."""
+    out = torch.empty_like(weight)
+    load_ext().pack_decode_weight(weight.contiguous(), out, gate_up)
+    return out
+
+
+def linear_residual(x: torch.Tensor, packed: torch.Tensor, residual: torch.Tensor,
                     r32: torch.Tensor) -> None:
     """In place: r = residual + bf16(x @ weight^T) (fp32), residual = bf16(r), r32 = r stored
     in the RMSNorm lane order (r32_positions): the projection plus the residual half of
-    fused_add_rmsnorm (sid/kernels/rmsnorm.py:27-42)."""
-    load_ext().linear_residual(x, weight, residual, r32)
+    fused_add_rmsnorm (sid/kernels/rmsnorm.py:27-42). packed = pack_decode_weight(weight)."""
+    load_ext().linear_residual(x, packed, residual, r32)
 
 
 def rmsnorm_linear_silu_mul(src: torch.Tensor, norm_w: torch.Tensor, eps: float,
                             weight: torch.Tensor) -> torch.Tensor:
-    """silu(gate) * up of bf16(rmsnorm(src) * norm_w) @ weight^T; src an r32 (fp32, lane
-    order) or bf16 rows in column order, [T, H]."""
+    """silu(gate) * up of bf16(rmsnorm(src) * norm_w) @ gate_up^T; src an r32 (fp32, lane
+    order) or bf16 rows in column order, [T, H]; weight = pack_decode_weight(gate_up,
+    gate_up=True)."""
     out = torch.empty(src.shape[0], weight.shape[0] // 2, dtype=torch.bfloat16, device=src.device)
     load_ext().rmsnorm_linear_silu_mul(src, norm_w, eps, weight, out)
     return out
@@ -108,7 +117,8 @@ def rmsnorm_qkv_post(src: torch.Tensor, norm_w: torch.Tensor, eps: float, weight
                      q_norm: torch.Tensor, k_norm: torch.Tensor, positions: torch.Tensor,
                      cos_sin: torch.Tensor, slots: torch.Tensor, k_cache: torch.Tensor,
                      v_cache: torch.Tensor, num_q_heads: int) -> torch.Tensor:
-    """qkv_post of the qkv projection of bf16(rmsnorm(src) * norm_w); returns q [T, HQ, D]."""
+    """qkv_post of the qkv projection of bf16(rmsnorm(src) * norm_w); returns q [T, HQ, D].
+    weight = pack_decode_weight(qkv)."""
     d = k_cache.shape[2]
     q = torch.empty(src.shape[0], num_q_heads, d, dtype=torch.bfloat16, device=src.device)
     load_ext().rmsnorm_qkv_post(src, norm_w, eps, weight, q_norm, k_norm, positions, cos_sin,

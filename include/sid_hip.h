@@ -279,8 +279,11 @@ int sid_qkv_post(const void* qkv, const float* partials, int nchunks, int64_t nu
  * request). Each output is bit-identical to the unfused sequence of the
  * entry points above (same reduction orders), so they are a speed choice.
  *
- * sid_linear_residual: y = x w^T (x bf16 [M, K] with row stride ldx, w bf16
- * [N, K]), then r = residual + bf16(y) in fp32, residual = bf16(r) (bf16
+ * The weights of these entry points are in the fragment-packed order made by
+ * sid_pack_decode_weight (same size as the [N, K] weight).
+ *
+ * sid_linear_residual: y = x w^T (x bf16 [M, K] with row stride ldx, w the
+ * packed bf16 [N, K]), then r = residual + bf16(y) in fp32, residual = bf16(r) (bf16
  * [M, N], in place) and r32 = r (fp32 [M, N]). Replaces self.o_proj /
  * self.down_proj + fused_add_rmsnorm's residual half (sid/model/qwen3.py:80,
  * 86; sid/kernels/rmsnorm.py:27-42); r32 is the value that add-norm
@@ -293,7 +296,7 @@ int sid_linear_residual(const void* x, int64_t ldx, const void* w, void* residua
  * sid_rmsnorm_linear_silu_mul: out = silu(g) * u (sid_linear_silu_mul's bits)
  * of x = bf16(rmsnorm(src) * norm_w), src fp32 [M, hidden] (src_fp32 != 0:
  * an r32 from sid_linear_residual) or bf16; w = [gate rows | up rows]
- * bf16 [2I, hidden]; out bf16 [M, I]. Replaces the rmsnorm half of
+ * bf16 [2I, hidden], packed with gate_up = 1; out bf16 [M, I]. Replaces the rmsnorm half of
  * fused_add_rmsnorm + gate_up_proj + silu * up (sid/model/qwen3.py:84-85).
  * hidden in {512, 1024}; I a multiple of 24.
  */
@@ -304,7 +307,7 @@ int sid_rmsnorm_linear_silu_mul(const void* src, int src_fp32, const void* norm_
 /*
  * sid_rmsnorm_qkv_post: sid_qkv_post over the projection of
  * x = bf16(rmsnorm(src) * norm_w) by w_qkv bf16 [(HQ + 2 HKV) D, hidden]
- * (src as above). Replaces the input rmsnorm / fused_add_rmsnorm + qkv_proj +
+ * (packed; src as above). Replaces the input rmsnorm / fused_add_rmsnorm + qkv_proj +
  * q/k-norm + RoPE + reshape_and_cache (sid/model/qwen3.py:49-61, 99-106).
  * hidden in {512, 1024}; D must be 128.
  */
@@ -322,6 +325,17 @@ int sid_rmsnorm_qkv_post(const void* src, int src_fp32, const void* norm_w, floa
  */
 int sid_rmsnorm_f32(const float* x, const void* w, void* out, int64_t rows, int hidden,
                     float eps, void* stream);
+
+/*
+ * sid_pack_decode_weight: packed = w (bf16 [N, K]) in fragment order: for
+ * 16-row block b, 256-wide chunk c, k-step s < 8 and lane l < 64, the 8 bf16
+ * at ((b * K / 256 + c) * 8 + s) * 512 + 8 l are row(b, l % 16), columns
+ * 256 c + 32 s + 8 (l / 16) .. +7, with row(b, r) = 16 b + r, or, for a
+ * gate_up weight (gate_up != 0, N = 2 I), gate row 8 b + r for r < 8 and up
+ * row I + 8 b + r - 8. N a multiple of 16, K of 256. Run once at load time.
+ */
+int sid_pack_decode_weight(const void* w, void* packed, int64_t n, int64_t k, int gate_up,
+                           void* stream);
 
 /*
  * out[i] = table[idx[i]] for bf16 rows of row_elems elements (row_elems a

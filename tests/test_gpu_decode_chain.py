@@ -26,7 +26,7 @@ def _w(n, k, scale=0.03):
 @pytest.mark.parametrize("k", [2048, 3072])
 def test_linear_residual_matches_unfused(t, k):
     from sid.kernels.matmul_persistent import linear
-    from sid.kernels.ops import linear_residual, r32_positions, rmsnorm_f32
+    from sid.kernels.ops import linear_residual, pack_decode_weight, r32_positions, rmsnorm_f32
     from sid.kernels.rmsnorm import fused_add_rmsnorm
     inv = torch.argsort(r32_positions(H)).cuda()  # column order -> r32 order
     print(f"linear_residual t={t} k={k}", flush=True)
@@ -38,7 +38,7 @@ def test_linear_residual_matches_unfused(t, k):
     h0, r0 = fused_add_rmsnorm(linear(x, w), res.clone(), nw, 1e-6)
     r1 = res.clone()
     r32 = torch.full((t, H), float("nan"), device="cuda")
-    linear_residual(x, w, r1, r32)
+    linear_residual(x, pack_decode_weight(w), r1, r32)
     r32_raw = r32.clone()
     assert torch.equal(r1, r0)
     r32 = r32[:, r32_positions(H).cuda()]  # column order
@@ -54,7 +54,7 @@ def test_linear_residual_matches_unfused(t, k):
 @pytest.mark.parametrize("src_fp32", [True, False])
 def test_rmsnorm_linear_silu_mul_matches_unfused(t, src_fp32):
     from sid.kernels.matmul_persistent import linear_silu_mul
-    from sid.kernels.ops import rmsnorm_f32, rmsnorm_linear_silu_mul
+    from sid.kernels.ops import pack_decode_weight, rmsnorm_f32, rmsnorm_linear_silu_mul
     from sid.kernels.rmsnorm import rmsnorm
     print(f"rmsnorm_linear_silu_mul t={t} f32={src_fp32}", flush=True)
     torch.manual_seed(11 * t + src_fp32)
@@ -65,7 +65,7 @@ def test_rmsnorm_linear_silu_mul_matches_unfused(t, src_fp32):
     w = _w(6144, H, 0.05)
     x = rmsnorm_f32(src, nw, 1e-6) if src_fp32 else rmsnorm(src, nw, 1e-6)
     want = linear_silu_mul(x, w)
-    got = rmsnorm_linear_silu_mul(src, nw, 1e-6, w)
+    got = rmsnorm_linear_silu_mul(src, nw, 1e-6, pack_decode_weight(w, gate_up=True))
     assert torch.equal(got, want)
 
 
@@ -73,7 +73,7 @@ def test_rmsnorm_linear_silu_mul_matches_unfused(t, src_fp32):
 @pytest.mark.parametrize("src_fp32", [True, False])
 def test_rmsnorm_qkv_post_matches_unfused(t, src_fp32):
     from sid.kernels.matmul_persistent import linear
-    from sid.kernels.ops import qkv_post, rmsnorm_f32, rmsnorm_qkv_post
+    from sid.kernels.ops import pack_decode_weight, qkv_post, rmsnorm_f32, rmsnorm_qkv_post
     from sid.kernels.rmsnorm import rmsnorm
     from sid.kernels.rope import RotaryEmbedding
     print(f"rmsnorm_qkv_post t={t} f32={src_fp32}", flush=True)
@@ -98,19 +98,20 @@ def test_rmsnorm_qkv_post_matches_unfused(t, src_fp32):
     q0 = qkv_post(linear(x, w), qn, kn, 1e-6, pos, rope.cos_sin, slots, kc0, vc0, HQ)
     kc1 = torch.zeros_like(kc0)
     vc1 = torch.zeros_like(kc0)
-    q1 = rmsnorm_qkv_post(src, nw, 1e-6, w, qn, kn, pos, rope.cos_sin, slots, kc1, vc1, HQ)
+    q1 = rmsnorm_qkv_post(src, nw, 1e-6, pack_decode_weight(w), qn, kn, pos, rope.cos_sin, slots,
+                          kc1, vc1, HQ)
     assert torch.equal(q1, q0)
     assert torch.equal(kc1, kc0) and torch.equal(vc1, vc0)
 
 
 def test_decode_chain_rows_are_batch_invariant():
     """A row's chain outputs do not depend on the batch around it (M-invariance)."""
-    from sid.kernels.ops import linear_residual, rmsnorm_linear_silu_mul
+    from sid.kernels.ops import linear_residual, pack_decode_weight, rmsnorm_linear_silu_mul
     torch.manual_seed(3)
     big = torch.randn(200, 3072, device="cuda", dtype=torch.bfloat16)
-    w = _w(H, 3072)
+    w = pack_decode_weight(_w(H, 3072))
     res = torch.randn(200, H, device="cuda", dtype=torch.bfloat16)
-    wg = _w(6144, H, 0.05)
+    wg = pack_decode_weight(_w(6144, H, 0.05), gate_up=True)
     nw = (1 + 0.1 * torch.randn(H, device="cuda")).to(torch.bfloat16)
     r_all, f_all = res.clone(), torch.empty(200, H, device="cuda")
     linear_residual(big, w, r_all, f_all)
@@ -120,6 +121,22 @@ def test_decode_chain_rows_are_batch_invariant():
         linear_residual(big[lo:hi].contiguous(), w, r_part, f_part)
         assert torch.equal(r_part, r_all[lo:hi]) and torch.equal(f_part, f_all[lo:hi])
         assert torch.equal(rmsnorm_linear_silu_mul(f_part, nw, 1e-6, wg), act_all[lo:hi])
+
+
+def test_pack_decode_weight_layout():
+    """packed[b][c][s][lane] = row(b, lane % 16), cols 256 c + 32 s + 8 (lane // 16) .. +7."""
+    from sid.kernels.ops import pack_decode_weight
+    torch.manual_seed(4)
+    for n, k, gu in ((64, 512, False), (48, 768, True)):
+        w = torch.randn(n, k, device="cuda").to(torch.bfloat16)
+        p = pack_decode_weight(w, gate_up=gu).cpu().view(n // 16, k // 256, 8, 64, 8)
+        wc = w.cpu()
+        if gu:  # block b = [gate rows 8b..8b+7 | up rows inter + 8b..]
+            inter = n // 2
+            wc = torch.cat([wc[:inter].view(inter // 8, 8, k), wc[inter:].view(inter // 8, 8, k)],
+                           1).view(n, k)
+        want = wc.view(n // 16, 16, k // 256, 8, 4, 8).permute(0, 2, 3, 4, 1, 5).reshape(p.shape)
+        assert torch.equal(p, want)
 
 
 @pytest.mark.parametrize("bs", [1, 13, 64])
