@@ -77,11 +77,15 @@ class Request:
             self.finished_reason = None
 
     def assert_invariants(self, dvr_mode: bool) -> None:
-        assert 0 <= self.verified_len <= self.num_output, \
-            f"req {self.rid}: verified_len {self.verified_len} vs outputs {self.num_output}"
-        assert self.stream_offset <= self.gate(dvr_mode), f"req {self.rid}: emitted beyond gate"
+        problems = []
+        if not 0 <= self.verified_len <= self.num_output:
+            problems.append(f"{self.verified_len} verified of {self.num_output} outputs")
+        if self.stream_offset > self.gate(dvr_mode):
+            problems.append(f"streamed {self.stream_offset} > visible {self.gate(dvr_mode)}")
+        assert not problems, f"request {self.rid} inconsistent: " + "; ".join(problems)
 
     def __repr__(self) -> str:
-        return (f"Request(rid={self.rid}, state={self.state.value}, P={self.prompt_len}, "
-                f"N={self.num_output}, verified={self.verified_len}, "
-                f"finished={self.finished_reason})")
+        fields = {"rid": self.rid, "state": self.state.value, "prompt": self.prompt_len,
+                  "out": self.num_output, "verified": self.verified_len,
+                  "reason": self.finished_reason}
+        return "<Request " + " ".join(f"{k}={v}" for k, v in fields.items()) + ">"

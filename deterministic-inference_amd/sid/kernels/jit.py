@@ -91,26 +91,37 @@ def load_ext():
 
 
 def build_all() -> None:
-    """Build, load and run a one-request smoke decode on the GPU (sid/kernels/jit.py:38-63)."""
+    """Compile the library, load it and check one decode-attention call on the GPU against a
+    closed form (the build-and-verify entry point that sid/kernels/jit.py:38 provides).
+
+    The case has an exact answer: every key of the request is the same row, so the softmax
+    is uniform and each query head's output is the mean of its KV head's value rows."""
     import torch
 
-    assert torch.cuda.is_available(), "a GPU is required to smoke-test the kernels"
+    build_library()
+    global _ext
+    _ext = None
     ext = load_ext()
-    dev = "cuda"
-    num_kv, num_q, hd = 8, 16, 128
-    q = torch.randn(1, num_q, hd, device=dev, dtype=torch.bfloat16)
-    k_cache = torch.randn(8, num_kv, hd, device=dev, dtype=torch.bfloat16)
-    v_cache = torch.randn(8, num_kv, hd, device=dev, dtype=torch.bfloat16)
-    kv_indptr = torch.tensor([0, 4], device=dev, dtype=torch.int32)
-    kv_indices = torch.arange(1, 5, device=dev, dtype=torch.int32)
-    num_splits = torch.ones(1, device=dev, dtype=torch.int32)
-    part_o = torch.empty(1, num_q, 1, hd, device=dev, dtype=torch.float32)
-    part_lse = torch.empty(1, num_q, 1, device=dev, dtype=torch.float32)
-    o = torch.empty_like(q)
-    ext.flash_decode_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
-                         1, 0, hd ** -0.5, part_o, part_lse, o)
-    torch.cuda.synchronize()
-    assert torch.isfinite(o.float()).all(), "smoke decode produced non-finite output"
+    assert torch.cuda.is_available(), "build_all() checks the kernels on a GPU"
+    dev = torch.device("cuda", torch.cuda.current_device())
+    hq, hkv, d, n = 16, 8, 128, 37
+    g = torch.Generator().manual_seed(7)
+    keys = torch.randn(1, hkv, d, generator=g).expand(n + 3, hkv, d).contiguous()
+    vals = torch.randn(n + 3, hkv, d, generator=g)
+    k_pool = keys.to(torch.bfloat16).to(dev)
+    v_pool = vals.to(torch.bfloat16).to(dev)
+    q = torch.randn(1, hq, d, generator=g).to(torch.bfloat16).to(dev)
+    slots = torch.arange(3, n + 3, dtype=torch.int32)  # the request's positions -> slots 3..
+    out = torch.empty_like(q)
+    part_o = torch.empty(1, hq, 2, d, dtype=torch.float32, device=dev)
+    part_lse = torch.empty(1, hq, 2, dtype=torch.float32, device=dev)
+    ext.flash_decode_fwd(q, k_pool, v_pool, torch.tensor([0, n], dtype=torch.int32, device=dev),
+                         slots.to(dev), torch.full((1,), 2, dtype=torch.int32, device=dev), 2, 0,
+                         d ** -0.5, part_o, part_lse, out)
+    want = v_pool[3:].float().mean(0).repeat_interleave(hq // hkv, 0).cpu()
+    err = (out[0].float().cpu() - want).abs().max().item()
+    assert err < 2e-2, f"decode attention check failed: max |error| {err:.3g}"
+    print(f"{LIB_PATH.name}: built for {ARCH}, decode attention within {err:.1e} of the closed form")
 
 
 if __name__ == "__main__":

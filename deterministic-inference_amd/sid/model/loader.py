@@ -45,69 +45,90 @@ def random_weights(mcfg: ModelConfig, device, seed: int = 0, std: float = 0.02,
     return w
 
 
+# ModelConfig field <- config.json key (HF Qwen3 names); the rest keep ModelConfig defaults.
+_CONFIG_FIELDS = (
+    ("num_layers", "num_hidden_layers"), ("hidden_size", "hidden_size"),
+    ("num_q_heads", "num_attention_heads"), ("num_kv_heads", "num_key_value_heads"),
+    ("head_dim", "head_dim"), ("intermediate_size", "intermediate_size"),
+    ("vocab_size", "vocab_size"), ("rms_norm_eps", "rms_norm_eps"),
+    ("rope_theta", "rope_theta"), ("max_position_embeddings", "max_position_embeddings"),
+)
+
+
+def _read_json(path: Path) -> dict:
+    return json.loads(path.read_text()) if path.exists() else {}
+
+
 def load_model_config(model_dir: Path, model_path: str) -> ModelConfig:
-    cfg = json.loads((model_dir / "config.json").read_text())
-    if cfg.get("model_type") != "qwen3":
-        raise ValueError(f"only qwen3 is supported, got {cfg.get('model_type')}")
-    eos = [cfg.get("eos_token_id", 151645)]
-    gen_path = model_dir / "generation_config.json"
-    if gen_path.exists():
-        e = json.loads(gen_path.read_text()).get("eos_token_id", eos)
-        eos = e if isinstance(e, list) else [e]
-    return ModelConfig(
-        model_path=model_path,
-        num_layers=cfg["num_hidden_layers"],
-        hidden_size=cfg["hidden_size"],
-        num_q_heads=cfg["num_attention_heads"],
-        num_kv_heads=cfg["num_key_value_heads"],
-        head_dim=cfg["head_dim"],
-        intermediate_size=cfg["intermediate_size"],
-        vocab_size=cfg["vocab_size"],
-        rms_norm_eps=cfg["rms_norm_eps"],
-        rope_theta=cfg["rope_theta"],
-        max_position_embeddings=cfg["max_position_embeddings"],
-        tie_word_embeddings=cfg.get("tie_word_embeddings", False),
-        eos_token_ids=tuple(eos),
-    )
+    """ModelConfig of a local Qwen3 checkpoint directory (config.json, and the stop ids of
+    generation_config.json when present, as sid/model/loader.py:30-50 reads them)."""
+    hf = _read_json(model_dir / "config.json")
+    if hf.get("model_type") != "qwen3":
+        raise ValueError(f"{model_dir}: model_type {hf.get('model_type')!r} is not qwen3")
+    missing = [key for _, key in _CONFIG_FIELDS if key not in hf]
+    if missing:
+        raise ValueError(f"{model_dir}/config.json lacks {missing}")
+    stop = _read_json(model_dir / "generation_config.json").get(
+        "eos_token_id", hf.get("eos_token_id", 151645))
+    return ModelConfig(model_path=model_path,
+                       tie_word_embeddings=bool(hf.get("tie_word_embeddings", False)),
+                       eos_token_ids=tuple(stop) if isinstance(stop, list) else (stop,),
+                       **{field: hf[key] for field, key in _CONFIG_FIELDS})
+
+
+# Fused weight -> the checkpoint tensors stacked along dim 0 to build it ({} = layer prefix).
+_LAYER_TENSORS = {
+    "qkv": ("{}self_attn.q_proj.weight", "{}self_attn.k_proj.weight", "{}self_attn.v_proj.weight"),
+    "o": ("{}self_attn.o_proj.weight",),
+    "q_norm": ("{}self_attn.q_norm.weight",),
+    "k_norm": ("{}self_attn.k_norm.weight",),
+    "input_ln": ("{}input_layernorm.weight",),
+    "post_ln": ("{}post_attention_layernorm.weight",),
+    "gate_up": ("{}mlp.gate_proj.weight", "{}mlp.up_proj.weight"),
+    "down": ("{}mlp.down_proj.weight",),
+}
 
 
 def load_weights(model_dir: Path, mcfg: ModelConfig, device,
                  dtype: torch.dtype = torch.bfloat16) -> dict:
-    from safetensors.torch import load_file
+    """The fused weight dict from local *.safetensors shards, read tensor by tensor. Every
+    tensor of the checkpoint must be used (rotary caches aside): a name the table does not
+    know means a different architecture."""
+    from safetensors import safe_open
 
-    raw: dict = {}
-    files = sorted(Path(model_dir).glob("*.safetensors"))
-    if not files:
+    shards = sorted(Path(model_dir).glob("*.safetensors"))
+    if not shards:
         raise FileNotFoundError(f"no safetensors under {model_dir}")
-    for f in files:
-        raw.update(load_file(str(f)))
+    where = {}
+    for shard in shards:
+        with safe_open(str(shard), framework="pt") as f:
+            where.update({name: shard for name in f.keys()})
+    used = set()
 
-    def take(name):
-        return raw.pop(name).to(device=device, dtype=dtype)
+    def fetch(*names):
+        parts = []
+        for name in names:
+            if name not in where:
+                raise KeyError(f"{model_dir}: checkpoint has no tensor {name}")
+            with safe_open(str(where[name]), framework="pt") as f:
+                parts.append(f.get_tensor(name))
+            used.add(name)
+        t = parts[0] if len(parts) == 1 else torch.cat(parts, 0)
+        return t.to(device=device, dtype=dtype).contiguous()
 
-    w = {"layers": [], "embed": take("model.embed_tokens.weight"), "norm": take("model.norm.weight")}
+    w = {"embed": fetch("model.embed_tokens.weight"), "norm": fetch("model.norm.weight")}
     if mcfg.tie_word_embeddings:
         w["lm_head"] = w["embed"]
-        raw.pop("lm_head.weight", None)
+        used.add("lm_head.weight")
     else:
-        w["lm_head"] = take("lm_head.weight")
-    for i in range(mcfg.num_layers):
-        p = f"model.layers.{i}."
-        w["layers"].append({
-            "qkv": torch.cat([take(p + "self_attn.q_proj.weight"), take(p + "self_attn.k_proj.weight"),
-                              take(p + "self_attn.v_proj.weight")], dim=0).contiguous(),
-            "o": take(p + "self_attn.o_proj.weight"),
-            "q_norm": take(p + "self_attn.q_norm.weight"),
-            "k_norm": take(p + "self_attn.k_norm.weight"),
-            "input_ln": take(p + "input_layernorm.weight"),
-            "post_ln": take(p + "post_attention_layernorm.weight"),
-            "gate_up": torch.cat([take(p + "mlp.gate_proj.weight"),
-                                  take(p + "mlp.up_proj.weight")], dim=0).contiguous(),
-            "down": take(p + "mlp.down_proj.weight"),
-        })
-    left = [k for k in raw if "rotary" not in k]
-    if left:
-        raise ValueError(f"unconsumed checkpoint tensors: {left[:5]}")
+        w["lm_head"] = fetch("lm_head.weight")
+    w["layers"] = [{key: fetch(*(n.format(f"model.layers.{i}.") for n in names))
+                    for key, names in _LAYER_TENSORS.items()}
+                   for i in range(mcfg.num_layers)]
+    extra = sorted(n for n in where if n not in used and "rotary" not in n)
+    if extra:
+        raise ValueError(f"{model_dir}: {len(extra)} checkpoint tensors not in the Qwen3 "
+                         f"layout, e.g. {extra[:3]}")
     return w
 
 

@@ -33,15 +33,18 @@ from test_gpu_model import _batch_dict, _cpu_weights
 pytestmark = pytest.mark.gpu
 
 
-def _check(logits, ref):
-    """28 layers at full context: bf16 rounding flips compound over depth, so the bar is
-    statistical: mean |error| < 2e-2 (about one bf16 ulp at |logit| ~ 2), fewer than 1 in
+def _check(logits, ref, min_agree=0.8):
+    """28 layers at full context: bf16 rounding flips compound over depth, so the logit bar
+    is statistical: mean |error| < 2e-2 (about one bf16 ulp at |logit| ~ 2), fewer than 1 in
     10^4 logits off by more than 0.1 (measured: 1-2 in 10^5), none by more than 0.25.
-    Argmax: a row whose token differs from the oracle's must be a near-tie within the
-    measured error band (the oracle's gap between the two tokens below twice the largest
-    error on this batch: two logits moving that far in opposite directions). The random-init
-    model's logits are flat (top-2 gaps ~0.1, the size of 28 layers of bf16 noise), so some
-    rows do flip; at least half must agree exactly (garbage would agree on none)."""
+    Argmax, per row with that row's own error e_r = max |logit error| of the row:
+      * a row whose oracle top-2 gap exceeds 2 e_r must give the oracle's token (no two
+        logits can move far enough to swap it);
+      * a row that gives another token must be a near-tie: the oracle's gap between its
+        token and ours is below 2 e_r;
+      * at least `min_agree` of the rows agree exactly (measured 0.86 on this batch: the
+        random-init model's logits are flat, top-2 gaps ~0.1, the size of 28 layers of bf16
+        noise; a model with a swapped operand or a wrong norm agrees on almost none)."""
     got = logits.float().cpu()
     err = (got - ref).abs()
     print(f"logits vs oracle: mean {err.mean().item():.2e}  max {err.max().item():.3f}  "
@@ -50,14 +53,21 @@ def _check(logits, ref):
     assert (err > 0.1).float().mean().item() < 1e-4
     assert err.max().item() < 0.25
     a, b = got.argmax(-1), ref.argmax(-1)
-    band = 2 * err.max().item()
+    row_err = err.max(-1).values
+    top2 = ref.topk(2, dim=-1).values
+    decided = (top2[:, 0] - top2[:, 1]) > 2 * row_err
     agree = (a == b).float().mean().item()
-    print(f"argmax agreement {agree:.3f}", flush=True)
-    assert agree >= 0.5
+    print(f"argmax agreement {agree:.3f} (floor {min_agree}); rows with a decided oracle "
+          f"argmax {int(decided.sum())} of {ref.shape[0]}, all of which must agree", flush=True)
+    assert agree >= min_agree
     for r in range(ref.shape[0]):
-        if a[r] != b[r]:
-            gap = (ref[r, b[r]] - ref[r, a[r]]).item()
-            assert gap < band, f"row {r}: argmax {a[r]} vs oracle {b[r]} (gap {gap}, band {band})"
+        if a[r] == b[r]:
+            continue
+        assert not decided[r], f"row {r}: oracle top-2 gap exceeds 2x the row's error, yet " \
+                               f"argmax {int(a[r])} != oracle {int(b[r])}"
+        gap = (ref[r, b[r]] - ref[r, a[r]]).item()
+        assert gap < 2 * row_err[r].item(), \
+            f"row {r}: argmax {int(a[r])} vs oracle {int(b[r])}, gap {gap:.3g} > 2 x {row_err[r]:.3g}"
 
 
 def _compact(kv, fb, layers):

@@ -7,11 +7,13 @@ column exactly, and non-finite logits take the exact path."""
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
 from oracle.sampler import sample_exact_ref
-from test_gpu_sampler import _check
+from test_gpu_sampler import _score
 
 pytestmark = pytest.mark.gpu
 
@@ -43,14 +45,26 @@ def test_fused_sample_equals_oracle(lm_head, m):
     n = torch.full((m,), -1, dtype=torch.int64)
     ones = torch.ones(m)
     want = sample_exact_ref(logits, temps.cpu(), n, ones, seeds.cpu(), pos.cpu())
-    for r in range(m):
-        if got[r] != want[r]:  # only a float near-tie of the scores may differ
-            _check(logits[r:r + 1], temps.cpu()[r:r + 1], n[:1], ones[:1], seeds.cpu()[r:r + 1],
-                   pos.cpu()[r:r + 1])
-    # the unfused HIP path (logits + sid_sample_rows) on the same logits
+    _assert_near_ties(got, want, logits, temps.cpu(), seeds.cpu(), pos.cpu())
+    # the unfused HIP path (logits + sid_sample_rows) on the same logits: per row the same
+    # token, or a near-tie under the same rule
     from sid.engine.sampler import sample
     unfused = sample(logits.cuda(), temps, n.cuda(), ones.cuda(), seeds, pos).cpu()
-    assert (got == unfused).float().mean().item() >= (0.95 if m > 1 else 1.0)
+    _assert_near_ties(got, unfused, logits, temps.cpu(), seeds.cpu(), pos.cpu())
+
+
+def _assert_near_ties(got, want, logits, temps, seeds, pos):
+    """Every row where the fused token differs must be a stochastic row whose fused token
+    scores within 1e-4 of the other one under the exact rule (the exp/log ulps of torch's
+    CPU kernels and of the device differ; nothing else may)."""
+    for r in range(got.shape[0]):
+        if got[r] == want[r]:
+            continue
+        t = float(temps[r])
+        assert t > 0, f"greedy row {r}: {int(got[r])} != {int(want[r])}"
+        a = _score(logits[r], t, -1, 1.0, int(seeds[r]), int(pos[r]), int(got[r]))
+        b = _score(logits[r], t, -1, 1.0, int(seeds[r]), int(pos[r]), int(want[r]))
+        assert math.isfinite(a) and abs(a - b) < 1e-4, (r, int(got[r]), int(want[r]), a, b)
 
 
 def test_certificate_equals_full_recompute(lm_head):
