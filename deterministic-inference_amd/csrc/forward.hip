@@ -39,6 +39,7 @@ struct Carver {
 };
 
 struct Layout {
+  float* r32;     // the decode chain's fp32 residual sums (r32 order)
   void* resid;
   void* x;
   void* proj;     // split-K partials (fp32) or a bf16 projection output
@@ -63,6 +64,7 @@ Layout plan(const sid_qwen3_model* m, const sid_extend_batch* b, void* ws) {
   Carver c{static_cast<char*>(ws), 0, 0};
   Layout l{};
   l.resid = c.take(t * h * 2);
+  l.r32 = static_cast<float*>(c.take(t * h * 4));
   l.x = c.take(t * h * 2);
   // One buffer for the largest projection output: fp32 chunk partials [K/256][t][n] on the
   // split-K path, bf16 [t][n] on the direct one (o and down write straight into x).
@@ -95,6 +97,40 @@ Layout plan(const sid_qwen3_model* m, const sid_extend_batch* b, void* ws) {
     const int rc_ = (call);         \
     if (rc_ != SID_OK) return rc_;  \
   } while (0)
+
+// The decode chain serves a batch when every layer has its packed weights and the shapes
+// are the chain kernels' (hidden 512 / 1024, head_dim 128, I a multiple of 24 and of 256).
+bool use_chain(const sid_qwen3_model* m, int64_t t) {
+  if (t > m->chain_max_tokens || m->head_dim != 128) return false;
+  if (m->hidden != 512 && m->hidden != 1024) return false;
+  if (m->intermediate % 24 != 0 || m->intermediate % 256 != 0 || m->intermediate > 4096) return false;
+  const int64_t ao = static_cast<int64_t>(m->num_q_heads) * m->head_dim;
+  if (ao % 256 != 0 || ao > 4096) return false;
+  for (int i = 0; i < m->num_layers; ++i) {
+    const sid_qwen3_layer& lw = m->layers[i];
+    if (!lw.qkv_packed || !lw.o_packed || !lw.gate_up_packed || !lw.down_packed) return false;
+  }
+  return true;
+}
+
+// lm_head over the sampled rows of l.x: the greedy argmax fused in (logits written if given)
+// or the fp32 logits.
+int lm_head(const sid_qwen3_model* m, const sid_extend_batch* b, const Layout& l, float* logits,
+            int64_t* greedy_tokens, void* stream) {
+  const int64_t t = b->num_tokens;
+  const int h = m->hidden;
+  const int64_t r = b->sample_indices ? b->num_samples : t;
+  const void* rows = l.x;
+  if (b->sample_indices) {
+    SID_TRY(sid_gather_rows(l.x, b->sample_indices, l.rows, r, h, t, stream));
+    rows = l.rows;
+  }
+  if (greedy_tokens) {
+    return sid_linear_argmax(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, l.argmax_ws,
+                             l.argmax_ws_bytes, greedy_tokens, stream);
+  }
+  return sid_linear(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, 1, stream);
+}
 
 }  // namespace
 }  // namespace sid
@@ -142,6 +178,29 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
 
   // residual = embed[ids]; x = rmsnorm(residual, input_ln of layer 0)
   SID_TRY(sid_gather_rows(m->embed, b->input_ids, l.resid, t, h, m->vocab, stream));
+  if (use_chain(m, t)) {
+    // Five launches per layer, the same bits (csrc/decode_chain.hip).
+    for (int i = 0; i < m->num_layers; ++i) {
+      const sid_qwen3_layer& lw = m->layers[i];
+      const bool first = i == 0;  // layer 0 normalises the embedding rows themselves
+      SID_TRY(sid_rmsnorm_qkv_post(first ? l.resid : static_cast<const void*>(l.r32), !first,
+                                   lw.input_ln, eps, lw.qkv_packed, t, h, hq, hkv, d,
+                                   lw.q_norm, lw.k_norm, b->positions, m->cos_sin,
+                                   m->max_positions, b->out_slots, l.q, lw.k_cache, lw.v_cache,
+                                   m->num_slots, stream));
+      SID_TRY(sid_extend_attention_fwd(l.q, lw.k_cache, lw.v_cache, b->qo_indptr, b->kv_indptr,
+                                       b->kv_indices, b->batch, t, hq, hkv, d, m->num_slots,
+                                       std::max(b->max_extend_len, 1), kvmax, m->sm_scale,
+                                       l.ext_ws, l.ext_ws_bytes, l.attn, stream));
+      SID_TRY(sid_linear_residual(l.attn, ao, lw.o_packed, l.resid, l.r32, t, h, ao, stream));
+      SID_TRY(sid_rmsnorm_linear_silu_mul(l.r32, 1, lw.post_ln, eps, lw.gate_up_packed, l.act,
+                                          t, h, inter, stream));
+      SID_TRY(sid_linear_residual(l.act, inter, lw.down_packed, l.resid, l.r32, t, h, inter,
+                                  stream));
+    }
+    SID_TRY(sid_rmsnorm_f32(l.r32, m->final_norm, l.x, t, h, eps, stream));
+    return lm_head(m, b, l, logits, greedy_tokens, stream);
+  }
   SID_TRY(sid_rmsnorm(l.resid, m->layers[0].input_ln, l.x, t, h, eps, stream));
   for (int i = 0; i < m->num_layers; ++i) {
     const sid_qwen3_layer& lw = m->layers[i];
@@ -192,14 +251,5 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
       SID_TRY(sid_fused_add_rmsnorm(l.x, l.resid, next_w, t, h, eps, stream));
     }
   }
-  const void* rows = l.x;
-  if (b->sample_indices) {
-    SID_TRY(sid_gather_rows(l.x, b->sample_indices, l.rows, r, h, t, stream));
-    rows = l.rows;
-  }
-  if (greedy_tokens) {  // the greedy argmax fused into the lm_head (logits written if given)
-    return sid_linear_argmax(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, l.argmax_ws,
-                             l.argmax_ws_bytes, greedy_tokens, stream);
-  }
-  return sid_linear(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, 1, stream);
+  return lm_head(m, b, l, logits, greedy_tokens, stream);
 }

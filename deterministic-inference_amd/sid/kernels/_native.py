@@ -59,7 +59,7 @@ EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward",
             "sid_flash_decode_noalloc_scratch_bytes", "sid_linear_sample_workspace_bytes",
             *_SIGNATURES)
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 
 def _check(cond: bool, msg: str) -> None:

@@ -21,14 +21,15 @@ _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_
 class Layer(ctypes.Structure):
     _fields_ = [("input_ln", _vp), ("qkv", _vp), ("q_norm", _vp), ("k_norm", _vp), ("o", _vp),
                 ("post_ln", _vp), ("gate_up", _vp), ("down", _vp), ("k_cache", _vp),
-                ("v_cache", _vp)]
+                ("v_cache", _vp), ("qkv_packed", _vp), ("o_packed", _vp),
+                ("gate_up_packed", _vp), ("down_packed", _vp)]
 
 
 class Model(ctypes.Structure):
     _fields_ = [("num_layers", _i32), ("hidden", _i32), ("num_q_heads", _i32),
                 ("num_kv_heads", _i32), ("head_dim", _i32), ("intermediate", _i32),
                 ("vocab", _i32), ("rms_eps", _f32), ("sm_scale", _f32),
-                ("split_k_max_tokens", _i32), ("num_slots", _i64), ("max_positions", _i64),
+                ("split_k_max_tokens", _i32), ("chain_max_tokens", _i32), ("num_slots", _i64), ("max_positions", _i64),
                 ("cos_sin", _vp), ("embed", _vp), ("final_norm", _vp), ("lm_head", _vp),
                 ("layers", ctypes.POINTER(Layer))]
 
@@ -54,24 +55,30 @@ def _bind(lib) -> None:
 class NativeQwen3:
     """Descriptor of one model + KV cache (pointers stay valid while both live)."""
 
-    def __init__(self, model, kv_cache, split_k_max_tokens: int):
+    def __init__(self, model, kv_cache, split_k_max_tokens: int, chain_max_tokens: int = 0):
+        """chain_max_tokens > 0: batches up to that many tokens run the decode-step chain
+        with the model's packed weights (Qwen3Model._packed_weights)."""
         cfg, w = model.cfg, model.w
         self.ext = load_ext()
         _bind(self.ext.lib)
         layers = w["layers"]
+        packed = model._packed_weights() if chain_max_tokens > 0 else None
         self.layers = (Layer * cfg.num_layers)()
         for i, lw in enumerate(layers):
             kp, vp = kv_cache.layer(i)
+            pw = ((packed[i]["qkv"].data_ptr(), packed[i]["o"].data_ptr(),
+                   packed[i]["gate_up"].data_ptr(), packed[i]["down"].data_ptr())
+                  if packed is not None else (None, None, None, None))
             self.layers[i] = Layer(lw["input_ln"].data_ptr(), lw["qkv"].data_ptr(),
                                    lw["q_norm"].data_ptr(), lw["k_norm"].data_ptr(),
                                    lw["o"].data_ptr(), lw["post_ln"].data_ptr(),
                                    lw["gate_up"].data_ptr(), lw["down"].data_ptr(),
-                                   kp.data_ptr(), vp.data_ptr())
+                                   kp.data_ptr(), vp.data_ptr(), *pw)
         kp0, _ = kv_cache.layer(0)
         self.model = Model(cfg.num_layers, cfg.hidden_size, cfg.num_q_heads, cfg.num_kv_heads,
                            cfg.head_dim, cfg.intermediate_size, cfg.vocab_size,
                            float(cfg.rms_norm_eps), float(model.sm_scale), split_k_max_tokens,
-                           kp0.shape[0], model.rope.cos_sin.shape[0],
+                           chain_max_tokens, kp0.shape[0], model.rope.cos_sin.shape[0],
                            model.rope.cos_sin.data_ptr(), w["embed"].data_ptr(),
                            w["norm"].data_ptr(), w["lm_head"].data_ptr(), self.layers)
         self.vocab = cfg.vocab_size

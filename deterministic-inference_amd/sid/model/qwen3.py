@@ -18,7 +18,7 @@ from sid.kernels.extend_attention import extend_attention_fwd
 from sid.kernels.matmul_persistent import (linear, linear_argmax, linear_argmax_supported,
                                             linear_partials, linear_sample, linear_silu_mul,
                                             linear_silu_mul_preferred)
-from sid.kernels.ops import (argmax_rows, decode_chain_supported, embedding,
+from sid.kernels.ops import (DECODE_CHAIN_MAX_ROWS, argmax_rows, decode_chain_supported, embedding,
                              fused_add_rmsnorm_partials, gather_rows, linear_residual,
                              pack_decode_weight, qkv_post,
                              rmsnorm_f32, rmsnorm_linear_silu_mul, rmsnorm_qkv_post, silu_mul,
@@ -211,7 +211,9 @@ class Qwen3Model:
 
     def _native_forward(self, fb: ForwardBatch, kv_cache, greedy: bool) -> torch.Tensor:
         from sid.model.native import NativeQwen3
-        key = (id(kv_cache), tuple(kv_cache.layer(0)[0].shape))
+        key = (id(kv_cache), tuple(kv_cache.layer(0)[0].shape), self.decode_chain)
         if self._native is None or self._native.key != key:
-            self._native = NativeQwen3(self, kv_cache, SPLIT_K_MAX_TOKENS)
+            self._native = NativeQwen3(self, kv_cache, SPLIT_K_MAX_TOKENS,
+                                       DECODE_CHAIN_MAX_ROWS if self.decode_chain else 0)
+            self._native.key = key
         return self._native.forward(fb, greedy)

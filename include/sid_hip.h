@@ -392,9 +392,13 @@ int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bia
  * has no counterpart of its own in the reference, whose forward is Python.
  * A projection with N <= 2048 output columns uses the split-K path up to
  * 4 * split_k_max_tokens tokens, N <= 4096 up to split_k_max_tokens, wider ones
- * below split_k_max_tokens (the results are the same either way). Outputs:
- * logits fp32 [R, vocab] and/or greedy_tokens int64 [R] (R = num_samples, or
- * num_tokens without sample_indices).
+ * below split_k_max_tokens (the results are the same either way). When the
+ * layer's packed weights (sid_pack_decode_weight) are given and the batch has
+ * at most chain_max_tokens tokens, each layer instead runs the decode-step
+ * chain (sid_rmsnorm_qkv_post, extend attention, sid_linear_residual,
+ * sid_rmsnorm_linear_silu_mul, sid_linear_residual): the same bits in five
+ * launches. Outputs: logits fp32 [R, vocab] and/or greedy_tokens int64 [R]
+ * (R = num_samples, or num_tokens without sample_indices).
  */
 typedef struct {
   const void* input_ln;
@@ -407,6 +411,11 @@ typedef struct {
   const void* down;
   void* k_cache;
   void* v_cache;
+  /* fragment-packed copies of qkv, o, gate_up (gate_up = 1) and down, or all NULL */
+  const void* qkv_packed;
+  const void* o_packed;
+  const void* gate_up_packed;
+  const void* down_packed;
 } sid_qwen3_layer;
 
 typedef struct {
@@ -420,6 +429,7 @@ typedef struct {
   float rms_eps;
   float sm_scale;
   int split_k_max_tokens;
+  int chain_max_tokens; /* batches up to this size take the chain (packed weights given) */
   int64_t num_slots;
   int64_t max_positions;
   const float* cos_sin;
