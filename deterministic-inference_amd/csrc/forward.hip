@@ -86,7 +86,8 @@ Layout plan(const sid_qwen3_model* m, const sid_extend_batch* b, void* ws) {
                                                         static_cast<int>(kvmax));
   l.ext_ws = l.ext_ws_bytes > 0 ? c.take(l.ext_ws_bytes) : nullptr;
   l.rows = b->sample_indices ? c.take(r * h * 2) : nullptr;
-  l.argmax_ws_bytes = sid_linear_argmax_workspace_bytes(r);
+  l.argmax_ws_bytes = b->temperatures ? sid_linear_sample_workspace_bytes(r)
+                                      : sid_linear_argmax_workspace_bytes(r);
   l.argmax_ws = l.argmax_ws_bytes > 0 ? c.take(l.argmax_ws_bytes) : nullptr;
   l.total = c.used;
   return l;
@@ -125,6 +126,11 @@ int lm_head(const sid_qwen3_model* m, const sid_extend_batch* b, const Layout& l
     SID_TRY(sid_gather_rows(l.x, b->sample_indices, l.rows, r, h, t, stream));
     rows = l.rows;
   }
+  if (greedy_tokens && b->temperatures) {  // the sampler fused into the lm_head
+    return sid_linear_sample(rows, h, m->lm_head, r, m->vocab, h, b->temperatures, b->seeds,
+                             b->sample_positions, l.argmax_ws, l.argmax_ws_bytes, greedy_tokens,
+                             logits, b->sample_flags, stream);
+  }
   if (greedy_tokens) {
     return sid_linear_argmax(rows, h, m->lm_head, nullptr, logits, r, m->vocab, h, l.argmax_ws,
                              l.argmax_ws_bytes, greedy_tokens, stream);
@@ -155,6 +161,8 @@ extern "C" int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_exte
                   b->kv_indices,
               "qwen3_extend_forward: null batch field");
   SID_REQUIRE(logits || greedy_tokens, "qwen3_extend_forward: no output");
+  SID_REQUIRE(!b->temperatures || (greedy_tokens && b->seeds && b->sample_positions),
+              "qwen3_extend_forward: sampling needs tokens, seeds and sample_positions");
   const int64_t t = b->num_tokens;
   const int64_t r = b->sample_indices ? b->num_samples : t;
   SID_REQUIRE(r > 0, "qwen3_extend_forward: no sampled rows");

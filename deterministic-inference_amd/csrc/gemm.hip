@@ -257,6 +257,115 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) 
   return v > bv || (v == bv && i < bi);
 }
 
+struct SampleStats {
+  float* mx;
+  float* sm;
+  float* a1v;
+  float* a1x;
+  float* a2v;
+  int* a1i;
+};
+
+__device__ __forceinline__ void softmax_merge(float& m, float& s, float om, float os) {
+  const float nm = fmaxf(m, om);
+  const float a = m == -INFINITY ? 0.0f : s * expf(m - nm);
+  const float b = om == -INFINITY ? 0.0f : os * expf(om - nm);
+  m = nm;
+  s = a + b;
+}
+
+// One lane's sampler statistics over the columns it has seen (see linear_sample_kernel):
+// greedy rows keep only (v1, i1) = the best (logit, column) under argmax_better.
+struct SState {
+  float m, s, v1, x1, v2;
+  int i1;
+};
+
+__device__ __forceinline__ SState sstate_empty() {
+  return SState{-INFINITY, 0.0f, -INFINITY, -INFINITY, -INFINITY, 0x7fffffff};
+}
+
+// Column `col` with bf16-rounded logit vr, for a row with temperature t and noise row hash h.
+__device__ __forceinline__ void sstate_add(SState& a, float vr, int col, float t, uint32_t h) {
+  if (!(t > 0.0f)) {
+    if (argmax_better(vr, col, a.v1, a.i1)) {
+      a.v1 = vr;
+      a.i1 = col;
+    }
+    return;
+  }
+  const float xv = vr / t;
+  if (xv > a.m) {
+    a.s = a.s * expf(a.m - xv) + 1.0f;
+    a.m = xv;
+  } else {
+    a.s += expf(xv - a.m);
+  }
+  const float xg = xv + seeded_gumbel(h, col);
+  if (xg > a.v1 || (xg == a.v1 && col < a.i1)) {
+    a.v2 = a.v1;
+    a.v1 = xg;
+    a.x1 = xv;
+    a.i1 = col;
+  } else {
+    a.v2 = fmaxf(a.v2, xg);
+  }
+}
+
+// a <- a merged with b (a fixed function of the two states).
+__device__ __forceinline__ void sstate_merge(SState& a, const SState& b, bool greedy) {
+  if (greedy) {
+    if (argmax_better(b.v1, b.i1, a.v1, a.i1)) {
+      a.v1 = b.v1;
+      a.i1 = b.i1;
+    }
+    return;
+  }
+  softmax_merge(a.m, a.s, b.m, b.s);
+  if (b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1)) {
+    a.v2 = fmaxf(a.v1, b.v2);
+    a.v1 = b.v1;
+    a.x1 = b.x1;
+    a.i1 = b.i1;
+  } else {
+    a.v2 = fmaxf(a.v2, fmaxf(b.v1, b.v2));
+  }
+}
+
+// Merge over the 16 lanes of a DPP row (xor butterfly; every lane ends with the same state).
+__device__ __forceinline__ void sstate_merge16(SState& a, bool greedy) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int mask = 1; mask < 16; mask <<= 1) {
+    SState b;
+    b.m = lane_xor(a.m, mask);
+    b.s = lane_xor(a.s, mask);
+    b.v1 = lane_xor(a.v1, mask);
+    b.x1 = lane_xor(a.x1, mask);
+    b.v2 = lane_xor(a.v2, mask);
+    b.i1 = __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, a.i1);
+    sstate_merge(a, b, greedy);
+  }
+}
+
+__device__ __forceinline__ void sstate_store(const SampleStats& st, int64_t o, const SState& a) {
+  st.mx[o] = a.m;
+  st.sm[o] = a.s;
+  st.a1v[o] = a.v1;
+  st.a1x[o] = a.x1;
+  st.a2v[o] = a.v2;
+  st.a1i[o] = a.i1;
+}
+
+// Per-row inputs of a fused sampler epilogue; statistics go to st at [group][cand_rows].
+struct SampleIn {
+  const float* temps;
+  const int64_t* seeds;
+  const int64_t* positions;
+  SampleStats st;
+  int64_t cand_rows;
+};
+
 // ---- large-M tiled GEMM (prefill) ---------------------------------------------------------
 //
 // 128 x 128 output tile per 4-wave workgroup (wave (wm, wn): 64 x 64 = 4 x 4 MFMA blocks),
@@ -292,11 +401,12 @@ constexpr int TT_SUB_PER_CHUNK = KC / TT_K;
 // inter columns, so a lane holds both values of its outputs; the epilogue writes
 // act[row][c] = silu_mul1(gate, up) of the bf16-rounded projections ([M, inter], the bits of
 // sid_silu_mul over sid_linear's output) and no projection.
-template <int WM, int WN, int MB, int NB, int PF, bool AM = false, bool SW = false>
-__global__ void __launch_bounds__(WM * WN * 64, AM ? 4 : 1) linear_tiled_kernel(
+template <int WM, int WN, int MB, int NB, int PF, bool AM = false, bool SW = false,
+          bool SP = false>
+__global__ void __launch_bounds__(WM * WN * 64, (AM || SP) ? 4 : 1) linear_tiled_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ bias, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
-    int out_fp32, float* __restrict__ best_val, int* __restrict__ best_idx) {
+    int out_fp32, float* __restrict__ best_val, int* __restrict__ best_idx, SampleIn sp) {
   constexpr int TM = WM * MB * 16;
   constexpr int TN = WN * NB * 16;
   constexpr int THREADS = WM * WN * 64;
@@ -465,6 +575,64 @@ __global__ void __launch_bounds__(WM * WN * 64, AM ? 4 : 1) linear_tiled_kernel(
         }
       }
     }
+  } else if constexpr (SP) {
+    // Sampler epilogue, one row block at a time: each lane's statistics over its columns
+    // (logits written as fp32 when y is given), merged over the 16 column lanes of a row,
+    // then over the WN waves of a row band in wave order through LDS (the x tile buffer,
+    // free once every wave is past its last MFMA); one record per (column tile, row).
+    float* s_f = reinterpret_cast<float*>(&sa[0][0]);  // [5][WN][TM] floats, then [WN][TM] ints
+    int* s_i = reinterpret_cast<int*>(s_f + 5 * WN * TM);
+    static_assert(6 * WN * TM * 4 <= TM * TT_KS * 2, "sampler scratch exceeds the x tile");
+    __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int lr = MB * 16 * wm + 16 * mb + 4 * g + i;
+        const int64_t row = m0 + lr;
+        const int64_t rc = min<int64_t>(row, M - 1);
+        const float t = sp.temps[rc];
+        const uint32_t h = gumbel_row(sp.seeds[rc], sp.positions[rc]);
+        SState a = sstate_empty();
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int64_t col = n0 + NB * 16 * wn + 16 * nb + r;
+          if (col >= N || row >= M) continue;
+          const float vr = round_bf16(tot[mb][nb][i]);
+          if (y != nullptr) static_cast<float*>(y)[row * N + col] = vr;
+          sstate_add(a, vr, static_cast<int>(col), t, h);
+        }
+        sstate_merge16(a, !(t > 0.0f));
+        if (r == 0) {
+          const int o = wn * TM + lr;
+          s_f[o] = a.m;
+          s_f[WN * TM + o] = a.s;
+          s_f[2 * WN * TM + o] = a.v1;
+          s_f[3 * WN * TM + o] = a.x1;
+          s_f[4 * WN * TM + o] = a.v2;
+          s_i[o] = a.i1;
+        }
+      }
+    }
+    __syncthreads();
+    for (int lr = tid; lr < TM; lr += THREADS) {
+      const int64_t row = m0 + lr;
+      if (row >= M) continue;
+      const bool greedy = !(sp.temps[row] > 0.0f);
+      SState a = sstate_empty();
+#pragma unroll
+      for (int q = 0; q < WN; ++q) {
+        const int o = q * TM + lr;
+        const SState b{s_f[o], s_f[WN * TM + o], s_f[2 * WN * TM + o], s_f[3 * WN * TM + o],
+                       s_f[4 * WN * TM + o], s_i[o]};
+        if (q == 0) {
+          a = b;
+        } else {
+          sstate_merge(a, b, greedy);
+        }
+      }
+      sstate_store(sp.st, static_cast<int64_t>(blockIdx.x) * sp.cand_rows + row, a);
+    }
   } else if constexpr (!AM) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -552,15 +720,16 @@ __global__ void __launch_bounds__(WM * WN * 64, AM ? 4 : 1) linear_tiled_kernel(
   }
 }
 
-template <int WM, int WN, int MB, int NB, int PF, bool AM = false, bool SW = false>
+template <int WM, int WN, int MB, int NB, int PF, bool AM = false, bool SW = false,
+          bool SP = false>
 void launch_tiled(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t m,
                   int64_t n, int64_t k, int out_fp32, hipStream_t s, float* best_val = nullptr,
-                  int* best_idx = nullptr) {
+                  int* best_idx = nullptr, SampleIn sp = SampleIn{}) {
   constexpr int TM = WM * MB * 16, TN = WN * NB * 16;
   const dim3 grid((unsigned)((n + TN - 1) / TN), (unsigned)((m + TM - 1) / TM));
-  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB, PF, AM, SW>), grid, dim3(WM * WN * 64), 0, s,
-                     (const bf16_t*)x, ldx, (const bf16_t*)w, (const bf16_t*)bias, y, m, n, k,
-                     out_fp32, best_val, best_idx);
+  hipLaunchKernelGGL((linear_tiled_kernel<WM, WN, MB, NB, PF, AM, SW, SP>), grid,
+                     dim3(WM * WN * 64), 0, s, (const bf16_t*)x, ldx, (const bf16_t*)w,
+                     (const bf16_t*)bias, y, m, n, k, out_fp32, best_val, best_idx, sp);
 }
 
 // sid_linear takes the tiled kernel from this many rows up: 8 waves (4 x 2), each 32 x 64
@@ -815,23 +984,6 @@ __global__ void __launch_bounds__(256) argmax_finalize_kernel(const float* __res
 // (by a margin far above float rounding) cannot hold the winner. A wave that fails the test
 // (a near-tie, or non-finite statistics: then every wave) has its logits recomputed for the
 // row with the same MFMA sequence (identical bits) and every column scored exactly.
-struct SampleStats {
-  float* mx;
-  float* sm;
-  float* a1v;
-  float* a1x;
-  float* a2v;
-  int* a1i;
-};
-
-__device__ __forceinline__ void softmax_merge(float& m, float& s, float om, float os) {
-  const float nm = fmaxf(m, om);
-  const float a = m == -INFINITY ? 0.0f : s * expf(m - nm);
-  const float b = om == -INFINITY ? 0.0f : os * expf(om - nm);
-  m = nm;
-  s = a + b;
-}
-
 template <int MBS>
 __global__ void __launch_bounds__(STREAM_WAVES * 64) linear_sample_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w, int M, int N,
@@ -1057,7 +1209,7 @@ __global__ void __launch_bounds__(kFinThreads) sample_finalize_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w, int N,
     SampleStats st, int num_waves, int M, const float* __restrict__ temps,
     const int64_t* __restrict__ seeds, const int64_t* __restrict__ positions,
-    int* __restrict__ redo, int64_t* __restrict__ out, int recompute_all) {
+    int* __restrict__ redo, int64_t* __restrict__ out, int recompute_all, int group_tiles) {
   __shared__ float s_v[kFinThreads / 64];
   __shared__ int s_i[kFinThreads / 64];
   __shared__ float s_red[kFinThreads / 64];
@@ -1150,8 +1302,11 @@ __global__ void __launch_bounds__(kFinThreads) sample_finalize_kernel(
     // column) and score every column.
     for (int k = wave; k < nredo; k += kFinThreads / 64) {
       const int wv = list[k];
-      const int tb = static_cast<int>(static_cast<int64_t>(wv) * tiles / num_waves);
-      const int te = static_cast<int>(static_cast<int64_t>(wv + 1) * tiles / num_waves);
+      // The group's 16-column tiles: a streaming wave's run, or a fixed-width column tile.
+      const int tb = group_tiles > 0 ? wv * group_tiles
+                                     : static_cast<int>(static_cast<int64_t>(wv) * tiles / num_waves);
+      const int te = group_tiles > 0 ? min(tiles, (wv + 1) * group_tiles)
+                                     : static_cast<int>(static_cast<int64_t>(wv + 1) * tiles / num_waves);
       for (int tile = tb; tile < te; ++tile) {
         const int col = tile * 16 + r;
         const bf16_t* wrow = w + static_cast<int64_t>(col) * WIDE_K + 8 * g;
@@ -1535,13 +1690,20 @@ static void launch_sample_mbs(const bf16_t* x, int64_t ldx, const void* w, int m
                      row0);
 }
 
+// The streaming sampler reads the weights once per 64-row group; above this many rows (or
+// when asked) the tiled GEMM with the sampler epilogue reads them once per 128-row tile
+// (candidate groups: 128-column tiles instead of streaming waves). Measured at T = 0.7,
+// 151936 x 1024, graph-timed (streaming vs tiled, us): 1 row 80 vs 108, 64 rows 120 vs
+// 142, 128 rows 214 vs 158, 192 rows 265 vs 266, 256 rows 285 vs 284.
+constexpr int64_t kStreamSampleMaxM = 64;
+
 extern "C" int sid_linear_sample(const void* x, int64_t ldx, const void* w, int64_t m, int64_t n,
                                  int64_t k, const float* temperatures, const int64_t* seeds,
                                  const int64_t* positions, void* workspace,
-                                 int64_t workspace_bytes, int64_t* out_idx, int flags,
-                                 void* stream) {
+                                 int64_t workspace_bytes, int64_t* out_idx, float* logits,
+                                 int flags, void* stream) {
   SID_REQUIRE(m >= 0 && n >= 0 && k >= 0, "linear_sample: negative size");
-  SID_REQUIRE(flags == 0 || flags == 1, "linear_sample: unknown flags %d", flags);
+  SID_REQUIRE((flags & ~7) == 0 && (flags & 6) != 6, "linear_sample: bad flags %d", flags);
   if (m == 0) return SID_OK;
   SID_REQUIRE(n > 0, "linear_sample: no columns");
   SID_REQUIRE(out_idx && workspace && temperatures && seeds && positions,
@@ -1556,29 +1718,46 @@ extern "C" int sid_linear_sample(const void* x, int64_t ldx, const void* w, int6
               (long long)workspace_bytes, (long long)need);
   SID_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
               "linear_sample: workspace must be 16-byte aligned");
-  const int waves = stream_grid() * STREAM_WAVES;
-  const int64_t plane = static_cast<int64_t>(waves) * m;
+  SID_REQUIRE(!(flags & 4) || logits == nullptr,
+              "linear_sample: the streaming grouping writes no logits");
+  const bool tiled =
+      (flags & 2) != 0 || ((flags & 4) == 0 && (m > kStreamSampleMaxM || logits != nullptr));
+  const int stream_groups = stream_grid() * STREAM_WAVES;
+  const int groups = tiled ? static_cast<int>((n + 127) / 128) : stream_groups;
+  SID_REQUIRE(groups <= stream_groups, "linear_sample: N=%lld has more than %d column tiles",
+              (long long)n, stream_groups);
+  const int64_t plane = static_cast<int64_t>(stream_groups) * m;
   float* base = static_cast<float*>(workspace);
   SampleStats st{base, base + plane, base + 2 * plane, base + 3 * plane, base + 4 * plane,
                  reinterpret_cast<int*>(base + 5 * plane)};
   int* redo = reinterpret_cast<int*>(base + 6 * plane);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int mi = static_cast<int>(m);
-  for (int r0 = 0; r0 < mi; r0 += MROWS) {
-    const int mg = min(MROWS, mi - r0);
-    const bf16_t* xg = static_cast<const bf16_t*>(x) + static_cast<int64_t>(r0) * ldx;
-    switch ((mg + 15) / 16) {
-      case 1: launch_sample_mbs<1>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
-      case 2: launch_sample_mbs<2>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
-      case 3: launch_sample_mbs<3>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
-      default: launch_sample_mbs<4>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
-    }
+  if (tiled) {
+    SID_REQUIRE((m + 127) / 128 <= 65535, "linear_sample: too many rows");
+    launch_tiled<4, 2, 2, 4, 1, false, false, true>(
+        x, ldx, w, nullptr, logits, m, n, k, 1, s, nullptr, nullptr,
+        SampleIn{temperatures, seeds, positions, st, m});
     rc = check_launch("linear_sample");
     if (rc != SID_OK) return rc;
+  } else {
+    for (int r0 = 0; r0 < mi; r0 += MROWS) {
+      const int mg = min(MROWS, mi - r0);
+      const bf16_t* xg = static_cast<const bf16_t*>(x) + static_cast<int64_t>(r0) * ldx;
+      switch ((mg + 15) / 16) {
+        case 1: launch_sample_mbs<1>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
+        case 2: launch_sample_mbs<2>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
+        case 3: launch_sample_mbs<3>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
+        default: launch_sample_mbs<4>(xg, ldx, w, mg, (int)n, temperatures, seeds, positions, st, mi, r0, s); break;
+      }
+      rc = check_launch("linear_sample");
+      if (rc != SID_OK) return rc;
+    }
   }
   hipLaunchKernelGGL(sample_finalize_kernel, dim3((unsigned)m), dim3(kFinThreads), 0, s,
-                     (const bf16_t*)x, ldx, (const bf16_t*)w, (int)n, st, waves, mi, temperatures,
-                     seeds, positions, redo, out_idx, flags);
+                     (const bf16_t*)x, ldx, (const bf16_t*)w, (int)n, st, groups, mi,
+                     temperatures, seeds, positions, redo, out_idx, flags & 1,
+                     tiled ? 8 : 0);
   return check_launch("linear_sample finalize");
 }
 

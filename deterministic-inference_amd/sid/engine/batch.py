@@ -53,6 +53,9 @@ class ForwardBatch:
     invariant: bool = False
     all_greedy: Optional[bool] = None  # host-known: every row has temperature 0
     untruncated: Optional[bool] = None  # host-known: no row has a top-k / top-p limit
+    # softmax-sum grouping of the lm_head-fused sampler (linear_sample's `tiles`): None = by
+    # row count; True / False = fixed, for tokens that must not depend on the batch size
+    sample_tiles: Optional[bool] = None
     graph_key: Optional[tuple] = None  # set when the inputs live in graph-static buffers
     real_rows: Optional[int] = None    # rows of real requests when padded (decode graphs)
     # decode batches in the graph-static buffers: build_paged_decode_indices arguments, run at the

@@ -113,32 +113,50 @@ class ModelRunner:
         return linear_sample_supported(self.cfg.max_decode_batch, self.mcfg.hidden_size)
 
     def fused_sample(self, fb: ForwardBatch) -> bool:
-        """Whether a decode batch without top-k / top-p limits draws its tokens inside the
-        lm_head (sid_linear_sample) instead of writing logits for the sampler kernel.
-        batch_invariant: the engine's choice (_invariant_fused). Elsewhere by speed: fused up
-        to 128 rows (it streams the weights once per 64 rows; measured at T = 0.7: 1 row 74
-        vs 178 us, 64: 114 vs 205, 128: 205 vs 231, 256: 393 vs 329); dvr commits only the
-        verifier's tokens, so its decode rows may take either path."""
-        if fb.mode != ForwardMode.DECODE or not fb.untruncated:
+        """Whether a batch without top-k / top-p limits draws its tokens inside the lm_head
+        (sid_linear_sample) instead of writing logits for the sampler kernel, and with which
+        softmax-sum grouping (set on fb.sample_tiles; it is part of a row's result, see
+        linear_sample):
+          * DVR verify passes: always, with 128-column tiles at every size (their tokens are
+            the committed ones and must not depend on the pass's size);
+          * batch_invariant decode batches: the engine's one choice (_invariant_fused), with
+            the streaming grouping at every size;
+          * other decode batches: by speed, grouping by row count (T = 0.7, graph-timed:
+            1 row 80 vs 178 us for logits + sampler kernel, 64: 120 vs 205, 128: 158 vs 231,
+            256: 284 vs 329); dvr commits only the verifier's tokens, nondet is free."""
+        if not fb.untruncated or fb.mode == ForwardMode.PREFILL:
             return False
+        if not linear_sample_supported(fb.input_ids.shape[0] if fb.sample_indices is None
+                                       else fb.sample_indices.shape[0], self.mcfg.hidden_size):
+            return False
+        if fb.mode == ForwardMode.VERIFY:
+            fb.sample_tiles = True
+            return True
         if fb.invariant:
+            fb.sample_tiles = False
             return self._invariant_fused()
-        rows = fb.input_ids.shape[0]
-        return linear_sample_supported(rows, self.mcfg.hidden_size) and rows <= 128
+        fb.sample_tiles = None
+        return True
 
     def step(self, fb: ForwardBatch) -> torch.Tensor:
         """forward + sample -> int64 tokens [R]. An all-greedy batch takes the fused
-        lm_head + argmax path, a decode batch the fused lm_head + sampler where
-        fused_sample says so (no logits written); the rest writes the logits and runs the
-        sampler kernel over them. A batch_invariant decode batch that mixes rows with and
-        without top-k / top-p limits, on an engine whose choice is the fused sampler, gets
-        both: the fused sampler's tokens for the rows without limits (as in any other batch),
-        the sampler kernel's for the others."""
+        lm_head + argmax path, a batch without top-k / top-p limits the fused lm_head +
+        sampler where fused_sample says so (no logits written); the rest writes the logits
+        and runs the sampler kernel over them. A batch that mixes rows with and without
+        limits and needs the fused sampler's tokens for the latter (a batch_invariant decode
+        batch on an engine whose choice is the fused sampler, or a verify pass) gets both:
+        the fused sampler's tokens for the rows without limits (as in any other batch), the
+        sampler kernel's for the others."""
         if fb.all_greedy:
             return self.forward(fb, greedy=True)
         if self.fused_sample(fb):
             return self.forward(fb, sample=True)
-        if fb.mode == ForwardMode.DECODE and fb.invariant and self._invariant_fused():
+        mixed_verify = fb.mode == ForwardMode.VERIFY and linear_sample_supported(
+            fb.sample_indices.shape[0] if fb.sample_indices is not None else fb.input_ids.shape[0],
+            self.mcfg.hidden_size)
+        mixed_invariant = fb.mode == ForwardMode.DECODE and fb.invariant and self._invariant_fused()
+        if mixed_verify or mixed_invariant:
+            fb.sample_tiles = True if mixed_verify else False
             logits, fused = self.forward(fb, sample=True, with_logits=True)
             r = logits.shape[0]
             free = (fb.top_ks[:r] <= 0) & (fb.top_ps[:r] >= 1.0)

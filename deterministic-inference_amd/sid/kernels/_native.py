@@ -44,8 +44,8 @@ _SIGNATURES = {
                                               _i32, _i64, _i32, _i32, _i32, _i32, _i32, _vp,
                                               _f32, _vp, _vp],
     "sid_sample_rows": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp],
-    "sid_linear_sample": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i32,
-                          _vp],
+    "sid_linear_sample": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
+                          _i32, _vp],
     "sid_linear_argmax": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
     "sid_linear_residual": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "sid_rmsnorm_linear_silu_mul": [_vp, _i32, _vp, _f32, _vp, _vp, _i64, _i64, _i64, _vp],
@@ -59,7 +59,7 @@ EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward",
             "sid_flash_decode_noalloc_scratch_bytes", "sid_linear_sample_workspace_bytes",
             *_SIGNATURES)
-ABI_VERSION = 18
+ABI_VERSION = 20
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -309,8 +309,13 @@ class NativeLib:
         return int(self.lib.sid_linear_sample_workspace_bytes(m))
 
     def linear_sample(self, x, w, temperatures, seeds, positions, workspace, out,
-                      recompute_all: bool = False) -> None:
+                      recompute_all: bool = False, tiles=None, logits=None) -> None:
+        """tiles: None = grouping by row count; True = 128-column tiles; False = streaming
+        waves."""
         m, k, n = self._linear_check(x, w)
+        if logits is not None:
+            _gpu(logits, "logits", torch.float32)
+            _check(tuple(logits.shape) == (m, n), "logits must be [M, N]")
         for name, t, dt in (("temperatures", temperatures, torch.float32),
                             ("seeds", seeds, torch.int64), ("positions", positions, torch.int64),
                             ("out", out, torch.int64)):
@@ -320,7 +325,8 @@ class NativeLib:
         self._call("sid_linear_sample", x.data_ptr(), x.stride(0) if m > 1 else k, w.data_ptr(),
                    m, n, k, temperatures.data_ptr(), seeds.data_ptr(), positions.data_ptr(),
                    workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-                   out.data_ptr(), int(recompute_all), _stream(x))
+                   out.data_ptr(), logits.data_ptr() if logits is not None else None,
+                   int(recompute_all) | {None: 0, True: 2, False: 4}[tiles], _stream(x))
 
     @staticmethod
     def _linear_check(x, w):

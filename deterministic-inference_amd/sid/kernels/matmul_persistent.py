@@ -114,12 +114,17 @@ def linear_sample(x: torch.Tensor, weight: torch.Tensor, temperatures: torch.Ten
                   seeds: torch.Tensor, positions: torch.Tensor,
                   workspace: Optional[torch.Tensor] = None,
                   out: Optional[torch.Tensor] = None,
-                  recompute_all: bool = False) -> torch.Tensor:
-    """Tokens int64 [M] drawn from the logits x @ weight^T without writing them: greedy rows
-    (temperature 0) take the argmax, the others the seeded Gumbel-max draw of
-    sid/engine/sampler.py:32-69 with no top-k / top-p limit. The logits are exactly those
-    of linear(..., out_fp32=True); needs linear_sample_supported(M, K). recompute_all scores
-    every column exactly instead of certifying per-wave candidates (a check; slow)."""
+                  recompute_all: bool = False, tiles: Optional[bool] = None,
+                  logits: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Tokens int64 [M] drawn from the logits x @ weight^T: greedy rows (temperature 0) take
+    the argmax, the others the seeded Gumbel-max draw of sid/engine/sampler.py:32-69 with no
+    top-k / top-p limit. The logits are exactly those of linear(..., out_fp32=True) (written
+    to `logits` when given, else not at all); needs linear_sample_supported(M, K).
+    A row's token depends on the row and on how the softmax sum is grouped: tiles=None picks
+    by speed (streaming waves up to 64 rows, 128-column tiles above or with logits);
+    tiles=True / False fix the tiles / the streaming waves, for callers whose tokens must not
+    depend on the batch size. recompute_all scores every column exactly instead of
+    certifying per-group candidates (a check; slow)."""
     m, k = x.shape
     ext = load_ext()
     if workspace is None:
@@ -128,5 +133,5 @@ def linear_sample(x: torch.Tensor, weight: torch.Tensor, temperatures: torch.Ten
     if out is None:
         out = torch.empty(m, dtype=torch.int64, device=x.device)
     ext.linear_sample(x, weight, temperatures.float().contiguous(), seeds.long().contiguous(),
-                      positions.long().contiguous(), workspace, out, recompute_all)
+                      positions.long().contiguous(), workspace, out, recompute_all, tiles, logits)
     return out

@@ -38,7 +38,9 @@ class Batch(ctypes.Structure):
     _fields_ = [("num_tokens", _i64), ("batch", _i32), ("max_extend_len", _i32),
                 ("max_kv_len", _i32), ("num_kv_indices", _i64), ("input_ids", _vp),
                 ("positions", _vp), ("out_slots", _vp), ("qo_indptr", _vp), ("kv_indptr", _vp),
-                ("kv_indices", _vp), ("sample_indices", _vp), ("num_samples", _i64)]
+                ("kv_indices", _vp), ("sample_indices", _vp), ("num_samples", _i64),
+                ("temperatures", _vp), ("seeds", _vp), ("sample_positions", _vp),
+                ("sample_flags", _i32)]
 
 
 def _bind(lib) -> None:
@@ -84,24 +86,32 @@ class NativeQwen3:
         self.vocab = cfg.vocab_size
         self.key = (id(kv_cache), tuple(kv_cache.layer(0)[0].shape))
 
-    def forward(self, fb, greedy: bool) -> torch.Tensor:
-        """Logits fp32 [R, V] of the sampled rows, or their greedy tokens int64 [R]."""
+    def forward(self, fb, greedy: bool, sample: bool = False, with_logits: bool = False,
+                sample_tiles: bool = True):
+        """Logits fp32 [R, V] of the sampled rows, or their greedy tokens int64 [R], or
+        (sample=True) the tokens the lm_head-fused sampler draws for them (no top-k / top-p;
+        grouping: 128-column tiles, or sid_linear_sample's choice by row count when
+        sample_tiles is False), with with_logits=True as (logits, tokens)."""
         t = fb.input_ids.numel()
         dev = fb.input_ids.device
         r = fb.sample_indices.numel() if fb.sample_indices is not None else t
+        samp = (fb.temperatures[:r].data_ptr(), fb.seeds[:r].data_ptr(),
+                fb.sample_positions[:r].data_ptr(), 2 if sample_tiles else 0) if sample \
+            else (None, None, None, 0)
         b = Batch(t, fb.qo_indptr.numel() - 1, max(fb.max_extend_len, 1),
                   int(fb.max_kv_len or fb.max_seq_len or 0), fb.kv_indices.numel(),
                   fb.input_ids.data_ptr(), fb.positions.data_ptr(), fb.out_slots.data_ptr(),
                   fb.qo_indptr.data_ptr(), fb.kv_indptr.data_ptr(), fb.kv_indices.data_ptr(),
-                  fb.sample_indices.data_ptr() if fb.sample_indices is not None else None, r)
+                  fb.sample_indices.data_ptr() if fb.sample_indices is not None else None, r,
+                  *samp)
         lib = self.ext.lib
         need = int(lib.sid_qwen3_extend_workspace_bytes(ctypes.byref(self.model), ctypes.byref(b)))
         ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
         logits: Optional[torch.Tensor] = None
         tokens: Optional[torch.Tensor] = None
-        if greedy:
-            tokens = torch.empty(r, dtype=torch.int64, device=dev)  # no logits written
-        else:
+        if greedy or sample:
+            tokens = torch.empty(r, dtype=torch.int64, device=dev)
+        if not (greedy or sample) or with_logits:
             logits = torch.empty(r, self.vocab, dtype=torch.float32, device=dev)
         rc = lib.sid_qwen3_extend_forward(
             ctypes.byref(self.model), ctypes.byref(b), ws.data_ptr(), ws.numel(),
@@ -110,4 +120,6 @@ class NativeQwen3:
             torch.cuda.current_stream(dev).cuda_stream)
         if rc != 0:
             raise RuntimeError(f"sid_qwen3_extend_forward: {lib.sid_last_error().decode()}")
-        return tokens if greedy else logits
+        if tokens is None:
+            return logits
+        return (logits, tokens) if with_logits else tokens

@@ -145,15 +145,15 @@ class Qwen3Model:
         greedy=True, the greedy tokens int64 [R] instead (argmax of those logits, fused into
         the lm_head GEMM for decode-sized R); with sample=True (decode batches of at most 256
         rows, no top-k / top-p limit), the sampled tokens int64 [R], drawn inside the lm_head
-        GEMM without writing the logits (with_logits=True: (logits, those tokens)).
+        GEMM without writing the logits (with_logits=True: (logits, those tokens)); the
+        draw's grouping is fb.sample_tiles (see linear_sample; verify passes: tiles).
 
         Same op order as sid/model/qwen3.py:88-115; the residual add + RMSNorm that follows
         each o / down projection consumes the projection directly (fused), and the down
         projection of layer i feeds layer i+1's input norm (or the final norm)."""
         decode_backend = decode_backend_kind(decode_backend)
-        assert not sample or fb.mode == ForwardMode.DECODE, "fused sampling serves decode batches"
         if self.native_extend and fb.mode != ForwardMode.DECODE:
-            return self._native_forward(fb, kv_cache, greedy)
+            return self._native_forward(fb, kv_cache, greedy, sample, with_logits)
         cfg = self.cfg
         eps = cfg.rms_norm_eps
         layers = self.w["layers"]
@@ -198,22 +198,29 @@ class Qwen3Model:
         rows = x if fb.sample_indices is None else gather_rows(x, fb.sample_indices)
         if sample:  # the sampler fused into the lm_head (rows without top-k / top-p)
             r = rows.shape[0]
-            tokens = linear_sample(rows, self.w["lm_head"], fb.temperatures[:r], fb.seeds[:r],
-                                   fb.sample_positions[:r])
-            if with_logits:  # also the logits, for the rows that need the sampler kernel
-                return linear(rows, self.w["lm_head"], out_fp32=True), tokens
-            return tokens
+            args = (rows, self.w["lm_head"], fb.temperatures[:r], fb.seeds[:r],
+                    fb.sample_positions[:r])
+            if not with_logits:
+                return linear_sample(*args, tiles=fb.sample_tiles)
+            # also the logits, for the rows that need the sampler kernel: the tiled sampler
+            # writes them in its own pass; the streaming grouping cannot
+            if fb.sample_tiles is False:
+                return linear(rows, self.w["lm_head"], out_fp32=True), linear_sample(*args, tiles=False)
+            logits = torch.empty(r, self.cfg.vocab_size, dtype=torch.float32, device=rows.device)
+            return logits, linear_sample(*args, tiles=True, logits=logits)
         if greedy:
             if linear_argmax_supported(rows.shape[0], rows.shape[1]):
                 return linear_argmax(rows, self.w["lm_head"])
             return argmax_rows(linear(rows, self.w["lm_head"], out_fp32=True))
         return linear(rows, self.w["lm_head"], out_fp32=True)
 
-    def _native_forward(self, fb: ForwardBatch, kv_cache, greedy: bool) -> torch.Tensor:
+    def _native_forward(self, fb: ForwardBatch, kv_cache, greedy: bool, sample: bool = False,
+                        with_logits: bool = False):
         from sid.model.native import NativeQwen3
         key = (id(kv_cache), tuple(kv_cache.layer(0)[0].shape), self.decode_chain)
         if self._native is None or self._native.key != key:
             self._native = NativeQwen3(self, kv_cache, SPLIT_K_MAX_TOKENS,
                                        DECODE_CHAIN_MAX_ROWS if self.decode_chain else 0)
             self._native.key = key
-        return self._native.forward(fb, greedy)
+        return self._native.forward(fb, greedy, sample, with_logits,
+                                    sample_tiles=fb.sample_tiles is not False)

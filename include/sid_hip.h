@@ -397,8 +397,10 @@ int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bia
  * at most chain_max_tokens tokens, each layer instead runs the decode-step
  * chain (sid_rmsnorm_qkv_post, extend attention, sid_linear_residual,
  * sid_rmsnorm_linear_silu_mul, sid_linear_residual): the same bits in five
- * launches. Outputs: logits fp32 [R, vocab] and/or greedy_tokens int64 [R]
- * (R = num_samples, or num_tokens without sample_indices).
+ * launches. Outputs: logits fp32 [R, vocab] and/or tokens int64 [R]
+ * (R = num_samples, or num_tokens without sample_indices): the greedy argmax,
+ * or with b->temperatures the fused sampler's draw (sid_linear_sample: rows
+ * without a top-k / top-p limit; needs hidden 1024 and R <= 256).
  */
 typedef struct {
   const void* input_ln;
@@ -453,11 +455,16 @@ typedef struct {
   const int32_t* kv_indices;
   const int64_t* sample_indices; /* NULL: every token row */
   int64_t num_samples;
+  /* Sampled rows' draw parameters (sid_linear_sample), or NULL: greedy argmax */
+  const float* temperatures;
+  const int64_t* seeds;
+  const int64_t* sample_positions;
+  int sample_flags; /* sid_linear_sample's grouping flags (2: column tiles) */
 } sid_extend_batch;
 
 int64_t sid_qwen3_extend_workspace_bytes(const sid_qwen3_model* m, const sid_extend_batch* b);
 int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_extend_batch* b, void* workspace,
-                             int64_t workspace_bytes, float* logits, int64_t* greedy_tokens,
+                             int64_t workspace_bytes, float* logits, int64_t* tokens,
                              void* stream);
 
 /*
@@ -468,18 +475,23 @@ int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_extend_batch* b
  * argmax_c log(softmax(l / T)_c + 1e-10) + gumbel(seeds[r], positions[r], c)
  * with the reference's hash, i.e. sample() with top_k <= 0 and top_p >= 1
  * (rows with a top-k / top-p limit need sid_sample_rows over the logits).
- * The logits have the bits of sid_linear's fp32 output. Workspace:
+ * The logits have the bits of sid_linear's fp32 output; they are written to
+ * `logits` (fp32 [M, N]) when it is not NULL. Workspace:
  * sid_linear_sample_workspace_bytes(M) bytes, 16-byte aligned. Replaces the
  * logits epilogue of Qwen3Model.forward (sid/model/qwen3.py:113-115) plus
- * sample() for untruncated rows. flags: 0; 1 = recompute every column of every
- * stochastic row exactly instead of certifying the per-wave candidates (a
- * check of the certificate: same tokens, much slower).
+ * sample() for untruncated rows. The softmax sum is accumulated over groups of
+ * columns: streaming waves (up to 64 rows) or 128-column tiles (more rows, or
+ * logits requested); a row's token depends only on the row and the grouping,
+ * so a caller that needs tokens independent of the batch size fixes the
+ * grouping: flag 2 = column tiles, flag 4 = streaming waves (no logits).
+ * flag 1 = recompute every column of every stochastic row exactly instead of
+ * certifying the per-group candidates (a check: same tokens, much slower).
  */
 int64_t sid_linear_sample_workspace_bytes(int64_t m);
 int sid_linear_sample(const void* x, int64_t ldx, const void* w, int64_t m, int64_t n, int64_t k,
                       const float* temperatures, const int64_t* seeds, const int64_t* positions,
-                      void* workspace, int64_t workspace_bytes, int64_t* out, int flags,
-                      void* stream);
+                      void* workspace, int64_t workspace_bytes, int64_t* out, float* logits,
+                      int flags, void* stream);
 
 /*
  * out[r] = argmax(logits[r, :]) with first-index tie-break; fp32 logits

@@ -35,12 +35,17 @@ def _rows(m, seed):
     return x, temps, seeds, pos
 
 
-@pytest.mark.parametrize("m", [1, 5, 64, 100])
-def test_fused_sample_equals_oracle(lm_head, m):
+@pytest.mark.parametrize("m,tiles", [(1, None), (5, None), (64, None), (100, None),
+                                     (5, True), (64, True), (128, None), (256, None),
+                                     (100, False), (256, False)])
+def test_fused_sample_equals_oracle(lm_head, m, tiles):
+    """Streaming-wave groups up to 64 rows (tiles=None) or at any size (False); 128-column
+    tile groups above 64 rows (None) or at any size (True: the grouping verify passes
+    use)."""
     from sid.kernels.matmul_persistent import linear, linear_sample
     x, temps, seeds, pos = _rows(m, 10 + m)
-    print(f"fused sampler m={m}", flush=True)
-    got = linear_sample(x, lm_head, temps, seeds, pos).cpu()
+    print(f"fused sampler m={m} tiles={tiles}", flush=True)
+    got = linear_sample(x, lm_head, temps, seeds, pos, tiles=tiles).cpu()
     logits = linear(x, lm_head, out_fp32=True).cpu()
     n = torch.full((m,), -1, dtype=torch.int64)
     ones = torch.ones(m)
@@ -67,11 +72,24 @@ def _assert_near_ties(got, want, logits, temps, seeds, pos):
         assert math.isfinite(a) and abs(a - b) < 1e-4, (r, int(got[r]), int(want[r]), a, b)
 
 
-def test_certificate_equals_full_recompute(lm_head):
+@pytest.mark.parametrize("m,tiles", [(64, None), (64, True), (200, None), (200, False)])
+def test_certificate_equals_full_recompute(lm_head, m, tiles):
     from sid.kernels.matmul_persistent import linear_sample
-    x, temps, seeds, pos = _rows(64, 3)
-    a = linear_sample(x, lm_head, temps, seeds, pos)
-    b = linear_sample(x, lm_head, temps, seeds, pos, recompute_all=True)
+    x, temps, seeds, pos = _rows(m, 3)
+    a = linear_sample(x, lm_head, temps, seeds, pos, tiles=tiles)
+    b = linear_sample(x, lm_head, temps, seeds, pos, recompute_all=True, tiles=tiles)
+    assert torch.equal(a, b)
+
+
+def test_tiled_sampler_writes_the_logits(lm_head):
+    """With a logits buffer the tiled sampler writes sid_linear's fp32 logits and draws the
+    same tokens as without it."""
+    from sid.kernels.matmul_persistent import linear, linear_sample
+    x, temps, seeds, pos = _rows(70, 9)
+    lg = torch.full((70, V), float("nan"), device="cuda")
+    a = linear_sample(x, lm_head, temps, seeds, pos, logits=lg)
+    b = linear_sample(x, lm_head, temps, seeds, pos, tiles=True)
+    assert torch.equal(lg, linear(x, lm_head, out_fp32=True))
     assert torch.equal(a, b)
 
 
@@ -91,11 +109,15 @@ def test_non_finite_logits_follow_the_reference(lm_head):
     assert got.tolist() == want.tolist()
 
 
-def test_fused_sample_is_row_independent(lm_head):
-    """A row's token does not depend on the other rows of the batch (or on its slot)."""
+@pytest.mark.parametrize("tiles", [False, True])
+def test_fused_sample_is_row_independent(lm_head, tiles):
+    """A row's token does not depend on the other rows of the batch (or on its slot), for a
+    fixed grouping (streaming waves or tiles, at any size)."""
     from sid.kernels.matmul_persistent import linear_sample
-    x, temps, seeds, pos = _rows(80, 21)
-    full = linear_sample(x, lm_head, temps, seeds, pos)
-    for j in (0, 17, 63, 64, 79):
-        one = linear_sample(x[j:j + 1], lm_head, temps[j:j + 1], seeds[j:j + 1], pos[j:j + 1])
+    n = 200 if tiles else 80
+    x, temps, seeds, pos = _rows(n, 21)
+    full = linear_sample(x, lm_head, temps, seeds, pos, tiles=tiles)
+    for j in (0, 17, 63, 64, 79, n - 1):
+        one = linear_sample(x[j:j + 1], lm_head, temps[j:j + 1], seeds[j:j + 1], pos[j:j + 1],
+                            tiles=tiles)
         assert one.item() == full[j].item()

@@ -2,8 +2,9 @@
 the host: nothing here launches a kernel. The fused and the logits + sampler paths agree
 except at float near-ties, so in batch_invariant mode the choice must not depend on the
 batch (one answer per engine; a batch mixing rows with and without top-k / top-p limits
-still takes the fused path for the latter, tests/test_gpu_engine.py), while nondet/dvr
-pick the faster path by row count."""
+still takes the fused path for the latter, tests/test_gpu_engine.py) and the grouping is
+fixed (streaming waves); nondet/dvr decode batches fuse up to the kernel's 256 rows with the
+grouping left to the row count; DVR verify passes always fuse, with 128-column tiles."""
 
 from __future__ import annotations
 
@@ -36,16 +37,31 @@ def test_batch_invariant_choice_is_one_per_engine(max_batch, expect):
     assert got == {expect}
 
 
-def test_nondet_picks_by_rows():
+def test_invariant_grouping_is_fixed():
     r = _runner(256)
-    assert ModelRunner.fused_sample(r, _fb(1, False))
-    assert ModelRunner.fused_sample(r, _fb(128, False))
-    assert not ModelRunner.fused_sample(r, _fb(129, False))
-    assert not ModelRunner.fused_sample(r, _fb(256, False))
+    for rows in (1, 64, 65, 256):
+        fb = _fb(rows, True)
+        assert ModelRunner.fused_sample(r, fb) and fb.sample_tiles is False
 
 
-def test_truncated_or_non_decode_batches_never_fuse():
+def test_nondet_fuses_up_to_256_rows():
+    r = _runner(512)
+    for rows in (1, 128, 129, 256):
+        fb = _fb(rows, False)
+        assert ModelRunner.fused_sample(r, fb) and fb.sample_tiles is None
+    assert not ModelRunner.fused_sample(r, _fb(257, False))
+
+
+def test_verify_passes_fuse_with_tiles():
+    r = _runner(256)
+    for rows in (1, 32, 128, 256):
+        fb = _fb(rows, True, mode=ForwardMode.VERIFY)
+        assert ModelRunner.fused_sample(r, fb) and fb.sample_tiles is True
+
+
+def test_truncated_or_prefill_batches_never_fuse():
     r = _runner(256)
     assert not ModelRunner.fused_sample(r, _fb(8, False, untruncated=False))
     assert not ModelRunner.fused_sample(r, _fb(8, True, untruncated=False))
-    assert not ModelRunner.fused_sample(r, _fb(8, True, mode=ForwardMode.VERIFY))
+    assert not ModelRunner.fused_sample(r, _fb(8, True, untruncated=False, mode=ForwardMode.VERIFY))
+    assert not ModelRunner.fused_sample(r, _fb(8, False, mode=ForwardMode.PREFILL))
