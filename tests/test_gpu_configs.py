@@ -10,11 +10,13 @@ config 4  a DVR verify pass of G=4 sequences x W=32 over 2048-token prefixes und
           its logits vs forward_ref in extend mode, and the watched request's tokens
           SHA-256-identical when it decodes in 1-, 4-, 8- and 16-wide batches with random
           co-tenants (reference tests/test_09_dvr_e2e.py).
-config 5  continuous batching with config 5's distributions at a reduced request count
-          (lognormal prompts, median 512, capped at 8192; max_new_tokens ~ U[64, 512];
-          seeded Gumbel-max at T = 0.7; half is_deterministic): the deterministic requests'
-          tokens do not change when the arrival order does (dvr), and in batch_invariant
-          mode no request's tokens do (reference tests/test_10_batch_invariant.py:41-74).
+config 5  continuous batching with config 5's distributions (lognormal prompts, median
+          512, capped at 8192; max_new_tokens ~ U[64, 512]; seeded Gumbel-max at T = 0.7;
+          half is_deterministic), at 40 requests and at the stated 512 with the bench's
+          engine settings: the deterministic requests' tokens do not change when the
+          arrival order does (dvr), and in batch_invariant mode no request's tokens do
+          (reference tests/test_10_batch_invariant.py:41-74); the KV pool's free count
+          returns to its start value.
 """
 
 from __future__ import annotations
@@ -222,3 +224,32 @@ def test_config5_arrival_order_does_not_change_tokens(mode):
     checked = [i for i, p in enumerate(params) if mode == Mode.BATCH_INVARIANT or p.is_deterministic]
     for i in checked:
         assert runs[0][i] == runs[1][i], i
+
+
+@pytest.mark.parametrize("mode", [Mode.DVR, Mode.BATCH_INVARIANT])
+def test_config5_full_512_requests(mode):
+    """Config 5 at its stated size and engine settings (the bench's: 512 requests,
+    256-row decode batches, 600k-token pool): the checked requests' tokens (dvr: the
+    deterministic ones; batch_invariant: all) are unchanged when the arrival order is
+    permuted, every request gets its max_new_tokens, and the KV pool's free count returns
+    to its start value after each run (reference tests/test_10_batch_invariant.py:41-74)."""
+    prompts, params = _config5_requests(512)
+    cfg = EngineConfig(mode=mode, kv_pool_tokens=600_000, max_reqs=260, max_seq_len=9000,
+                       max_decode_batch=256, seed=0)
+    eng = Engine(cfg)
+    free0 = eng.kv.free_count
+    order = np.random.default_rng(11).permutation(len(prompts))
+    runs = []
+    for perm in (np.arange(len(prompts)), order):
+        print(f"config 5: {mode.value}, {len(prompts)} requests", flush=True)
+        outs = eng.generate([prompts[i] for i in perm], [params[i] for i in perm])
+        toks = [None] * len(prompts)
+        for i, o in zip(perm, outs):
+            toks[i] = o.token_ids
+            assert len(o.token_ids) == params[i].max_new_tokens
+        runs.append(toks)
+        assert eng.kv.free_count == free0
+    checked = [i for i, p in enumerate(params) if mode == Mode.BATCH_INVARIANT or p.is_deterministic]
+    assert len(checked) >= 200
+    changed = [i for i in checked if runs[0][i] != runs[1][i]]
+    assert not changed, f"{len(changed)} of {len(checked)} checked requests changed: {changed[:8]}"
