@@ -51,6 +51,9 @@ def parse():
                          "2 = cache write + decode attention at B=32; 4 = DVR verify pass; "
                          "5 = continuous-batching stress")
     ap.add_argument("--stress-requests", type=int, default=512)
+    ap.add_argument("--headline-only", action="store_true",
+                    help="config 3 only: skip the other BASELINE configs' figures that the "
+                         "default run attaches under other_configs")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one 256 MiB device-to-device copy (known bytes) so that "
                          "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE readings can be scaled")
@@ -422,6 +425,23 @@ def main():
         "gemms": gemms,
         "cpu_baseline": base,
     }
+    if not args.headline_only:
+        # The other BASELINE configs, measured in the same run (each its own workload, after
+        # the headline's is freed): 1 and 2 decode-attention ops with rooflines and CPU
+        # baselines, 4 the DVR verify pass, 5 continuous batching in the three modes.
+        import gc
+        import bench_configs
+        del wl
+        gc.collect()
+        torch.cuda.empty_cache()
+        others = {}
+        for n in (1, 2, 4, 5):
+            args.config = n
+            others[str(n)] = bench_configs.run(args)
+            gc.collect()
+            torch.cuda.empty_cache()
+        args.config = 3
+        out["other_configs"] = others
     print(json.dumps(out), flush=True)
 
 

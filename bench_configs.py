@@ -240,8 +240,22 @@ def config4(args):
     def one():
         runner.step(fb)
     us = _time_us(one, reps=20, warm=3, graph=False)  # runner.step replays its own graph
+    # Algorithmic bytes of a pass: every weight once (28 layers + the tied lm_head) and each
+    # sequence's K/V rows once per layer (2 x 8 heads x 128 x 2 B per token).
+    mcfg = runner.mcfg
+    w_bytes = sum(t.numel() * t.element_size() for lw in runner.model.w["layers"]
+                  for k_, t in lw.items()) + runner.model.w["lm_head"].numel() * 2
+    kv_tokens = int(fb.kv_indptr[-1].item())
+    kv_bytes = mcfg.num_layers * kv_tokens * mcfg.num_kv_heads * mcfg.head_dim * 2 * 2
+    pass_bytes = w_bytes + kv_bytes
     return {"metric": "DVR verify pass (G=4 x W=32 over 2048-token prefixes) (config 4)",
             "value": round(us / 1e3, 3), "unit": "ms/pass", "higher_is_better": False,
+            "roofline": {"bound": "hbm", "achieved": round(pass_bytes / us / 1e3, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(pass_bytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                         "traffic": None, "kernel": "whole verify pass (native executor)",
+                         "bytes_per_launch": int(pass_bytes), "weight_bytes": int(w_bytes),
+                         "kv_bytes": int(kv_bytes)},
             "verify_tokens_per_s": round(128 / (us * 1e-6), 1),
             "sha256_watched_by_decode_width": hashes,
             "sha256_identical": len(set(hashes.values())) == 1,
