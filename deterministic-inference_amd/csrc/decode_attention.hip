@@ -48,6 +48,16 @@ __host__ __device__ __forceinline__ int kv_per_split(int seq_len, int n_splits, 
   return ceil_div(ceil_div(seq_len, n_splits), HEUR_TILE) * HEUR_TILE;
 }
 
+// The split count of a request when the caller passes no num_splits array: the reference's
+// policies restated on the device (sid/kernels/decode_attention.py:65-85): fixed-size splits
+// cover the sequence, the heuristic takes one split per 32 tokens up to the grid's split
+// count. A request without tokens gets 0 (its output is zeros).
+__device__ __forceinline__ int derived_splits(int seq_len, int max_splits, int fixed_split) {
+  if (seq_len <= 0) return 0;
+  if (fixed_split > 0) return ceil_div(seq_len, fixed_split);
+  return min(ceil_div(seq_len, HEUR_TILE), max_splits);
+}
+
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a),
                                          __builtin_bit_cast(bf16x2_v, b), c, false);
@@ -126,7 +136,7 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ kv_indptr,
     const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ num_splits,
-    int fixed_split, int seg, float sm_scale, int64_t num_slots, int part_stride,
+    int max_splits, int fixed_split, int seg, float sm_scale, int64_t num_slots, int part_stride,
     float* __restrict__ part_o, float* __restrict__ part_lse, bf16_t* __restrict__ o_direct,
     const int32_t* __restrict__ wg_order) {
   constexpr int IT = NW * TPL;  // tokens per workgroup iteration
@@ -151,7 +161,8 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
 
   const int kv_base = kv_indptr[b];
   const int seq_len = kv_indptr[b + 1] - kv_base;
-  const int n_splits = num_splits[b];
+  const int n_splits = num_splits != nullptr ? num_splits[b]
+                                             : derived_splits(seq_len, max_splits, fixed_split);
 
   __shared__ float s_m[NW][HQ];
   __shared__ float s_l[NW][HQ];
@@ -447,14 +458,14 @@ constexpr int kNumVariants = 4;
 
 int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
-                  int batch, int64_t num_slots, int fixed_split_size, int seg, int grid_slots,
-                  float sm_scale, float* part_o, float* part_lse, int part_stride, void* o,
+                  int max_splits, int batch, int64_t num_slots, int fixed_split_size, int seg,
+                  int grid_slots, float sm_scale, float* part_o, float* part_lse, int part_stride, void* o,
                   int variant, const int32_t* wg_order, hipStream_t s) {
   const bool direct = (grid_slots == 1);
   auto stage1 = [&](auto kern, int nw) {
     hipLaunchKernelGGL(kern, dim3(batch, grid_slots), dim3(nw * 64), 0, s, (const bf16_t*)q,
                        (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr, kv_indices,
-                       num_splits, fixed_split_size, seg, sm_scale, num_slots, part_stride, part_o,
+                       num_splits, max_splits, fixed_split_size, seg, sm_scale, num_slots, part_stride, part_o,
                        part_lse, direct ? (bf16_t*)o : nullptr, wg_order);
   };
   switch (variant) {
@@ -480,7 +491,7 @@ int check_decode_args(const void* q, const void* k_cache, const void* v_cache,
                       const int32_t* num_splits, void* o, int batch, int num_q_heads,
                       int num_kv_heads, int head_dim, int64_t num_slots, int max_splits,
                       int fixed_split_size) {
-  SID_REQUIRE(q && k_cache && v_cache && kv_indptr && kv_indices && num_splits && o,
+  SID_REQUIRE(q && k_cache && v_cache && kv_indptr && kv_indices && o,
               "flash_decode_fwd: null pointer");
   SID_REQUIRE(head_dim == HEAD_DIM, "flash_decode_fwd: head_dim must be %d, got %d", HEAD_DIM,
               head_dim);
@@ -526,8 +537,8 @@ extern "C" int sid_flash_decode_segments_fwd(
                 "(part_batch %d, part_stride %d, batch %d, grid_slots %d)",
                 part_batch, part_stride, batch, grid_slots);
   }
-  return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, batch, num_slots,
-                       fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
+  return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, max_splits, batch,
+                       num_slots, fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
                        part_stride, o, variant, wg_order, static_cast<hipStream_t>(stream));
 }
 
@@ -538,6 +549,7 @@ extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const vo
                                     int max_splits, int fixed_split_size, float sm_scale,
                                     float* part_o, float* part_lse, int part_batch,
                                     int part_stride, void* o, void* stream) {
+  SID_REQUIRE(batch <= 0 || num_splits != nullptr, "flash_decode_fwd: null num_splits");
   // One segment per split: the grid has exactly the reference's max_splits slots.
   return sid_flash_decode_segments_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                        batch, num_q_heads, num_kv_heads, head_dim, num_slots,
@@ -625,7 +637,7 @@ extern "C" int sid_flash_decode_segments_fwd_noalloc(
     part_lse = reinterpret_cast<float*>(base + lse_off);
   }
   // Stage 2 reads only the slots stage 1 wrote in this call, so nothing is cleared.
-  return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, batch, num_slots,
-                       fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
+  return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, max_splits, batch,
+                       num_slots, fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
                        grid_slots, o, variant, wg_order, static_cast<hipStream_t>(stream));
 }

@@ -59,7 +59,7 @@ EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward",
             "sid_flash_decode_noalloc_scratch_bytes", "sid_linear_sample_workspace_bytes",
             *_SIGNATURES)
-ABI_VERSION = 20
+ABI_VERSION = 21
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -72,6 +72,11 @@ def _gpu(t: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> None:
     _check(t.is_contiguous(), f"{name} must be contiguous")
     if dtype is not None:
         _check(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _ptr(t) -> int:
+    """Device address of an optional tensor (0 for None)."""
+    return 0 if t is None else t.data_ptr()
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -131,8 +136,9 @@ class NativeLib:
         _gpu(kv_indptr, "kv_indptr", torch.int32)
         _check(kv_indptr.numel() == b + 1, "kv_indptr must have B+1 entries")
         _gpu(kv_indices, "kv_indices", torch.int32)
-        _gpu(num_splits, "num_splits", torch.int32)
-        _check(num_splits.numel() == b, "num_splits must have B entries")
+        if num_splits is not None:  # None: derived on the device from the lengths
+            _gpu(num_splits, "num_splits", torch.int32)
+            _check(num_splits.numel() == b, "num_splits must have B entries")
         _gpu(part_o, "part_o", torch.float32)
         _gpu(part_lse, "part_lse", torch.float32)
         _check(part_o.dim() == 4 and part_o.shape[1] == hq and part_o.shape[3] == d,
@@ -146,7 +152,7 @@ class NativeLib:
         order = self._order_ptr(wg_order, b * slots)
         self._call("sid_flash_decode_segments_fwd", q.data_ptr(), k_cache.data_ptr(),
                    v_cache.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
-                   num_splits.data_ptr(), b, hq, hkv, d, k_cache.shape[0], int(max_splits),
+                   _ptr(num_splits), b, hq, hkv, d, k_cache.shape[0], int(max_splits),
                    int(fixed_split_size), int(segment_size), slots, int(variant), order,
                    float(sm_scale),
                    part_o.data_ptr(), part_lse.data_ptr(), part_o.shape[0], part_o.shape[2],
@@ -168,15 +174,16 @@ class NativeLib:
         _gpu(kv_indptr, "kv_indptr", torch.int32)
         _check(kv_indptr.numel() == b + 1, "kv_indptr must have B+1 entries")
         _gpu(kv_indices, "kv_indices", torch.int32)
-        _gpu(num_splits, "num_splits", torch.int32)
-        _check(num_splits.numel() == b, "num_splits must have B entries")
+        if num_splits is not None:  # None: derived on the device from the lengths
+            _gpu(num_splits, "num_splits", torch.int32)
+            _check(num_splits.numel() == b, "num_splits must have B entries")
         _gpu(o, "o", torch.bfloat16)
         _check(o.shape == q.shape, "o must have q's shape")
         slots = int(max_splits) if grid_slots is None else int(grid_slots)
         order = self._order_ptr(wg_order, b * slots)
         self._call("sid_flash_decode_segments_fwd_noalloc", q.data_ptr(), k_cache.data_ptr(),
                    v_cache.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
-                   num_splits.data_ptr(), b, hq, k_cache.shape[1], d, k_cache.shape[0],
+                   _ptr(num_splits), b, hq, k_cache.shape[1], d, k_cache.shape[0],
                    int(max_splits), int(fixed_split_size), int(segment_size), slots,
                    int(variant), order, float(sm_scale), o.data_ptr(), _stream(q))
 

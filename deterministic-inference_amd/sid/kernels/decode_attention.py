@@ -333,23 +333,23 @@ class DecodeAttention:
 
     def plan(self, seq_lens: torch.Tensor, max_seq_len: int, invariant: bool,
              policy_batch: int | None = None, geometry: tuple | None = None):
-        """(num_splits int32 [B] on device, grid splits, fixed split size, segment size,
-        grid slots). max_seq_len bounds every request's length (host-side, no sync);
-        policy_batch: the real request count when seq_lens has padding rows; geometry: the
+        """(num_splits, grid splits, fixed split size, segment size, grid slots).
+        num_splits is None: the kernel derives each request's split count from its length
+        (ceil(len / fixed split) for fixed splits, min(ceil(len / 32), grid splits) for the
+        heuristic), so a step launches no elementwise kernels for it. max_seq_len bounds
+        every request's length (host-side, no sync); policy_batch: the real request count when seq_lens has padding rows; geometry: the
         nondet (grid splits, segment size, grid slots) chosen by plan_variant, if any."""
         bs = seq_lens.shape[0] if policy_batch is None else int(policy_batch)
         max_len = max(int(max_seq_len), 1)
         if invariant:
             tile = self.invariant_split_size
-            num_splits = ((seq_lens + tile - 1) // tile).to(torch.int32)
             grid = max(1, -(-max_len // tile))
-            return num_splits, grid, tile, tile, grid
+            return None, grid, tile, tile, grid
         if geometry is None:
             geometry = nondet_geometry(bs, max_len, self.num_kv_heads, self.cu_count(),
                                        self.max_kv_splits)
         splits, seg, slots = geometry
-        num_splits = torch.clamp((seq_lens + 31) // 32, max=splits).to(torch.int32)
-        return num_splits, splits, 0, seg, slots
+        return None, splits, 0, seg, slots
 
     def forward(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, seq_lens: torch.Tensor,

@@ -95,7 +95,12 @@ int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache
  * b + batch * y. It changes which workgroup runs which segment, never the
  * result (a heaviest-first order balances ragged batches over the CUs);
  * entries outside the grid are skipped, so a map that is not a permutation
- * leaves partials unwritten (ABI 15).
+ * leaves partials unwritten (ABI 15). num_splits may be NULL here (not in
+ * sid_flash_decode_fwd): each request's split count is then derived on the
+ * device from its length, ceil(len / fixed_split_size) for fixed splits,
+ * else min(ceil(len / 32), max_splits), the values the reference's policies
+ * give (sid/kernels/decode_attention.py:65-85), with no host-side or
+ * elementwise kernel to compute them (ABI 21).
  */
 int sid_flash_decode_segments_fwd(const void* q, const void* k_cache, const void* v_cache,
                                   const int32_t* kv_indptr, const int32_t* kv_indices,

@@ -190,6 +190,30 @@ def test_workgroup_order_does_not_change_bits(policy):
     assert_close_bf16(o, decode_attention_ref(q, k, v, indptr, idx, SCALE))
 
 
+@pytest.mark.parametrize("policy", ["heuristic", "fixed256", "splits8"])
+def test_device_derived_split_counts_equal_explicit(policy):
+    """num_splits = None: the kernel derives each request's split count from its length
+    (the reference's policies); bitwise the same output as the explicit array, empty
+    requests included."""
+    ext = _ext()
+    lens = [1, 31, 32, 33, 255, 257, 1000, 0, 4097, 64]
+    q, k, v, indptr, idx = decode_inputs(lens, seed=17)
+    ns, grid, fixed = _policy(lens, policy)  # the oracle's split counts
+    slots = _slots(lens, ns, fixed, 64)
+    want = _run(q, k, v, indptr, idx, ns, grid, fixed, seg=64, slots=slots)
+    part_o = torch.full((len(lens), HQ, slots, D), float("nan"), device="cuda")
+    part_lse = torch.full((len(lens), HQ, slots), float("nan"), device="cuda")
+    got = torch.empty_like(q)
+    ext.flash_decode_fwd(q, k, v, indptr, idx, None, grid, fixed, SCALE, part_o, part_lse, got,
+                         segment_size=64, grid_slots=slots)
+    assert torch.equal(got, want)
+    assert (got[7] == 0).all()
+    got2 = torch.empty_like(q)
+    ext.flash_decode_fwd_noalloc(q, k, v, indptr, idx, None, grid, fixed, SCALE, got2,
+                                 segment_size=64, grid_slots=slots)
+    assert torch.equal(got2, want)
+
+
 def test_direct_single_split_equals_two_stage():
     """Grid 1 writes o directly; a grid of 2 with every request on one split runs the
     merge pass. Both must give the same bits (merge of one split is the identity)."""
