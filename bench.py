@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--headline-only", action="store_true",
                     help="config 3 only: skip the other BASELINE configs' figures that the "
                          "default run attaches under other_configs")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="config 4: time the verify pass alone (skip the decode-width token "
+                         "comparison), e.g. for a kernel profile of the pass")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one 256 MiB device-to-device copy (known bytes) so that "
                          "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE readings can be scaled")
@@ -310,27 +313,46 @@ def cpu_model() -> str:
 
 
 def gemm_report(wl):
-    """The decode step's projections at its real shape (M = batch rows) with their weights
-    coming from HBM: the four projections of every layer run in the step's order (qkv, o,
-    gate_up with its SwiGLU epilogue, down) over all 28 layers' weights, 880 MB, more than the
-    256 MB last-level cache holds, captured in one HIP graph and timed with HIP events around
-    a replay. A projection's figure is the chain's time minus the time of the same chain
-    without it, per layer: its in-chain cost, launch boundary included. The lm_head (311 MB,
-    also larger than the cache) is timed alone, with its greedy argmax finalize. MFMA rate is
-    against the bf16 dense peak, weight-read rate against HBM; at M = 64 the projections are
+    """The decode step's non-attention kernels at its real shape (M = batch rows) with their
+    weights coming from HBM: the decode chain of every layer in the step's order (input norm
+    + qkv + q/k-norm + RoPE + KV write; o + residual; post-attention norm + gate_up + SwiGLU;
+    down + residual) over all 28 layers' packed weights, 880 MB, more than the 256 MB
+    last-level cache holds, captured in one HIP graph and timed with HIP events around a
+    replay. A kernel's figure is the chain's time minus the time of the same chain without
+    it, per layer: its in-chain cost, launch boundary included. The lm_head (311 MB, also
+    larger than the cache) is timed alone, with its greedy argmax finalize. MFMA rate is
+    against the bf16 dense peak, weight-read rate against HBM; at M = 64 these kernels are
     bound by latency, not by either."""
     torch = wl.torch
-    from sid.kernels.matmul_persistent import linear_argmax, linear_partials, linear_silu_mul
-    w = wl.runner.model.w
+    from sid.kernels.matmul_persistent import linear_argmax
+    from sid.kernels.ops import linear_residual, rmsnorm_linear_silu_mul, rmsnorm_qkv_post
+    model = wl.runner.model
+    cfg = model.cfg
+    w = model.w
     layers = w["layers"]
+    packed = model._packed_weights()
     m = len(wl.reqs)
     g = torch.Generator(device="cuda").manual_seed(7)
     xs = {k: torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
-          for k in (1024, 2048, 3072)}
-    ops = {"qkv": lambda lw: linear_partials(xs[1024], lw["qkv"]),
-           "o": lambda lw: linear_partials(xs[2048], lw["o"]),
-           "gate_up+silu": lambda lw: linear_silu_mul(xs[1024], lw["gate_up"]),
-           "down": lambda lw: linear_partials(xs[3072], lw["down"])}
+          for k in (2048, 3072)}
+    residual = torch.randn(m, 1024, device="cuda", generator=g).to(torch.bfloat16)
+    r32 = torch.randn(m, 1024, device="cuda", generator=g)
+    r32_in = r32.clone()
+    pos = torch.arange(m, device="cuda") + 2048
+    slots = torch.arange(m, device="cuda")
+    k_pool = torch.zeros(m, cfg.num_kv_heads, cfg.head_dim, device="cuda", dtype=torch.bfloat16)
+    v_pool = torch.zeros_like(k_pool)
+    eps = cfg.rms_norm_eps
+    ops = {
+        "qkv (norm + q/k-norm + RoPE + KV write)": lambda lw, pw: rmsnorm_qkv_post(
+            r32_in, lw["input_ln"], eps, pw["qkv"], lw["q_norm"], lw["k_norm"], pos,
+            model.rope.cos_sin, slots, k_pool, v_pool, cfg.num_q_heads),
+        "o (+ residual)": lambda lw, pw: linear_residual(xs[2048], pw["o"], residual, r32),
+        "gate_up (norm + SwiGLU)": lambda lw, pw: rmsnorm_linear_silu_mul(
+            r32_in, lw["post_ln"], eps, pw["gate_up"]),
+        "down (+ residual)": lambda lw, pw: linear_residual(xs[3072], pw["down"], residual, r32),
+    }
+    weights = dict(zip(ops, ("qkv", "o", "gate_up", "down")))
 
     def timed(fn, reps=1):
         for _ in range(2):
@@ -354,20 +376,20 @@ def gemm_report(wl):
 
     def chain(skip=None):
         def run():
-            for lw in layers:
+            for lw, pw in zip(layers, packed):
                 for name, op in ops.items():
                     if name != skip:
-                        op(lw)
+                        op(lw, pw)
         return timed(run)
 
     full = chain()
     out = {}
-    for name, wt in (("qkv", layers[0]["qkv"]), ("o", layers[0]["o"]),
-                     ("gate_up+silu", layers[0]["gate_up"]), ("down", layers[0]["down"])):
+    for name in ops:
         us = (full - chain(skip=name)) / len(layers)
-        out[name] = (wt.shape, us)
+        out[name] = (layers[0][weights[name]].shape, us)
     lm = w["lm_head"]
-    out["lm_head+argmax"] = (lm.shape, timed(lambda: linear_argmax(xs[1024], lm), reps=20))
+    x1024 = torch.randn(m, 1024, device="cuda", generator=g).to(torch.bfloat16)
+    out["lm_head+argmax"] = (lm.shape, timed(lambda: linear_argmax(x1024, lm), reps=20))
     shapes = {}
     for name, ((n, k), us) in out.items():
         flops = 2 * m * n * k
@@ -378,9 +400,9 @@ def gemm_report(wl):
                         "hbm_frac": round(n * k * 2 / us / 1e3 / HBM_PEAK_GBS, 4)}
     return {"peak_bf16_tflops": MFMA_BF16_PEAK_TFLOPS, "peak_hbm_GBps": HBM_PEAK_GBS,
             "chain_us_per_layer": round(full / len(layers), 2),
-            "note": "weights from HBM: the 28 layers' projections in step order (880 MB per "
-                    "pass); per-projection figures are in-chain costs (chain minus chain "
-                    "without it), launch boundaries included",
+            "note": "weights from HBM: the 28 layers' decode chains in step order (880 MB of "
+                    "packed weights per pass); per-kernel figures are in-chain costs (chain "
+                    "minus chain without it), launch boundaries included",
             "shapes": shapes}
 
 
