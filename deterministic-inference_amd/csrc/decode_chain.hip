@@ -189,48 +189,62 @@ __device__ __forceinline__ bf16x8_v a_frag(const char* tile, int row, int c, int
 
 // ---- projection + residual add ------------------------------------------------------------
 //
-// y = x w^T for a 16-row x 16-column tile over K = 256 NCH: wave c stages chunk c of the x
-// rows and loads chunk c of the packed w block, then accumulates it from zero; the chunk
-// sums meet in LDS and are folded c0 + c1 + ... in order; then r = residual + bf16(y)
-// (fp32), residual = bf16(r), r32 = r (in r32 order).
-template <int NCH>
+// y = x w^T for a 16-row x 16 NBW-column tile over K = 256 NCH: wave c stages chunk c of the
+// x rows and loads chunk c of the NBW packed w blocks, then accumulates each block from zero;
+// the chunk sums meet in LDS and are folded c0 + c1 + ... in order; then
+// r = residual + bf16(y) (fp32), residual = bf16(r), r32 = r (in r32 order).
+// These kernels are bound by the bytes each workgroup pulls through its CU's L2 port (time
+// ~ 3 us + per-CU bytes / ~55 GB/s, measured), so at 128 rows a workgroup takes 32 columns
+// (NBW = 2): the staged rows then serve twice the weight bytes, and the CUs pull 25% fewer
+// bytes than with two 16-column workgroups each.
+template <int NCH, int NBW>
 __global__ void __launch_bounds__(NCH * 64) linear_residual_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ wpk,
     bf16_t* __restrict__ residual, float* __restrict__ r32, int M, int N, int R) {
-  constexpr int SS = 17;  // LDS row stride of a chunk tile (floats)
-  __shared__ float sacc[NCH][16 * SS];
+  constexpr int COLS = 16 * NBW;
+  constexpr int SS = COLS + 1;  // LDS row stride of a chunk tile (floats)
+  static_assert(16 * SS * 4 <= 8192, "a chunk-sum tile must fit its wave's staging region");
+  // Wave c's chunk sums overwrite its own staged rows once they are in registers.
   __shared__ __align__(16) char stage[NCH][8192];
+  auto sacc = [&](int c) { return reinterpret_cast<float*>(stage[c]); };
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   int tile, rg;
-  xcd_tile(blockIdx.x, N / 16, R, tile, rg);
-  const int n0 = tile * 16;
+  xcd_tile(blockIdx.x, N / COLS, R, tile, rg);
+  const int n0 = tile * COLS;
   const int m0 = rg * 16;
   stage_tile(stage[wave], x, ldx, m0, M - 1, static_cast<int64_t>(wave) * KC, lane);
-  bf16x8_v xf[NSTEP], wf[NSTEP];
-  packed_load(wf, wpk, tile, wave, NCH, lane);
+  bf16x8_v xf[NSTEP], wf[NBW][NSTEP];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) packed_load(wf[j], wpk, tile * NBW + j, wave, NCH, lane);
   wait_loads();
   staged_frags(xf, stage[wave], lane);
-  f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int s = 0; s < NSTEP; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[s], wf[s], acc, 0, 0, 0);
-  // Lane holds rows 4 g + i of column r.
   const int r = lane & 15;
   const int g = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sacc[wave][(4 * g + i) * SS + r] = acc[i];
-  __syncthreads();
-  const int erow = threadIdx.x >> 4;
-  const int ecol = threadIdx.x & 15;
-  if (threadIdx.x >= 256 || m0 + erow >= M) return;
-  const int64_t off = static_cast<int64_t>(m0 + erow) * N + n0 + ecol;
-  const bf16_t res = residual[off];
-  float tot = sacc[0][erow * SS + ecol];
+  for (int j = 0; j < NBW; ++j) {
+    f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int c = 1; c < NCH; ++c) tot += sacc[c][erow * SS + ecol];
-  const float rr = bf16_to_f32(res) + round_bf16(tot);
-  residual[off] = f32_to_bf16(rr);
-  r32[static_cast<int64_t>(m0 + erow) * N + r32_pos(n0 + ecol)] = rr;
+    for (int s = 0; s < NSTEP; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[s], wf[j][s], acc, 0, 0, 0);
+    // Lane holds rows 4 g + i of column 16 j + r.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sacc(wave)[(4 * g + i) * SS + 16 * j + r] = acc[i];
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < 16 * COLS; o += NCH * 64) {
+    const int erow = o / COLS;
+    const int ecol = o % COLS;
+    if (m0 + erow >= M) break;  // rows ascend with o
+    const int64_t off = static_cast<int64_t>(m0 + erow) * N + n0 + ecol;
+    const bf16_t res = residual[off];
+    float tot = sacc(0)[erow * SS + ecol];
+#pragma unroll
+    for (int c = 1; c < NCH; ++c) tot += sacc(c)[erow * SS + ecol];
+    const float rr = bf16_to_f32(res) + round_bf16(tot);
+    residual[off] = f32_to_bf16(rr);
+    r32[static_cast<int64_t>(m0 + erow) * N + r32_pos(n0 + ecol)] = rr;
+  }
 }
 
 // ---- RMSNorm + gate_up projection + SwiGLU ------------------------------------------------
@@ -243,13 +257,19 @@ __global__ void __launch_bounds__(NCH * 64) linear_residual_kernel(
 // and its rows' loads, normalises its rows into the shared A tile, transposes its weight
 // tile; then every wave runs its chunk's MFMAs for all row blocks, and the chunk sums are
 // folded in order in LDS (aliasing the transposition scratch, dead by then).
-template <int PL, bool F32, int MBS, int NB>
-__global__ void __launch_bounds__(2 * PL * NB * 64) norm_silu_kernel(
+//
+// NBW > 1: each wave owns NBW column blocks of its chunk (NB / NBW waves per chunk), so a
+// workgroup covers NBW times the columns with the same wave count and each normalised row is
+// shared by more weight bytes: at 128 rows (32-row workgroups, 48 gate columns each) the
+// workgroups pull 30% fewer bytes through their CUs' L2 ports than with 24 columns.
+template <int PL, bool F32, int MBS, int NB, int NBW = 1>
+__global__ void __launch_bounds__(2 * PL * (NB / NBW) * 64) norm_silu_kernel(
     const void* __restrict__ src, const uint4* __restrict__ norm_w, float eps,
     const bf16_t* __restrict__ w, bf16_t* __restrict__ out, int M, int inter, int R) {
+  static_assert(NB % NBW == 0, "column blocks per wave must divide the workgroup's");
   constexpr int NCH = 2 * PL;
   constexpr int H = 512 * PL;
-  constexpr int NW = NCH * NB;
+  constexpr int NW = NCH * (NB / NBW);
   constexpr int ROWS = 16 * MBS;
   constexpr int SS = 16 * NB + 1;    // LDS row stride of a chunk-sum tile (floats)
   constexpr int RPW = (ROWS + NW - 1) / NW;
@@ -260,7 +280,7 @@ __global__ void __launch_bounds__(2 * PL * NB * 64) norm_silu_kernel(
   const int r = lane & 15;
   const int g = lane >> 4;
   const int c = wave % NCH;
-  const int nb = wave / NCH;
+  const int nb0 = (wave / NCH) * NBW;  // first column block of this wave
   int tile, rg;
   xcd_tile(blockIdx.x, inter / (8 * NB), R, tile, rg);
   const int j0 = tile * 8 * NB;
@@ -275,8 +295,10 @@ __global__ void __launch_bounds__(2 * PL * NB * 64) norm_silu_kernel(
     const int row = wave + NW * q;
     if (row < ROWS) norm_row_load<PL, F32>(src, min(m0 + row, M - 1), lane, v[q]);
   }
-  bf16x8_v wf[NSTEP];
-  packed_load(wf, w, static_cast<int64_t>(tile) * NB + nb, c, NCH, lane);
+  bf16x8_v wf[NBW][NSTEP];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j)
+    packed_load(wf[j], w, static_cast<int64_t>(tile) * NB + nb0 + j, c, NCH, lane);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int q = 0; q < RPW; ++q) {
@@ -284,20 +306,29 @@ __global__ void __launch_bounds__(2 * PL * NB * 64) norm_silu_kernel(
     if (row < ROWS) norm_row_store<PL>(v[q], lane, nw, eps, sx, row);
   }
   __syncthreads();
-  f32x4_v acc[MBS];
+  f32x4_v acc[MBS][NBW];
 #pragma unroll
-  for (int mb = 0; mb < MBS; ++mb) acc[mb] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int mb = 0; mb < MBS; ++mb)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[mb][j] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) {
 #pragma unroll
-    for (int mb = 0; mb < MBS; ++mb)
-      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_frag<PL>(sx, 16 * mb + r, c, s, g),
-                                                        wf[s], acc[mb], 0, 0, 0);
+    for (int mb = 0; mb < MBS; ++mb) {
+      const bf16x8_v af = a_frag<PL>(sx, 16 * mb + r, c, s, g);
+#pragma unroll
+      for (int j = 0; j < NBW; ++j)
+        acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[j][s], acc[mb][j], 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int mb = 0; mb < MBS; ++mb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sacc[c][(16 * mb + 4 * g + i) * SS + 16 * nb + r] = acc[mb][i];
+    for (int j = 0; j < NBW; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sacc[c][(16 * mb + 4 * g + i) * SS + 16 * (nb0 + j) + r] = acc[mb][j][i];
+    }
   }
   __syncthreads();
   // ROWS x 8 NB outputs, two adjacent gate columns per thread.
@@ -483,20 +514,27 @@ extern "C" int sid_linear_residual(const void* x, int64_t ldx, const void* w, vo
               "linear_residual: K=%lld must be 1024, 2048, 3072 or 4096", (long long)k);
   SID_REQUIRE(ldx >= k && ldx % 8 == 0, "linear_residual: row stride %lld must be >= K and a multiple of 8", (long long)ldx);
   SID_REQUIRE(aligned16(x) && aligned16(w), "linear_residual: operands must be 16-byte aligned");
+#ifndef SID_LR_WIDE_MIN_M
+#define SID_LR_WIDE_MIN_M 96
+#endif
+  const int nbw = m >= SID_LR_WIDE_MIN_M ? 2 : 1;  // 32-column workgroups from 96 rows
   const int64_t R = (m + 15) / 16;
-  SID_REQUIRE(R * (n / 16) < (1ll << 31), "linear_residual: too large");
-  const dim3 grid((unsigned)(R * (n / 16)));
+  SID_REQUIRE(R * (n / (16 * nbw)) < (1ll << 31), "linear_residual: too large");
+  const dim3 grid((unsigned)(R * (n / (16 * nbw))));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   auto go = [&](auto kern, int nch) {
     hipLaunchKernelGGL(kern, grid, dim3(nch * 64), 0, s, (const bf16_t*)x, ldx, (const bf16_t*)w,
                        (bf16_t*)residual, r32, (int)m, (int)n, (int)R);
   };
+#define SID_LR(NCH) \
+  (nbw == 1 ? go(linear_residual_kernel<NCH, 1>, NCH) : go(linear_residual_kernel<NCH, 2>, NCH))
   switch (k) {
-    case 1024: go(linear_residual_kernel<4>, 4); break;
-    case 2048: go(linear_residual_kernel<8>, 8); break;
-    case 3072: go(linear_residual_kernel<12>, 12); break;
-    default: go(linear_residual_kernel<16>, 16); break;
+    case 1024: SID_LR(4); break;
+    case 2048: SID_LR(8); break;
+    case 3072: SID_LR(12); break;
+    default: SID_LR(16); break;
   }
+#undef SID_LR
   return check_launch("linear_residual");
 }
 
@@ -514,9 +552,16 @@ extern "C" int sid_rmsnorm_linear_silu_mul(const void* src, int src_fp32, const 
                   (reinterpret_cast<uintptr_t>(out) & 3) == 0,
               "rmsnorm_linear_silu_mul: misaligned operand");
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  // 16-row workgroups for a handful of rows, 32 rows beyond; from SID_SILU_WIDE_MIN_M rows
+  // each wave takes two column blocks (48 gate columns per workgroup), when they tile inter.
+#ifndef SID_SILU_WIDE_MIN_M
+#define SID_SILU_WIDE_MIN_M 96
+#endif
   const int mbs = m <= 16 ? 1 : 2;
+  const bool wide = mbs == 2 && m >= SID_SILU_WIDE_MIN_M && inter % 48 == 0;
+  const int nb = wide ? 6 : 3;
   const int64_t R = (m + 16 * mbs - 1) / (16 * mbs);
-  const int64_t tiles = inter / 24;
+  const int64_t tiles = inter / (8 * nb);
   SID_REQUIRE(R * tiles < (1ll << 31), "rmsnorm_linear_silu_mul: too large");
   const dim3 grid((unsigned)(R * tiles));
   auto go = [&](auto kern, int pl) {
@@ -525,13 +570,13 @@ extern "C" int sid_rmsnorm_linear_silu_mul(const void* src, int src_fp32, const 
   };
   const int pl = static_cast<int>(hidden / 512);
   const bool f = src_fp32 != 0;
-#define SID_NS(PL, F, MB) go(norm_silu_kernel<PL, F, MB, 3>, PL)
+#define SID_NS(PL, F)                                                            \
+  (mbs == 1 ? go(norm_silu_kernel<PL, F, 1, 3>, PL)                             \
+            : (wide ? go(norm_silu_kernel<PL, F, 2, 6, 2>, PL) : go(norm_silu_kernel<PL, F, 2, 3>, PL)))
   if (pl == 1) {
-    if (f) { if (mbs == 1) SID_NS(1, true, 1); else SID_NS(1, true, 2); }
-    else { if (mbs == 1) SID_NS(1, false, 1); else SID_NS(1, false, 2); }
+    if (f) SID_NS(1, true); else SID_NS(1, false);
   } else {
-    if (f) { if (mbs == 1) SID_NS(2, true, 1); else SID_NS(2, true, 2); }
-    else { if (mbs == 1) SID_NS(2, false, 1); else SID_NS(2, false, 2); }
+    if (f) SID_NS(2, true); else SID_NS(2, false);
   }
 #undef SID_NS
   return check_launch("rmsnorm_linear_silu_mul");

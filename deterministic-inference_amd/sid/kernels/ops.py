@@ -145,7 +145,9 @@ def decode_chain_supported(rows: int, hidden: int, intermediate: int, q_size: in
 # Decode batches up to this many rows take the fused chain; larger ones the split-K /
 # tiled projections with separate norm kernels (identical bits either way). The chain's
 # workgroups re-read their weight tiles once per 16 (32) rows, so large batches favour the
-# tiled GEMMs: 28-layer chain without attention, weights from HBM, graph-timed (us per
-# layer, chain vs split-K path): 32 rows 26.9 vs 30.1, 64: 27.0 vs 36.1, 128: 38.9 vs
-# 45.4, 160: 51.4 vs 50.5, 192: 56.6 vs 49.1, 256: 67.7 vs 53.4.
+# tiled GEMMs. 28-layer chain without attention, weights from HBM, graph-timed (us per
+# layer, chain vs split-K path): 32 rows 26.9 vs 30.1, 64: 27.0 vs 36.1, 128: 31.0 vs 45.4
+# (32-column workgroups from 96 rows). Whole decode steps at 160-256 rows differ by less
+# than 1% either way (160: 7.73 vs 7.77 ms, 192: 8.74 vs 8.69, 256: 11.27 vs 11.39), so the
+# cut stays at 128.
 DECODE_CHAIN_MAX_ROWS = 128
