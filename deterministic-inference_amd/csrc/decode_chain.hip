@@ -273,8 +273,12 @@ __global__ void __launch_bounds__(2 * PL * (NB / NBW) * 64) norm_silu_kernel(
   constexpr int ROWS = 16 * MBS;
   constexpr int SS = 16 * NB + 1;    // LDS row stride of a chunk-sum tile (floats)
   constexpr int RPW = (ROWS + NW - 1) / NW;
-  __shared__ __align__(16) char sx[ROWS * 2 * H];
-  __shared__ float sacc[NCH][ROWS * SS];
+  // The chunk sums reuse the A tile's LDS once every wave's MFMAs are done with it.
+  constexpr int kSx = ROWS * 2 * H;
+  constexpr int kSacc = NCH * ROWS * SS * 4;
+  __shared__ __align__(16) char smem[kSx > kSacc ? kSx : kSacc];
+  char* sx = smem;
+  auto sacc = [&](int k) { return reinterpret_cast<float*>(smem) + k * ROWS * SS; };
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
@@ -321,13 +325,14 @@ __global__ void __launch_bounds__(2 * PL * (NB / NBW) * 64) norm_silu_kernel(
         acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[j][s], acc[mb][j], 0, 0, 0);
     }
   }
+  __syncthreads();  // the A tile is dead from here on
 #pragma unroll
   for (int mb = 0; mb < MBS; ++mb) {
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        sacc[c][(16 * mb + 4 * g + i) * SS + 16 * (nb0 + j) + r] = acc[mb][j][i];
+        sacc(c)[(16 * mb + 4 * g + i) * SS + 16 * (nb0 + j) + r] = acc[mb][j][i];
     }
   }
   __syncthreads();
@@ -342,12 +347,12 @@ __global__ void __launch_bounds__(2 * PL * (NB / NBW) * 64) norm_silu_kernel(
     float y[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      float gs = sacc[0][base + e];
-      float us = sacc[0][base + 8 + e];
+      float gs = sacc(0)[base + e];
+      float us = sacc(0)[base + 8 + e];
 #pragma unroll
       for (int k = 1; k < NCH; ++k) {
-        gs += sacc[k][base + e];
-        us += sacc[k][base + 8 + e];
+        gs += sacc(k)[base + e];
+        us += sacc(k)[base + 8 + e];
       }
       y[e] = silu_mul1(round_bf16(gs), round_bf16(us));
     }
@@ -366,7 +371,9 @@ __global__ void __launch_bounds__(2 * PL * (NB / NBW) * 64) norm_silu_kernel(
 // q_out, k and v to the pools at slots[row] (negative or out-of-range slots skipped).
 constexpr int QD = 128;
 
-template <int PL, bool F32>
+// MBS = 2: 32-row workgroups (each weight fragment used for two row blocks), for batches
+// whose 16-row grid would not fit the CUs in one round.
+template <int PL, bool F32, int MBS>
 __global__ void __launch_bounds__(512) norm_qkv_kernel(
     const void* __restrict__ src, const uint4* __restrict__ norm_w, float eps,
     const bf16_t* __restrict__ w, int M, int num_q_heads, int num_kv_heads, int R,
@@ -377,8 +384,10 @@ __global__ void __launch_bounds__(512) norm_qkv_kernel(
   constexpr int NCH = 2 * PL;
   constexpr int H = 512 * PL;
   constexpr int YS = QD + 4;
-  __shared__ __align__(16) char sx[16 * 2 * H];
-  __shared__ __align__(16) float sy[16 * YS];
+  constexpr int ROWS = 16 * MBS;
+  constexpr int RPW = ROWS / 8;  // rows each wave normalises
+  __shared__ __align__(16) char sx[ROWS * 2 * H];
+  __shared__ __align__(16) float sy[ROWS * YS];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
@@ -386,26 +395,27 @@ __global__ void __launch_bounds__(512) norm_qkv_kernel(
   const int heads = num_q_heads + 2 * num_kv_heads;
   int head, rg;
   xcd_tile(blockIdx.x, heads, R, head, rg);
-  const int m0 = rg * 16;
+  const int m0 = rg * ROWS;
 
-  // Epilogue operands first (thread t < 256: row t / 16, head lanes t % 16), then the norm
-  // weights and rows, then the weight tiles: each wait covers only what it needs.
+  // Epilogue operands first (thread t < 16 ROWS: row t / 16, head lanes t % 16), then the
+  // norm weights and rows, then the weight tiles: each wait covers only what it needs.
   const int row = threadIdx.x >> 4;
   const int j = threadIdx.x & 15;
+  const bool epi = threadIdx.x < 16 * ROWS;
   const int64_t t = min(m0 + row, M - 1);
-  const bool valid = threadIdx.x < 256 && m0 + row < M;
+  const bool valid = epi && m0 + row < M;
   const bool is_v = head >= num_q_heads + num_kv_heads;
   const bool is_q = head < num_q_heads;
   int64_t slot = -1, pos = -1;
-  if (threadIdx.x < 256) {
+  if (epi) {
     slot = slots[t];
     pos = positions[t];
   }
   uint4 nw[PL];
   norm_w_load<PL>(norm_w, lane, nw);
-  float v[2][PL][8];
+  float v[RPW][PL][8];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) norm_row_load<PL, F32>(src, min(m0 + wave + 8 * q, M - 1), lane, v[q]);
+  for (int q = 0; q < RPW; ++q) norm_row_load<PL, F32>(src, min(m0 + wave + 8 * q, M - 1), lane, v[q]);
   bf16x8_v wf[NCH][NSTEP];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) packed_load(wf[c], w, static_cast<int64_t>(head) * 8 + wave, c, NCH, lane);
@@ -413,30 +423,33 @@ __global__ void __launch_bounds__(512) norm_qkv_kernel(
   // The rotary table row depends on the position: its loads go out once that one is back,
   // with everything issued after it still in flight.
   QkRopeIn in;
-  if (threadIdx.x < 256 && !is_v)
-    qk_rope_load(in, j, is_q ? q_norm : k_norm, pos, cos_sin, max_positions);
+  if (epi && !is_v) qk_rope_load(in, j, is_q ? q_norm : k_norm, pos, cos_sin, max_positions);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int q = 0; q < 2; ++q) norm_row_store<PL>(v[q], lane, nw, eps, sx, wave + 8 * q);
+  for (int q = 0; q < RPW; ++q) norm_row_store<PL>(v[q], lane, nw, eps, sx, wave + 8 * q);
   __syncthreads();
-  f32x4_v tot;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int mb = 0; mb < MBS; ++mb) {
+    f32x4_v tot;
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_frag<PL>(sx, r, c, s, g), wf[c][s], acc, 0, 0, 0);
-    if (c == 0) {
-      tot = acc;
-    } else {
+    for (int c = 0; c < NCH; ++c) {
+      f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) tot[i] += acc[i];
+      for (int s = 0; s < NSTEP; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_frag<PL>(sx, 16 * mb + r, c, s, g),
+                                                      wf[c][s], acc, 0, 0, 0);
+      if (c == 0) {
+        tot = acc;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tot[i] += acc[i];
+      }
     }
-  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sy[(4 * g + i) * YS + 16 * wave + r] = round_bf16(tot[i]);
+    for (int i = 0; i < 4; ++i) sy[(16 * mb + 4 * g + i) * YS + 16 * wave + r] = round_bf16(tot[i]);
+  }
   __syncthreads();
-  if (threadIdx.x >= 256) return;
+  if (!epi) return;
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = sy[row * YS + 8 * j + e];
@@ -508,6 +521,12 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // per CU through L2; measured per layer at 96 rows 36.8 -> 31.1 us, at 128 37.2 -> 31.0; at
 // 64 rows the halved workgroup count loses, 26.7 -> 30.6).
 constexpr int64_t kWideMinRows = 96;
+// Above 128 rows the 16-row qkv workgroups (and the 32-column o / down ones) number more than
+// the CUs hold at once, so the qkv workgroups take 32 rows and the o / down ones 64 columns:
+// per layer at 192 rows qkv 14.7 -> 11.9 us, down 12.9 -> 9.8; at 256 the chain 52.9 ->
+// 45.4 us.
+constexpr int64_t kQkvWideAboveRows = 128;
+constexpr int64_t kXWideAboveRows = 128;
 
 extern "C" int sid_linear_residual(const void* x, int64_t ldx, const void* w, void* residual,
                                    float* r32, int64_t m, int64_t n, int64_t k, void* stream) {
@@ -519,7 +538,8 @@ extern "C" int sid_linear_residual(const void* x, int64_t ldx, const void* w, vo
               "linear_residual: K=%lld must be 1024, 2048, 3072 or 4096", (long long)k);
   SID_REQUIRE(ldx >= k && ldx % 8 == 0, "linear_residual: row stride %lld must be >= K and a multiple of 8", (long long)ldx);
   SID_REQUIRE(aligned16(x) && aligned16(w), "linear_residual: operands must be 16-byte aligned");
-  const int nbw = m >= kWideMinRows ? 2 : 1;  // 32-column workgroups from 96 rows
+  // 32-column workgroups from 96 rows, 64-column ones above kXWideAboveRows.
+  const int nbw = m > kXWideAboveRows && n % 64 == 0 && k <= 3072 ? 4 : m >= kWideMinRows ? 2 : 1;
   const int64_t R = (m + 15) / 16;
   SID_REQUIRE(R * (n / (16 * nbw)) < (1ll << 31), "linear_residual: too large");
   const dim3 grid((unsigned)(R * (n / (16 * nbw))));
@@ -528,13 +548,16 @@ extern "C" int sid_linear_residual(const void* x, int64_t ldx, const void* w, vo
     hipLaunchKernelGGL(kern, grid, dim3(nch * 64), 0, s, (const bf16_t*)x, ldx, (const bf16_t*)w,
                        (bf16_t*)residual, r32, (int)m, (int)n, (int)R);
   };
-#define SID_LR(NCH) \
-  (nbw == 1 ? go(linear_residual_kernel<NCH, 1>, NCH) : go(linear_residual_kernel<NCH, 2>, NCH))
+#define SID_LR(NCH)                                                               \
+  (nbw == 1 ? go(linear_residual_kernel<NCH, 1>, NCH)                               \
+            : nbw == 2 ? go(linear_residual_kernel<NCH, 2>, NCH) : go(linear_residual_kernel<NCH, 4>, NCH))
   switch (k) {
     case 1024: SID_LR(4); break;
     case 2048: SID_LR(8); break;
     case 3072: SID_LR(12); break;
-    default: SID_LR(16); break;
+    default:
+      if (nbw == 1) go(linear_residual_kernel<16, 1>, 16); else go(linear_residual_kernel<16, 2>, 16);
+      break;
   }
 #undef SID_LR
   return check_launch("linear_residual");
@@ -602,7 +625,9 @@ extern "C" int sid_rmsnorm_qkv_post(const void* src, int src_fp32, const void* n
   SID_REQUIRE(aligned16(src) && aligned16(norm_w) && aligned16(w_qkv) && aligned16(q_out) &&
                   aligned16(k_cache) && aligned16(v_cache),
               "rmsnorm_qkv_post: operands must be 16-byte aligned");
-  const int64_t R = (m + 15) / 16;
+  // 32-row workgroups once 16-row ones would take more than one round of the CUs.
+  const int mbs = m > kQkvWideAboveRows ? 2 : 1;
+  const int64_t R = (m + 16 * mbs - 1) / (16 * mbs);
   const int heads = num_q_heads + 2 * num_kv_heads;
   SID_REQUIRE(R * heads < (1ll << 31), "rmsnorm_qkv_post: too large");
   const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -614,11 +639,14 @@ extern "C" int sid_rmsnorm_qkv_post(const void* src, int src_fp32, const void* n
                        max_positions, slots, (uint4*)q_out, (uint4*)k_cache, (uint4*)v_cache,
                        num_slots);
   };
+#define SID_NQ(PL, F) \
+  (mbs == 1 ? go(norm_qkv_kernel<PL, F, 1>) : go(norm_qkv_kernel<PL, F, 2>))
   if (hidden == 512) {
-    if (src_fp32) go(norm_qkv_kernel<1, true>); else go(norm_qkv_kernel<1, false>);
+    if (src_fp32) SID_NQ(1, true); else SID_NQ(1, false);
   } else {
-    if (src_fp32) go(norm_qkv_kernel<2, true>); else go(norm_qkv_kernel<2, false>);
+    if (src_fp32) SID_NQ(2, true); else SID_NQ(2, false);
   }
+#undef SID_NQ
   return check_launch("rmsnorm_qkv_post");
 }
 

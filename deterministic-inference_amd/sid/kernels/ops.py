@@ -147,7 +147,7 @@ def decode_chain_supported(rows: int, hidden: int, intermediate: int, q_size: in
 # workgroups re-read their weight tiles once per 16 (32) rows, so large batches favour the
 # tiled GEMMs. 28-layer chain without attention, weights from HBM, graph-timed (us per
 # layer, chain vs split-K path): 32 rows 26.9 vs 30.1, 64: 27.0 vs 36.1, 128: 31.0 vs 45.4
-# (32-column workgroups from 96 rows). Whole decode steps at 160-256 rows differ by less
-# than 1% either way (160: 7.73 vs 7.77 ms, 192: 8.74 vs 8.69, 256: 11.27 vs 11.39), so the
-# cut stays at 128.
-DECODE_CHAIN_MAX_ROWS = 128
+# (32-column workgroups from 96 rows); above 128 rows (32-row qkv and 64-column o / down
+# workgroups) whole decode steps: 160 rows 7.83 vs 7.96 ms, 192: 8.57 vs 8.70, 256: 11.12 vs
+# 11.30. Past 256 rows the chain's workgroups outnumber the CUs again.
+DECODE_CHAIN_MAX_ROWS = 256
