@@ -928,12 +928,26 @@ __global__ void __launch_bounds__(256) argmax_finalize_kernel(const float* __res
   const int row = blockIdx.x;
   float v = -INFINITY;
   int ix = 0x7fffffff;
-  for (int wv = threadIdx.x; wv < num_waves; wv += 256) {
-    const float cv = best_val[static_cast<int64_t>(wv) * M + row];
-    const int ci = best_idx[static_cast<int64_t>(wv) * M + row];
-    if (argmax_better(cv, ci, v, ix)) {
-      v = cv;
-      ix = ci;
+  // Eight candidates per thread loaded at once (one round trip for the 2048 waves of the
+  // persistent grid instead of eight); the order is total, so the visiting order is free.
+  constexpr int U = 8;
+  for (int base = threadIdx.x; base < num_waves; base += 256 * U) {
+    float cv[U];
+    int ci[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int wv = base + 256 * u;
+      const bool in = wv < num_waves;
+      const int64_t off = static_cast<int64_t>(in ? wv : 0) * M + row;
+      cv[u] = in ? best_val[off] : -INFINITY;
+      ci[u] = in ? best_idx[off] : 0x7fffffff;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (argmax_better(cv[u], ci[u], v, ix)) {
+        v = cv[u];
+        ix = ci[u];
+      }
     }
   }
   for (int mask = 1; mask < 64; mask <<= 1) {
