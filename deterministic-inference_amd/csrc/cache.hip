@@ -69,8 +69,22 @@ __global__ void __launch_bounds__(256) build_paged_decode_indices_kernel(
   int32_t* table = tables + row * max_pages;
   const int32_t mask = (1 << page_shift) - 1;
   const int last = len - 1;
-  for (int i = threadIdx.x; i < last; i += blockDim.x)
-    kv_indices[start + i] = (table[i >> page_shift] << page_shift) | (i & mask);
+  // Eight positions per thread per pass, their table entries loaded together (one round trip
+  // per 2048 positions instead of one per 256).
+  constexpr int U = 8;
+  for (int i0 = threadIdx.x; i0 < last; i0 += 256 * U) {
+    int32_t pg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + 256 * u;
+      pg[u] = i < last ? table[i >> page_shift] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + 256 * u;
+      if (i < last) kv_indices[start + i] = (pg[u] << page_shift) | (i & mask);
+    }
+  }
   if (threadIdx.x == 0) {
     const int32_t slot = static_cast<int32_t>(new_slots[b]);
     kv_indices[start + last] = slot;
