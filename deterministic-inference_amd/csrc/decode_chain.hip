@@ -213,6 +213,19 @@ __global__ void __launch_bounds__(NCH * 64) linear_residual_kernel(
   xcd_tile(blockIdx.x, N / COLS, R, tile, rg);
   const int n0 = tile * COLS;
   const int m0 = rg * 16;
+  // The epilogue's residual values first (thread t: outputs t, t + 64 NCH, ...), so the
+  // epilogue waits for no further round trip.
+  constexpr int OUTS = 16 * COLS;
+  constexpr int PER = (OUTS + NCH * 64 - 1) / (NCH * 64);
+  // Unconditional loads from clamped (in-bounds) positions: a guarded load would become a
+  // branch that waits for it on the spot.
+  bf16_t resv[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int o = min(static_cast<int>(threadIdx.x) + q * NCH * 64, OUTS - 1);
+    const int erow = min(m0 + o / COLS, M - 1);
+    resv[q] = residual[static_cast<int64_t>(erow) * N + n0 + o % COLS];
+  }
   stage_tile(stage[wave], x, ldx, m0, M - 1, static_cast<int64_t>(wave) * KC, lane);
   bf16x8_v xf[NSTEP], wf[NBW][NSTEP];
 #pragma unroll
@@ -232,12 +245,14 @@ __global__ void __launch_bounds__(NCH * 64) linear_residual_kernel(
     for (int i = 0; i < 4; ++i) sacc(wave)[(4 * g + i) * SS + 16 * j + r] = acc[i];
   }
   __syncthreads();
-  for (int o = threadIdx.x; o < 16 * COLS; o += NCH * 64) {
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int o = threadIdx.x + q * NCH * 64;
     const int erow = o / COLS;
     const int ecol = o % COLS;
-    if (m0 + erow >= M) break;  // rows ascend with o
+    if (o >= OUTS || m0 + erow >= M) break;  // rows ascend with o
     const int64_t off = static_cast<int64_t>(m0 + erow) * N + n0 + ecol;
-    const bf16_t res = residual[off];
+    const bf16_t res = resv[q];
     float tot = sacc(0)[erow * SS + ecol];
 #pragma unroll
     for (int c = 1; c < NCH; ++c) tot += sacc(c)[erow * SS + ecol];
