@@ -15,7 +15,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 HQ, HKV, D, H = 16, 8, 128, 1024
-ROWS = [1, 5, 16, 37, 64, 100, 128, 256]
+ROWS = [1, 5, 16, 37, 64, 100, 128, 161, 200, 256]
 
 
 def _w(n, k, scale=0.03):
@@ -105,7 +105,8 @@ def test_rmsnorm_qkv_post_matches_unfused(t, src_fp32):
 
 
 def test_decode_chain_rows_are_batch_invariant():
-    """A row's chain outputs do not depend on the batch around it (M-invariance)."""
+    """A row's chain outputs do not depend on the batch around it (M-invariance), across the
+    workgroup shapes the row count selects (16/32-column, 32/64-column, 16/32-row)."""
     from sid.kernels.ops import linear_residual, pack_decode_weight, rmsnorm_linear_silu_mul
     torch.manual_seed(3)
     big = torch.randn(200, 3072, device="cuda", dtype=torch.bfloat16)
@@ -121,6 +122,28 @@ def test_decode_chain_rows_are_batch_invariant():
         linear_residual(big[lo:hi].contiguous(), w, r_part, f_part)
         assert torch.equal(r_part, r_all[lo:hi]) and torch.equal(f_part, f_all[lo:hi])
         assert torch.equal(rmsnorm_linear_silu_mul(f_part, nw, 1e-6, wg), act_all[lo:hi])
+    # the qkv kernel (16-row workgroups up to 128 rows, 32-row ones above)
+    from sid.kernels.ops import rmsnorm_qkv_post
+    from sid.kernels.rope import RotaryEmbedding
+    wq = pack_decode_weight(_w((HQ + 2 * HKV) * D, H))
+    qn = (1 + 0.1 * torch.randn(D, device="cuda")).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(D, device="cuda")).to(torch.bfloat16)
+    rope = RotaryEmbedding(D, 4096, 1e6, "cuda")
+    pos = torch.randint(0, 4096, (200,), device="cuda")
+    slots = torch.randperm(400, device="cuda")[:200]
+
+    def qkv(lo, hi):
+        kc = torch.zeros(400, HKV, D, device="cuda", dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        q = rmsnorm_qkv_post(f_all[lo:hi].contiguous(), nw, 1e-6, wq, qn, kn, pos[lo:hi],
+                             rope.cos_sin, slots[lo:hi], kc, vc, HQ)
+        return q, kc[slots[lo:hi]], vc[slots[lo:hi]]
+
+    q_all, k_all, v_all = qkv(0, 200)
+    for lo, hi in ((0, 1), (40, 57), (100, 200), (199, 200)):
+        q, k, v = qkv(lo, hi)
+        assert torch.equal(q, q_all[lo:hi]) and torch.equal(k, k_all[lo:hi])
+        assert torch.equal(v, v_all[lo:hi])
 
 
 def test_pack_decode_weight_layout():
