@@ -194,9 +194,9 @@ __device__ __forceinline__ bf16x8_v a_frag(const char* tile, int row, int c, int
 // the chunk sums meet in LDS and are folded c0 + c1 + ... in order; then
 // r = residual + bf16(y) (fp32), residual = bf16(r), r32 = r (in r32 order).
 // These kernels are bound by the bytes each workgroup pulls through its CU's L2 port (time
-// ~ 3 us + per-CU bytes / ~55 GB/s, measured), so at 128 rows a workgroup takes 32 columns
-// (NBW = 2): the staged rows then serve twice the weight bytes, and the CUs pull 25% fewer
-// bytes than with two 16-column workgroups each.
+// ~ 3 us + per-CU bytes / ~55 GB/s, measured), so from 96 rows a workgroup takes 32 columns
+// (NBW = 2) and above 128 rows 64 (NBW = 4): the staged rows then serve more weight bytes,
+// and the CUs pull 25% fewer bytes than with two 16-column workgroups each.
 template <int NCH, int NBW>
 __global__ void __launch_bounds__(NCH * 64) linear_residual_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ wpk,
@@ -553,8 +553,9 @@ extern "C" int sid_linear_residual(const void* x, int64_t ldx, const void* w, vo
               "linear_residual: K=%lld must be 1024, 2048, 3072 or 4096", (long long)k);
   SID_REQUIRE(ldx >= k && ldx % 8 == 0, "linear_residual: row stride %lld must be >= K and a multiple of 8", (long long)ldx);
   SID_REQUIRE(aligned16(x) && aligned16(w), "linear_residual: operands must be 16-byte aligned");
-  // 32-column workgroups from 96 rows, 64-column ones above kXWideAboveRows.
-  const int nbw = m > kXWideAboveRows && n % 64 == 0 && k <= 3072 ? 4 : m >= kWideMinRows ? 2 : 1;
+  // 32-column workgroups from 96 rows, 64-column ones above kXWideAboveRows (K = 4096 keeps
+  // 32: its 16-wave workgroups would spill with four column blocks).
+  const int nbw = m > kXWideAboveRows && k <= 3072 ? 4 : m >= kWideMinRows ? 2 : 1;
   const int64_t R = (m + 15) / 16;
   SID_REQUIRE(R * (n / (16 * nbw)) < (1ll << 31), "linear_residual: too large");
   const dim3 grid((unsigned)(R * (n / (16 * nbw))));
