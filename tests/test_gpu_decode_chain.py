@@ -104,6 +104,54 @@ def test_rmsnorm_qkv_post_matches_unfused(t, src_fp32):
     assert torch.equal(kc1, kc0) and torch.equal(vc1, vc0)
 
 
+@pytest.mark.parametrize("t", [3, 40, 128])
+def test_hidden_512_chain_matches_unfused(t):
+    """The hidden-512 instantiations (two 256-wide chunks per row): norm + gate_up + SwiGLU
+    against rmsnorm + linear + silu_mul, norm + qkv + post against rmsnorm + linear +
+    qkv_post, and the o-shaped residual projection (K = 1024) against linear +
+    fused_add_rmsnorm, bitwise."""
+    from sid.kernels.matmul_persistent import linear
+    from sid.kernels.ops import (linear_residual, pack_decode_weight, qkv_post, r32_positions,
+                                 rmsnorm_f32, rmsnorm_linear_silu_mul, rmsnorm_qkv_post, silu_mul)
+    from sid.kernels.rmsnorm import fused_add_rmsnorm
+    from sid.kernels.rope import RotaryEmbedding
+    h = 512
+    print(f"hidden 512 t={t}", flush=True)
+    torch.manual_seed(17 + t)
+    nw = (1 + 0.1 * torch.randn(h, device="cuda")).to(torch.bfloat16)
+    # residual projection (K = 1024 -> N = 512) and the fp32 sum it leaves
+    x = torch.randn(t, 1024, device="cuda", dtype=torch.bfloat16)
+    wo = _w(h, 1024)
+    res = torch.randn(t, h, device="cuda", dtype=torch.bfloat16)
+    xn0, r0 = fused_add_rmsnorm(linear(x, wo), res.clone(), nw, 1e-6)
+    r1, r32 = res.clone(), torch.empty(t, h, device="cuda")
+    linear_residual(x, pack_decode_weight(wo), r1, r32)
+    assert torch.equal(r1, r0)
+    assert torch.equal(r32[:, r32_positions(h).cuda()].to(torch.bfloat16), r0)
+    assert torch.equal(rmsnorm_f32(r32, nw, 1e-6), xn0)
+    # norm + gate_up + SwiGLU from that sum
+    wg = _w(2 * 1536, h, 0.05)
+    want = silu_mul(linear(xn0, wg))
+    got = rmsnorm_linear_silu_mul(r32, nw, 1e-6, pack_decode_weight(wg, gate_up=True))
+    assert torch.equal(got, want)
+    # norm + qkv + q/k-norm + RoPE + cache write (8 q heads, 4 kv heads)
+    hq, hkv = 8, 4
+    wq = _w((hq + 2 * hkv) * D, h)
+    qn = (1 + 0.1 * torch.randn(D, device="cuda")).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(D, device="cuda")).to(torch.bfloat16)
+    rope = RotaryEmbedding(D, 4096, 1e6, "cuda")
+    pos = torch.randint(0, 4096, (t,), device="cuda")
+    slots = torch.randperm(300, device="cuda")[:t]
+    kc0 = torch.zeros(300, hkv, D, device="cuda", dtype=torch.bfloat16)
+    vc0 = torch.zeros_like(kc0)
+    q0 = qkv_post(linear(xn0, wq), qn, kn, 1e-6, pos, rope.cos_sin, slots, kc0, vc0, hq)
+    kc1, vc1 = torch.zeros_like(kc0), torch.zeros_like(kc0)
+    q1 = rmsnorm_qkv_post(r32, nw, 1e-6, pack_decode_weight(wq), qn, kn, pos, rope.cos_sin,
+                          slots, kc1, vc1, hq)
+    assert torch.equal(q1, q0)
+    assert torch.equal(kc1, kc0) and torch.equal(vc1, vc0)
+
+
 def test_decode_chain_rows_are_batch_invariant():
     """A row's chain outputs do not depend on the batch around it (M-invariance), across the
     workgroup shapes the row count selects (16/32-column, 32/64-column, 16/32-row)."""
