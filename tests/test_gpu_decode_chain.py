@@ -210,7 +210,7 @@ def test_pack_decode_weight_layout():
         assert torch.equal(p, want)
 
 
-@pytest.mark.parametrize("bs", [1, 13, 64])
+@pytest.mark.parametrize("bs", [1, 13, 64, 100, 200])
 def test_decode_forward_chain_equals_unfused(bs):
     """Whole decode forward (2 layers of the Qwen3-0.6B shape): chain == unfused, bitwise,
     logits and KV pools."""
@@ -246,7 +246,7 @@ def test_decode_forward_chain_equals_unfused(bs):
                       positions=(lens - 1).cuda(), out_slots=out_slots.cuda(),
                       kv_indptr=indptr.cuda(), kv_indices=idx.cuda(),
                       seq_lens=lens.to(torch.int32).cuda(), max_seq_len=int(lens.max()))
-    attn = DecodeAttention(64, HQ, HKV, D, 32, 256, 4096, "cuda")
+    attn = DecodeAttention(max(bs, 64), HQ, HKV, D, 32, 256, 4096, "cuda")
     outs = []
     for chain in (False, True):
         model = Qwen3Model(mcfg, w, "cuda")
