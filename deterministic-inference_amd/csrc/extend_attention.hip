@@ -11,8 +11,9 @@
 // Inside a split a query row runs an online softmax from a fresh state over the
 // split's tiles in order; the split states are then folded into the row's
 // running state in increasing split order by fold(). Tiles and splits beyond a
-// row's position are exact no-ops for it (rescale exp(0) = 1, p = 0, fold
-// weight exp(-1e30 - m) = 0). So a row's bits depend only on its q, its
+// row's position are exact no-ops for it (rescale 2^0 = 1, p = 0, fold
+// weight 2^(-1e30 - m) = 0). States keep their maximum m in log2 units
+// (scores times sm_scale * log2(e)). So a row's bits depend only on its q, its
 // absolute position and its sequence's keys. A launch either walks a query
 // tile's splits sequentially in one workgroup, or (when a workspace is given
 // and the grid would be small, e.g. the 4 x 32 verify pass) gives every split
@@ -27,8 +28,10 @@
 //                   assigned to MFMA rows so that each lane ends up holding 8
 //                   consecutive keys for its query, which is exactly the B
 //                   operand layout of the PV product (no shuffles needed);
-//   softmax       : online, per query row, reductions over the 4 lanes of a
-//                   row by xor 16 / xor 32 (max is order-free, sums commute);
+//   softmax       : online, per query row, with a lazy reference maximum (moved
+//                   only when a tile's maximum exceeds it by 2^8); reductions
+//                   over the 4 lanes of a row by xor 16 / xor 32 (max is
+//                   order-free, sums commute);
 //   O^T += V^T P^T: 8 dim blocks x 2 k-steps, A = V^T from a transposed LDS
 //                   copy of the V tile, B = bf16(P) (P is rounded to bf16
 //                   before the PV product, as sid/kernels/extend_attention.py:106).
@@ -47,6 +50,14 @@ constexpr int KSPLIT = 256;     // keys per split (4 tiles), anchored at positio
 constexpr int KS_STRIDE = D + 24;
 constexpr int VS_STRIDE = D + 24;
 constexpr float NEG_BIG = -1e30f;
+constexpr float LOG2E = 1.4426950408889634f;
+// Slack of the lazy softmax maximum, in log2 units: scores up to 2^LAZY_T above the row's
+// reference maximum are taken without moving it.
+constexpr float LAZY_T = 8.0f;
+
+// 2^x by the hardware instruction (v_exp_f32): the argument is at most LAZY_T, and results
+// that would be denormal may flush to zero.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Reductions over lanes l and l ^ 16 (l ^ 32): v_permlane16/32_swap hand each lane the
 // values of both lanes of its pair as (lower lane's, upper lane's), so both lanes compute
@@ -100,7 +111,7 @@ struct FoldScale {
 };
 __device__ __forceinline__ FoldScale fold_scale(float run_m, float m) {
   const float mn = fmaxf(run_m, m);
-  return {mn, __expf(run_m - mn), __expf(m - mn)};
+  return {mn, exp2_fast(run_m - mn), exp2_fast(m - mn)};
 }
 // Written as one explicit fma over a separately rounded product, so the compiler has no
 // contraction choice to make differently in different kernels.
@@ -127,6 +138,7 @@ struct Ctx {
   int kv_len;
   int h_kv;
   int q_abs;
+  int q_min;
   bool row_ok;
   int r, g, wave, lane, tid;
 };
@@ -177,10 +189,53 @@ __device__ __forceinline__ void store_tile(const TileRegs& r, const Ctx& c, bf16
   }
 }
 
+// Softmax of one tile's scores s (in place: s becomes p), in the exp2 domain:
+// p = 2^(s * sc2 - m) with sc2 = sm_scale * log2(e) and m the row's reference maximum in
+// the same units. The reference maximum is lazy: it moves to the tile's maximum only when
+// that exceeds it by more than LAZY_T, so p <= 2^LAZY_T and most tiles leave it (and the
+// accumulator) alone. Every decision is per row (per lane group), so a row's bits depend
+// on its own scores only. MASK: apply causality and row validity (keys beyond the row's
+// position give p = 0). Returns the accumulator's rescale factor (exactly 1 when the
+// reference maximum stays).
+template <bool MASK>
+__device__ __forceinline__ float softmax_tile(float (&s)[16], RowState& st, const Ctx& c, int t0,
+                                              float sc2) {
+  bool vis[16];
+  float tmax = NEG_BIG;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (MASK) {
+      const int key = t0 + 32 * (i >> 3) + 8 * c.g + (i & 7);
+      vis[i] = (key <= c.q_abs) & c.row_ok;
+      tmax = fmaxf(tmax, vis[i] ? s[i] : NEG_BIG);
+    } else {
+      tmax = fmaxf(tmax, s[i]);
+    }
+  }
+  tmax = pair16_max(tmax);
+  tmax = pair32_max(tmax);
+  const float mc = tmax * sc2;
+  const float m_used = mc > st.m + LAZY_T ? mc : st.m;
+  const float rescale = exp2_fast(st.m - m_used);
+  float psum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float p = exp2_fast(__builtin_fmaf(s[i], sc2, -m_used));
+    if constexpr (MASK) s[i] = vis[i] ? p : 0.0f;
+    else s[i] = p;
+    psum += s[i];
+  }
+  psum = pair16_sum(psum);
+  psum = pair32_sum(psum);
+  st.l = __builtin_fmaf(st.l, rescale, psum);
+  st.m = m_used;
+  return rescale;
+}
+
 // The 64-key tile starting at absolute key t0, already in LDS, folded into `st` (online
 // softmax).
 __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
-                                          const bf16x8_v (&qf)[4], float sm_scale,
+                                          const bf16x8_v (&qf)[4], float sc2,
                                           const bf16_t* sK, const bf16_t* sV) {
   // S^T blocks: lane holds logits of its query for keys 8g..8g+7 (s[0..7]) and
   // 32+8g..32+8g+7 (s[8..15]). MFMA row m of key block j holds key
@@ -200,29 +255,9 @@ __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
     for (int i = 0; i < 4; ++i) s[4 * j + i] = st4[i];
   }
 
-  float tmax = NEG_BIG;
-  bool vis[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int key = t0 + 32 * (i >> 3) + 8 * c.g + (i & 7);
-    vis[i] = c.row_ok && key <= c.q_abs;
-    s[i] = vis[i] ? s[i] * sm_scale : NEG_BIG;
-    tmax = fmaxf(tmax, s[i]);
-  }
-  tmax = pair16_max(tmax);
-  tmax = pair32_max(tmax);
-  const float m_new = fmaxf(st.m, tmax);
-  const float rescale = __expf(st.m - m_new);
-  float psum = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    s[i] = vis[i] ? __expf(s[i] - m_new) : 0.0f;
-    psum += s[i];
-  }
-  psum = pair16_sum(psum);
-  psum = pair32_sum(psum);
-  st.l = st.l * rescale + psum;
-  st.m = m_new;
+  // `full` (wave-uniform): every row of the wave sees every key of the tile, so no mask.
+  const float rescale = t0 + BN - 1 <= c.q_min ? softmax_tile<false>(s, st, c, t0, sc2)
+                                              : softmax_tile<true>(s, st, c, t0, sc2);
 
   bf16x8_v pf[2];
 #pragma unroll
@@ -234,12 +269,19 @@ __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
     u.w = pack_bf16x2(s[8 * kb + 6], s[8 * kb + 7]);
     pf[kb] = __builtin_bit_cast(bf16x8_v, u);
   }
+  // x * 1 == x: the rescale is skipped (same bits) unless some row of the wave moved its
+  // reference maximum.
+  if (__builtin_amdgcn_ballot_w64(rescale != 1.0f) != 0) {
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      st.acc[db][0] *= rescale;
+      st.acc[db][1] *= rescale;
+      st.acc[db][2] *= rescale;
+      st.acc[db][3] *= rescale;
+    }
+  }
 #pragma unroll
   for (int db = 0; db < 8; ++db) {
-    st.acc[db][0] *= rescale;
-    st.acc[db][1] *= rescale;
-    st.acc[db][2] *= rescale;
-    st.acc[db][3] *= rescale;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       // A = V^T rows 16 db + r (dims), columns 32 kb + 8 g .. +7 (keys): lane s of a group
@@ -256,8 +298,10 @@ __device__ __forceinline__ void tile_math(RowState& st, const Ctx& c, int t0,
 
 // Keys [t_begin, t_end) of one split (t_begin = split start, at most KSPLIT keys) folded
 // into `st` tile by tile, with the next tile's loads in flight during each tile's math.
+// (Issuing all of the split's tile loads up front measured slower on the verify fan-out:
+// 20.0 -> 21.6 us per layer.)
 __device__ __forceinline__ void run_tiles(RowState& st, const Ctx& c, int t_begin, int t_end,
-                                          const bf16x8_v (&qf)[4], float sm_scale, bf16_t* sK,
+                                          const bf16x8_v (&qf)[4], float sc2, bf16_t* sK,
                                           bf16_t* sV, int32_t* s_idx) {
   if (t_begin >= t_end) return;
   __syncthreads();  // previous split's tiles done with s_idx
@@ -270,7 +314,7 @@ __device__ __forceinline__ void run_tiles(RowState& st, const Ctx& c, int t_begi
     store_tile(r, c, sK, sV);
     __syncthreads();
     if (t0 + BN < t_end) load_tile(r, c, s_idx, t0 + BN - t_begin);
-    tile_math(st, c, t0, qf, sm_scale, sK, sV);
+    tile_math(st, c, t0, qf, sc2, sK, sV);
   }
 }
 
@@ -316,6 +360,8 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   const int qr = mtile * BQ + 16 * (c.wave & 1) + c.r;  // extend-local query row of this lane
   c.row_ok = qr < extend_len;
   c.q_abs = prefix + qr;
+  c.q_min = prefix + mtile * BQ + 16 * (c.wave & 1);  // the wave's first row
+  const float sc2 = sm_scale * LOG2E;
   c.k_cache = k_cache;
   c.v_cache = v_cache;
   c.idx = kv_indices + kv_start;
@@ -344,7 +390,7 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   if constexpr (FANOUT) {
     RowState st;
     fresh(st);
-    run_tiles(st, c, split * KSPLIT, min(visible_end, (split + 1) * KSPLIT), qf, sm_scale, sK,
+    run_tiles(st, c, split * KSPLIT, min(visible_end, (split + 1) * KSPLIT), qf, sc2, sK,
               sV, s_idx);
     if (!c.row_ok) return;
     const int64_t pr = static_cast<int64_t>(split) * total_q * num_q_heads + prow;
@@ -364,7 +410,7 @@ __global__ void __launch_bounds__(256) extend_attention_kernel(
   for (int sp = 0; sp < nsplits; ++sp) {
     RowState st;
     fresh(st);
-    run_tiles(st, c, sp * KSPLIT, min(visible_end, (sp + 1) * KSPLIT), qf, sm_scale, sK, sV,
+    run_tiles(st, c, sp * KSPLIT, min(visible_end, (sp + 1) * KSPLIT), qf, sc2, sK, sV,
               s_idx);
     fold(run, st.m, st.l, st.acc);
   }

@@ -35,6 +35,13 @@ HIPCC_FLAGS = [
 _ext = None
 
 
+# Per-source extra flags. extend_attention: the MFMA accumulators live in VGPRs (the
+# softmax rescales them with VALU ops, which cannot read AGPRs).
+SOURCE_FLAGS = {
+    "extend_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -56,7 +63,8 @@ def build_library(verbose: bool = False) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = BUILD_DIR / (src.stem + ".o")
-        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), f"-I{INCLUDE_DIR}", "-c",
+               str(src), "-o", str(obj)]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr[-4000:]}")
