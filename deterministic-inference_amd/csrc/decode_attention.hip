@@ -126,31 +126,32 @@ __host__ __device__ __forceinline__ bool segment_range(int seq_len, int n_splits
   return start < end;
 }
 
-// NW waves per workgroup; TPL tokens per wave iteration. The next iteration's slot indices
-// load while this one's rows are in flight (a long segment of a small batch is a chain of
-// iterations: fixed-256 at B = 1, ctx 1024 26.8 -> 23.7 us; no change on full grids). (A
-// software-pipelined variant with the next iteration's rows loading during this one's math
-// doubled the tile registers, lowered occupancy and measured no faster.)
+// LDS of one stage-1 workgroup: the waves' softmax states, then the merge's scales.
+template <int NW>
+struct Stage1Lds {
+  float m[NW][HQ];
+  float l[NW][HQ];
+  float acc[NW][HQ][HEAD_DIM];
+  float sc[NW][HQ];
+  float den[HQ];
+  float mx[HQ];
+};
+
+// The partial attention of request b over partial slot y (a segment of one split), by one
+// workgroup of NW waves taking TPL tokens per wave iteration. Every exit is
+// workgroup-uniform. The next iteration's slot indices load while this one's rows are in
+// flight (a long segment of a small batch is a chain of iterations: fixed-256 at B = 1, ctx
+// 1024 26.8 -> 23.7 us; no change on full grids). (Software-pipelined forms with the next
+// iteration's rows loading during this one's math measured no faster.)
 template <int NW, int TPL>
-__global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
-    const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ kv_indptr,
-    const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ num_splits,
-    int max_splits, int fixed_split, int seg, float sm_scale, int64_t num_slots, int part_stride,
-    float* __restrict__ part_o, float* __restrict__ part_lse, bf16_t* __restrict__ o_direct,
-    const int32_t* __restrict__ wg_order) {
+__device__ __forceinline__ void stage1_item(
+    Stage1Lds<NW>& sh, int b, int y, const bf16_t* __restrict__ q,
+    const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,
+    const int32_t* __restrict__ kv_indptr, const int32_t* __restrict__ kv_indices,
+    const int32_t* __restrict__ num_splits, int max_splits, int fixed_split, int seg,
+    float sm_scale, int64_t num_slots, int part_stride, float* __restrict__ part_o,
+    float* __restrict__ part_lse, bf16_t* __restrict__ o_direct) {
   constexpr int IT = NW * TPL;  // tokens per workgroup iteration
-  // The (request, slot) this workgroup computes: its own grid position, or the entry of
-  // wg_order at its linear id (a permutation of the grid, heaviest segments first; only the
-  // placement changes, not what is computed).
-  int b = blockIdx.x;
-  int y = blockIdx.y;
-  if (wg_order != nullptr) {
-    const int packed = wg_order[blockIdx.x + blockIdx.y * gridDim.x];
-    b = packed >> kOrderSlotBits;
-    y = packed & ((1 << kOrderSlotBits) - 1);
-    if (b >= static_cast<int>(gridDim.x) || y >= static_cast<int>(gridDim.y)) return;
-  }
   const int tid = threadIdx.x;
   // Wave index as a wave-uniform value: token positions derived from it are uniform, so
   // slot indices come in through scalar loads with no per-lane branches.
@@ -164,9 +165,9 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   const int n_splits = num_splits != nullptr ? num_splits[b]
                                              : derived_splits(seq_len, max_splits, fixed_split);
 
-  __shared__ float s_m[NW][HQ];
-  __shared__ float s_l[NW][HQ];
-  __shared__ float s_acc[NW][HQ][HEAD_DIM];
+  auto& s_m = sh.m;
+  auto& s_l = sh.l;
+  auto& s_acc = sh.acc;
 
   const int64_t out_row = static_cast<int64_t>(b) * HQ;
   // A slot with no tokens marks itself empty (log-sum-exp NEG_BIG): every slot below the
@@ -304,9 +305,9 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   // takes the max over the waves, every wave's scale and the denominator once; then each
   // thread folds 4 consecutive dims of one head (128-bit LDS reads), with the same
   // per-output operations in the same order as folding every dim on its own.
-  __shared__ float s_sc[NW][HQ];
-  __shared__ float s_den[HQ];
-  __shared__ float s_mx[HQ];
+  auto& s_sc = sh.sc;
+  auto& s_den = sh.den;
+  auto& s_mx = sh.mx;
   if (tid < HQ) {
     float mx = s_m[0][tid];
 #pragma unroll
@@ -346,6 +347,60 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
       *reinterpret_cast<float4*>(&part_o[prow * HEAD_DIM + d0]) = out;
       if (d0 == 0) part_lse[prow] = s_mx[h] + __logf(den);
     }
+  }
+}
+
+
+// Grid form: workgroup (b, y) of a batch x grid_slots grid, or the entry of wg_order at its
+// linear id (a permutation of the grid, heaviest segments first; only the placement changes,
+// not what is computed).
+template <int NW, int TPL>
+__global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
+    const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ kv_indptr,
+    const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ num_splits,
+    int max_splits, int fixed_split, int seg, float sm_scale, int64_t num_slots, int part_stride,
+    float* __restrict__ part_o, float* __restrict__ part_lse, bf16_t* __restrict__ o_direct,
+    const int32_t* __restrict__ wg_order) {
+  __shared__ Stage1Lds<NW> sh;
+  int b = blockIdx.x;
+  int y = blockIdx.y;
+  if (wg_order != nullptr) {
+    const int packed = wg_order[blockIdx.x + blockIdx.y * gridDim.x];
+    b = packed >> kOrderSlotBits;
+    y = packed & ((1 << kOrderSlotBits) - 1);
+    if (b >= static_cast<int>(gridDim.x) || y >= static_cast<int>(gridDim.y)) return;
+  }
+  stage1_item<NW, TPL>(sh, b, y, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
+                       max_splits, fixed_split, seg, sm_scale, num_slots, part_stride, part_o,
+                       part_lse, o_direct);
+}
+
+// Worker form: `workers` workgroups, worker w computing the items order[w], order[w +
+// workers], order[w + 2 workers], ... of the batch x grid_slots items (order: a permutation
+// of them all, empty slots included, dealt so the workers' token counts balance). Each item
+// is computed exactly as the grid form computes it, so only placement differs: the same bits.
+// Every worker runs a bounded loop over its share and exits.
+template <int NW, int TPL>
+__global__ void __launch_bounds__(NW * 64) decode_stage1_worker_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
+    const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ kv_indptr,
+    const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ num_splits,
+    int max_splits, int fixed_split, int seg, float sm_scale, int64_t num_slots, int part_stride,
+    float* __restrict__ part_o, float* __restrict__ part_lse, const int32_t* __restrict__ order,
+    int batch, int grid_slots) {
+  __shared__ Stage1Lds<NW> sh;
+  const int n_items = batch * grid_slots;
+  for (int i = blockIdx.x; i < n_items; i += gridDim.x) {
+    const int packed = order[i];
+    const int b = packed >> kOrderSlotBits;
+    const int y = packed & ((1 << kOrderSlotBits) - 1);
+    if (b < batch && y < grid_slots) {
+      stage1_item<NW, TPL>(sh, b, y, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
+                           max_splits, fixed_split, seg, sm_scale, num_slots, part_stride,
+                           part_o, part_lse, nullptr);
+    }
+    __syncthreads();  // the item's merge reads of the LDS are done before the next item's writes
   }
 }
 
@@ -460,7 +515,7 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
                   int max_splits, int batch, int64_t num_slots, int fixed_split_size, int seg,
                   int grid_slots, float sm_scale, float* part_o, float* part_lse, int part_stride, void* o,
-                  int variant, const int32_t* wg_order, hipStream_t s) {
+                  int variant, const int32_t* wg_order, int workers, hipStream_t s) {
   const bool direct = (grid_slots == 1);
   auto stage1 = [&](auto kern, int nw) {
     hipLaunchKernelGGL(kern, dim3(batch, grid_slots), dim3(nw * 64), 0, s, (const bf16_t*)q,
@@ -468,11 +523,26 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                        num_splits, max_splits, fixed_split_size, seg, sm_scale, num_slots, part_stride, part_o,
                        part_lse, direct ? (bf16_t*)o : nullptr, wg_order);
   };
-  switch (variant) {
-    case 1: stage1(decode_stage1_kernel<4, 1>, 4); break;
-    case 2: stage1(decode_stage1_kernel<8, 2>, 8); break;
-    case 3: stage1(decode_stage1_kernel<4, 2>, 4); break;
-    default: stage1(decode_stage1_kernel<4, 4>, 4); break;
+  auto worker = [&](auto kern, int nw) {
+    hipLaunchKernelGGL(kern, dim3(workers), dim3(nw * 64), 0, s, (const bf16_t*)q,
+                       (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr, kv_indices,
+                       num_splits, max_splits, fixed_split_size, seg, sm_scale, num_slots,
+                       part_stride, part_o, part_lse, wg_order, batch, grid_slots);
+  };
+  if (workers > 0 && !direct) {
+    switch (variant) {
+      case 1: worker(decode_stage1_worker_kernel<4, 1>, 4); break;
+      case 2: worker(decode_stage1_worker_kernel<8, 2>, 8); break;
+      case 3: worker(decode_stage1_worker_kernel<4, 2>, 4); break;
+      default: worker(decode_stage1_worker_kernel<4, 4>, 4); break;
+    }
+  } else {
+    switch (variant) {
+      case 1: stage1(decode_stage1_kernel<4, 1>, 4); break;
+      case 2: stage1(decode_stage1_kernel<8, 2>, 8); break;
+      case 3: stage1(decode_stage1_kernel<4, 2>, 4); break;
+      default: stage1(decode_stage1_kernel<4, 4>, 4); break;
+    }
   }
   int rc = check_launch("flash_decode_fwd stage1");
   if (rc != SID_OK || direct) return rc;
@@ -511,12 +581,13 @@ int check_decode_args(const void* q, const void* k_cache, const void* v_cache,
 
 using namespace sid;
 
-extern "C" int sid_flash_decode_segments_fwd(
+extern "C" int sid_flash_decode_workers_fwd(
     const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
     const int32_t* kv_indices, const int32_t* num_splits, int batch, int num_q_heads,
     int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
     int segment_size, int grid_slots, int variant, const int32_t* wg_order, float sm_scale,
-    float* part_o, float* part_lse, int part_batch, int part_stride, void* o, void* stream) {
+    float* part_o, float* part_lse, int part_batch, int part_stride, void* o, int workers,
+    void* stream) {
   SID_REQUIRE(batch >= 0, "flash_decode_fwd: negative batch");
   SID_REQUIRE(variant >= 0 && variant < kNumVariants, "flash_decode_fwd: unknown variant %d",
               variant);
@@ -530,6 +601,10 @@ extern "C" int sid_flash_decode_segments_fwd(
               "flash_decode_fwd: grid_slots %d out of range [1, %d]", grid_slots, kMaxGridSlots);
   SID_REQUIRE(batch < (1 << (31 - kOrderSlotBits)) && kMaxGridSlots <= (1 << kOrderSlotBits),
               "flash_decode_fwd: batch %d too large for the workgroup order", batch);
+  SID_REQUIRE(workers >= 0 && workers <= (1 << 20), "flash_decode_fwd: workers %d out of range",
+              workers);
+  SID_REQUIRE(workers == 0 || wg_order != nullptr,
+              "flash_decode_fwd: a worker launch needs the item order (wg_order)");
   if (grid_slots > 1) {
     SID_REQUIRE(part_o && part_lse, "flash_decode_fwd: null workspace");
     SID_REQUIRE(part_batch >= batch && part_stride >= grid_slots,
@@ -539,7 +614,20 @@ extern "C" int sid_flash_decode_segments_fwd(
   }
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, max_splits, batch,
                        num_slots, fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       part_stride, o, variant, wg_order, static_cast<hipStream_t>(stream));
+                       part_stride, o, variant, wg_order, workers, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sid_flash_decode_segments_fwd(
+    const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
+    const int32_t* kv_indices, const int32_t* num_splits, int batch, int num_q_heads,
+    int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
+    int segment_size, int grid_slots, int variant, const int32_t* wg_order, float sm_scale,
+    float* part_o, float* part_lse, int part_batch, int part_stride, void* o, void* stream) {
+  return sid_flash_decode_workers_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
+                                      batch, num_q_heads, num_kv_heads, head_dim, num_slots,
+                                      max_splits, fixed_split_size, segment_size, grid_slots,
+                                      variant, wg_order, sm_scale, part_o, part_lse, part_batch,
+                                      part_stride, o, 0, stream);
 }
 
 extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -639,5 +727,5 @@ extern "C" int sid_flash_decode_segments_fwd_noalloc(
   // Stage 2 reads only the slots stage 1 wrote in this call, so nothing is cleared.
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, max_splits, batch,
                        num_slots, fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       grid_slots, o, variant, wg_order, static_cast<hipStream_t>(stream));
+                       grid_slots, o, variant, wg_order, 0, static_cast<hipStream_t>(stream));
 }

@@ -27,4 +27,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* sid_last_error(void) { return sid::g_last_error; }
 
-extern "C" int sid_abi_version(void) { return 21; }
+extern "C" int sid_abi_version(void) { return 22; }

@@ -21,7 +21,8 @@ from sid.engine.batch import (DecodeStatic, ForwardBatch, ForwardMode, batch_buc
 from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
 from sid.kernels.decode_attention import (INVARIANT_VARIANT, DecodeAttention, length_bucket,
-                                          plan_variant, segment_tokens, workgroup_order)
+                                          plan_variant, segment_tokens, stage1_workers,
+                                          workgroup_order)
 from sid.kernels.matmul_persistent import linear_sample_supported
 from sid.model.loader import build_model_config, load_weights, random_weights
 from sid.model.qwen3 import Qwen3Model
@@ -198,13 +199,15 @@ class ModelRunner:
         return fb
 
     def _attach_order(self, fb: ForwardBatch, rows: int, invariant: bool, max_len: int,
-                      geom: tuple | None) -> bool:
-        """The attention's stage-1 workgroup order for this step (heaviest segments first,
-        balanced over the CUs; workgroup_order), from the host-known lengths and the plan the
-        forward will run: fixed splits in batch_invariant mode, else the nondet geometry.
-        Batches with fewer non-empty segments than CUs keep the grid's order (nothing to
-        balance, and reading the order first costs a small batch 0.2-0.4 us). Returns
-        whether an order was attached."""
+                      geom: tuple | None) -> int:
+        """The attention's stage-1 placement for this step, from the host-known lengths and
+        the plan the forward will run (fixed splits in batch_invariant mode, else the nondet
+        geometry): the heaviest-first workgroup order (workgroup_order, balanced over the
+        CUs) for the grid, or for a worker launch (stage1_workers) the same dealing over the
+        workers. Grids with fewer non-empty segments than CUs otherwise keep their own order
+        (nothing to balance, and reading the order first costs a small batch 0.2-0.4 us).
+        Placement never changes a result. Returns 0 (grid order), 1 (order attached) or the
+        worker count (fb.decode_workers)."""
         da = self.decode_attn
         if invariant:
             tile = da.invariant_split_size
@@ -213,14 +216,19 @@ class ModelRunner:
             (splits, seg, slots), fixed = geom, 0
         tokens = segment_tokens(fb.seq_lens_host, rows, splits, fixed, seg, slots)
         fb.decode_wg_order = None
-        if int(np.count_nonzero(tokens)) < da.cu_count():
-            return False
-        order = workgroup_order(tokens, da.cu_count())
+        fb.decode_workers = 0
+        cu = da.cu_count()
+        nonempty = int(np.count_nonzero(tokens))
+        workers = stage1_workers(nonempty, fb.decode_variant, slots, cu)
+        if workers == 0 and nonempty < cu:
+            return 0
+        order = workgroup_order(tokens, workers or cu)
         if self.graphs is not None:
             fb.decode_wg_order = self.graphs.decode_static.set_order(order)
         else:
             fb.decode_wg_order = torch.from_numpy(order).to(self.device)
-        return True
+        fb.decode_workers = workers
+        return workers or 1
 
     def _pick_variant(self, fb: ForwardBatch, bs: int, max_len: int) -> tuple:
         """The nondet plan's geometry and its stage-1 workgroup shape (fb.decode_variant),

@@ -40,6 +40,9 @@ _SIGNATURES = {
     "sid_flash_decode_segments_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
                                       _i32, _i32, _i32, _i32, _i32, _vp, _f32, _vp, _vp, _i32,
                                       _i32, _vp, _vp],
+    "sid_flash_decode_workers_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
+                                     _i32, _i32, _i32, _i32, _i32, _vp, _f32, _vp, _vp, _i32,
+                                     _i32, _vp, _i32, _vp],
     "sid_flash_decode_segments_fwd_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
                                               _i32, _i64, _i32, _i32, _i32, _i32, _i32, _vp,
                                               _f32, _vp, _vp],
@@ -59,7 +62,7 @@ EXPORTED = ("sid_last_error", "sid_abi_version", "sid_extend_attention_workspace
             "sid_qwen3_extend_workspace_bytes", "sid_qwen3_extend_forward",
             "sid_flash_decode_noalloc_scratch_bytes", "sid_linear_sample_workspace_bytes",
             *_SIGNATURES)
-ABI_VERSION = 21
+ABI_VERSION = 22
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -121,10 +124,11 @@ class NativeLib:
                          max_splits: int, fixed_split_size: int, sm_scale: float,
                          part_o, part_lse, o, segment_size: int = 0,
                          grid_slots: int | None = None, variant: int = 0,
-                         wg_order=None) -> None:
+                         wg_order=None, workers: int = 0) -> None:
         """segment_size / grid_slots / variant / wg_order: see sid_flash_decode_segments_fwd
         (defaults: one segment per split, grid of max_splits slots = the reference's
-        partition, the default workgroup shape, the grid's own order)."""
+        partition, the default workgroup shape, the grid's own order); workers > 0: stage 1
+        by that many workgroups over the items of wg_order (sid_flash_decode_workers_fwd)."""
         _gpu(q, "q", torch.bfloat16)
         _check(q.dim() == 3, "q must be [B, HQ, D]")
         b, hq, d = q.shape
@@ -150,13 +154,14 @@ class NativeLib:
         _check(o.shape == q.shape, "o must have q's shape")
         slots = int(max_splits) if grid_slots is None else int(grid_slots)
         order = self._order_ptr(wg_order, b * slots)
-        self._call("sid_flash_decode_segments_fwd", q.data_ptr(), k_cache.data_ptr(),
+        _check(workers == 0 or wg_order is not None, "a worker launch needs wg_order")
+        self._call("sid_flash_decode_workers_fwd", q.data_ptr(), k_cache.data_ptr(),
                    v_cache.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
                    _ptr(num_splits), b, hq, hkv, d, k_cache.shape[0], int(max_splits),
                    int(fixed_split_size), int(segment_size), slots, int(variant), order,
                    float(sm_scale),
                    part_o.data_ptr(), part_lse.data_ptr(), part_o.shape[0], part_o.shape[2],
-                   o.data_ptr(), _stream(q))
+                   o.data_ptr(), int(workers), _stream(q))
 
     def flash_decode_fwd_noalloc(self, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                  max_splits: int, fixed_split_size: int, sm_scale: float, o,

@@ -294,6 +294,27 @@ def workgroup_order(tokens: np.ndarray, cu_count: int) -> np.ndarray:
     return order
 
 
+# Worker launches (sid_flash_decode_workers_fwd): stage 1 as one workgroup per CU, each
+# computing in turn the (request, slot) items dealt to it (workgroup_order over the workers),
+# instead of one workgroup per item. Same items, same arithmetic: the same bits; only the
+# placement differs. Measured over 33 batch shapes (B = 1-256, uniform and config-5-like
+# lognormal lengths, nondet and batch_invariant plans, 4 KV pools rotated, graph-timed): an
+# 8 x 2 grid whose non-empty workgroups number between half the CUs and the CU count runs
+# 1.27-1.65x slower than the worker form (e.g. B = 96 lognormal, 241 non-empty 512-token
+# segments: 106.4 -> 70.4 us; batch_invariant B = 32 lognormal: 52.0 -> 31.6 us), while below
+# that band and above it the two are within a few percent (the worker form 0.94-1.03x of the
+# grid), and 4 x 1 / 4 x 2 grids lose with one worker per CU (0.66-0.80x).
+WORKERS_VARIANT = 2
+
+
+def stage1_workers(nonempty: int, variant: int, slots: int, cu_count: int) -> int:
+    """Workgroups of a worker launch for a plan with `nonempty` non-empty (request, slot)
+    items in `slots` slots per request with stage-1 shape `variant`, or 0 for the grid."""
+    if slots > 1 and variant == WORKERS_VARIANT and cu_count < 2 * nonempty <= 2 * cu_count:
+        return cu_count
+    return 0
+
+
 def workspace_slots(max_seq_len: int, max_kv_splits: int, invariant_split_size: int) -> int:
     """Partial slots per request the workspace must hold for any plan."""
     nondet = -(-max_seq_len // SEGMENT_SIZES[-1]) + max_kv_splits
@@ -356,14 +377,15 @@ class DecodeAttention:
                 max_seq_len: int, sm_scale: float, invariant: bool,
                 policy_batch: int | None = None, variant: int | None = None,
                 geometry: tuple | None = None,
-                wg_order: torch.Tensor | None = None) -> torch.Tensor:
+                wg_order: torch.Tensor | None = None, workers: int = 0) -> torch.Tensor:
         """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync).
         policy_batch: real requests among the B rows (the rest are empty padding); variant:
         the stage-1 workgroup shape (stage1_variant; None: INVARIANT_VARIANT in batch_invariant
         mode, else 0); geometry:
         plan_variant's nondet geometry for this batch (None: from the batch size and
         max_seq_len alone); wg_order: workgroup_order of this plan, on the device (None: the
-        grid's own order)."""
+        grid's own order); workers > 0: stage 1 by that many workgroups, each computing the
+        items of wg_order dealt to it (then a permutation of every (request, slot) item)."""
         if variant is None:
             variant = INVARIANT_VARIANT if invariant else 0
         assert not invariant or variant == INVARIANT_VARIANT, \
@@ -383,5 +405,5 @@ class DecodeAttention:
         self.ext.flash_decode_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                   grid_splits, fixed, sm_scale, self.part_o, self.part_lse, o,
                                   segment_size=seg, grid_slots=slots, variant=variant,
-                                  wg_order=wg_order)
+                                  wg_order=wg_order, workers=workers)
         return o

@@ -91,7 +91,8 @@ class Qwen3Model:
             o = decode_attn.forward(q, k_pool, v_pool, fb.kv_indptr, fb.kv_indices, fb.seq_lens,
                                     fb.max_seq_len, self.sm_scale, invariant=fb.invariant,
                                     policy_batch=fb.real_rows, variant=fb.decode_variant,
-                                    geometry=fb.decode_geometry, wg_order=fb.decode_wg_order)
+                                    geometry=fb.decode_geometry, wg_order=fb.decode_wg_order,
+                                    workers=fb.decode_workers)
         else:
             qo = fb.qo_indptr
             if qo is None:  # decode through the extend kernel: one query per request

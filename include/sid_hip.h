@@ -112,6 +112,29 @@ int sid_flash_decode_segments_fwd(const void* q, const void* k_cache, const void
                                   int part_stride, void* o, void* stream);
 
 /*
+ * sid_flash_decode_segments_fwd with stage 1 run by `workers` workgroups that
+ * each compute a share of the batch x grid_slots (request, slot) items in turn:
+ * worker w takes the items at entries w, w + workers, w + 2 * workers, ... of
+ * wg_order, which must then be a permutation of all of them (empty slots
+ * included), packed as in sid_flash_decode_segments_fwd. Every item is computed
+ * as the grid launch computes it, so the result is the same, bit for bit; the
+ * caller deals the items so that the workers' token counts balance (ragged
+ * batches, where the grid's workgroups cannot all be kept equally busy).
+ * workers == 0 is sid_flash_decode_segments_fwd. Ignored when grid_slots == 1.
+ * Builds on sid_flash_decode_fwd (sid/csrc/flash_decode.cu:307-406): same
+ * split geometry, partials and merge; the worker placement has no counterpart
+ * in the reference (ABI 22).
+ */
+int sid_flash_decode_workers_fwd(const void* q, const void* k_cache, const void* v_cache,
+                                 const int32_t* kv_indptr, const int32_t* kv_indices,
+                                 const int32_t* num_splits, int batch, int num_q_heads,
+                                 int num_kv_heads, int head_dim, int64_t num_slots,
+                                 int max_splits, int fixed_split_size, int segment_size,
+                                 int grid_slots, int variant, const int32_t* wg_order,
+                                 float sm_scale, float* part_o, float* part_lse, int part_batch,
+                                 int part_stride, void* o, int workers, void* stream);
+
+/*
  * No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): sid_flash_decode_segments_fwd without the part_o /

@@ -295,3 +295,47 @@ def test_workgroup_order_is_a_balanced_permutation():
     flat = np.full((4, 6), 7, dtype=np.int64)
     assert workgroup_order(flat, 4).tolist() == [(b << ORDER_SLOT_BITS) | y
                                                 for y in range(4) for b in range(6)]
+
+
+def test_stage1_workers_rule():
+    """Worker launches only for 8 x 2 plans of several slots whose non-empty items number
+    more than half the CUs and at most the CU count (one worker per CU)."""
+    from sid.kernels.decode_attention import WORKERS_VARIANT, stage1_workers
+    cu = 256
+    assert WORKERS_VARIANT == 2
+    assert stage1_workers(241, 2, 7, cu) == cu
+    assert stage1_workers(129, 2, 20, cu) == cu
+    assert stage1_workers(256, 2, 16, cu) == cu
+    assert stage1_workers(128, 2, 32, cu) == 0   # half the CUs or fewer: the grid
+    assert stage1_workers(257, 2, 16, cu) == 0   # more items than CUs: the grid
+    assert stage1_workers(241, 1, 7, cu) == 0    # 4 x 1 / 4 x 2 / 4 x 4 keep the grid
+    assert stage1_workers(241, 3, 7, cu) == 0
+    assert stage1_workers(241, 0, 7, cu) == 0
+    assert stage1_workers(200, 2, 1, cu) == 0    # single-slot grids write o directly
+
+
+def test_worker_dealing_covers_every_item_once():
+    """A worker launch's wg_order (workgroup_order over the workers): worker w takes the
+    entries w, w + W, ...; every (request, slot) item, empty ones included, is dealt to
+    exactly one worker, and the workers' token loads differ by at most one item's tokens
+    beyond a perfect split of the heaviest-first rounds."""
+    import numpy as np
+
+    from sid.kernels.decode_attention import ORDER_SLOT_BITS, workgroup_order
+    rng = np.random.default_rng(9)
+    slots, rows = 9, 40
+    tok = rng.integers(0, 512, size=(slots, rows))
+    tok[rng.random((slots, rows)) < 0.4] = 0
+    for workers in (1, 5, 64, 300, slots * rows + 3):
+        order = workgroup_order(tok, workers)
+        assert order.size == slots * rows
+        seen = set()
+        loads = np.zeros(workers, dtype=np.int64)
+        for w in range(workers):
+            for e in order[w::workers]:
+                b, y = int(e) >> ORDER_SLOT_BITS, int(e) & ((1 << ORDER_SLOT_BITS) - 1)
+                assert (b, y) not in seen
+                seen.add((b, y))
+                loads[w] += tok[y, b]
+        assert len(seen) == slots * rows
+        assert loads.max() - loads.min() <= tok.max()

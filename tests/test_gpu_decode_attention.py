@@ -190,6 +190,57 @@ def test_workgroup_order_does_not_change_bits(policy):
     assert_close_bf16(o, decode_attention_ref(q, k, v, indptr, idx, SCALE))
 
 
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+@pytest.mark.parametrize("policy", ["heuristic", "fixed256", "seg64"])
+def test_worker_launch_equals_grid(policy, variant):
+    """sid_flash_decode_workers_fwd: stage 1 by a fixed number of workgroups, each computing
+    the items dealt to it in turn, gives bitwise the grid launch's output, for worker counts
+    below, at and above the item count (ragged batch with an empty request and a one-token
+    request; NaN-prefilled workspaces, so every partial the merge reads is written), and
+    stays within the fp32 oracle's tolerance."""
+    from sid.kernels.decode_attention import segment_tokens, workgroup_order
+    ext = _ext()
+    rng = np.random.default_rng(21)
+    lens = [int(x) for x in np.minimum(rng.lognormal(np.log(400), 1.0, 24), 5000).astype(int)]
+    lens[5] = 0
+    lens[11] = 1
+    q, k, v, indptr, idx = decode_inputs(lens, seed=23)
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    if policy == "fixed256":
+        ns, grid = plan_fixed(lens)
+        fixed, seg, slots = 256, 256, grid
+    else:
+        ns, grid = plan_heuristic(lens, cu, HKV, 32)
+        fixed, seg = 0, (256 if policy == "heuristic" else 64)
+        slots = _slots(lens, ns, fixed, seg)
+    tok = segment_tokens(lens, len(lens), grid, fixed, seg, slots)
+    plain = _run(q, k, v, indptr, idx, ns, grid, fixed, seg=seg, slots=slots, variant=variant)
+    nst = torch.tensor(ns, dtype=torch.int32, device="cuda")
+    items = len(lens) * slots
+    for workers in (1, 7, cu, items + 5):
+        order = torch.from_numpy(workgroup_order(tok, workers)).cuda()
+        print(f"policy={policy} variant={variant} slots={slots} workers={workers}", flush=True)
+        part_o = torch.full((len(lens), HQ, slots, D), float("nan"), device="cuda")
+        part_lse = torch.full((len(lens), HQ, slots), float("nan"), device="cuda")
+        o = torch.empty_like(q)
+        ext.flash_decode_fwd(q, k, v, indptr, idx, nst, grid, fixed, SCALE, part_o, part_lse, o,
+                             segment_size=seg, grid_slots=slots, variant=variant,
+                             wg_order=order, workers=workers)
+        assert torch.equal(o, plain), workers
+    assert (o[5] == 0).all()
+    assert_close_bf16(o, decode_attention_ref(q, k, v, indptr, idx, SCALE))
+
+
+def test_worker_launch_needs_an_order():
+    lens = [300, 40]
+    q, k, v, indptr, idx = decode_inputs(lens, seed=3)
+    part_o = torch.empty((2, HQ, 4, D), device="cuda")
+    part_lse = torch.empty((2, HQ, 4), device="cuda")
+    with pytest.raises(RuntimeError, match="wg_order"):
+        _ext().flash_decode_fwd(q, k, v, indptr, idx, None, 4, 0, SCALE, part_o, part_lse,
+                                torch.empty_like(q), segment_size=64, grid_slots=4, workers=8)
+
+
 @pytest.mark.parametrize("policy", ["heuristic", "fixed256", "splits8"])
 def test_device_derived_split_counts_equal_explicit(policy):
     """num_splits = None: the kernel derives each request's split count from its length

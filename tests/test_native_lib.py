@@ -41,7 +41,7 @@ def test_python_binding_matches_header(ext):
 
 def test_abi_version(ext):
     from sid.kernels._native import ABI_VERSION
-    assert ext.lib.sid_abi_version() == ABI_VERSION == 21
+    assert ext.lib.sid_abi_version() == ABI_VERSION == 22
 
 
 def test_validation_errors_without_device_work(ext):
