@@ -765,7 +765,7 @@ constexpr int WXS = WIDE_K + 8;
 // the result does not depend on how the columns are split.
 constexpr int STREAM_WAVES = 8;
 
-template <int MBS, bool ARGMAX>
+template <int MBS, bool ARGMAX, bool LEAN = false>
 __global__ void __launch_bounds__(STREAM_WAVES * 64) linear_stream_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ bias, void* __restrict__ y, int M, int N, int out_fp32,
@@ -859,16 +859,20 @@ __global__ void __launch_bounds__(STREAM_WAVES * 64) linear_stream_kernel(
     }
     if (c != 3) return;
     const int col = (t_begin + (u >> 2) * t_step) * 16 + r;
-    const float bias_v = bias != nullptr ? bf16_to_f32(bias[col]) : 0.0f;
+    // LEAN: no bias and no logits written (the greedy-only call), so the epilogue holds no
+    // load and no store that the weight stream's waits would have to account for.
+    const bool has_bias = !LEAN && bias != nullptr;
+    const bool has_y = !LEAN && y != nullptr;
+    const float bias_v = has_bias ? bf16_to_f32(bias[col]) : 0.0f;
 #pragma unroll
     for (int mb = 0; mb < MBS; ++mb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 16 * mb + 4 * g + i;
         float v = total[mb][i];
-        if (bias != nullptr) v += bias_v;
+        if (has_bias) v += bias_v;
         const float vr = round_bf16(v);
-        if (y != nullptr && row < M) {
+        if (has_y && row < M) {
           const int64_t off = static_cast<int64_t>(row) * N + col;
           if (out_fp32) {
             static_cast<float*>(y)[off] = vr;
@@ -1425,20 +1429,35 @@ bool stream_shape_ok(int64_t m, int64_t n, int64_t k) {
   return m >= 1 && m <= kStreamMaxM && k == WIDE_K && n % 16 == 0 && n < (1ll << 31);
 }
 
+template <int MBS, bool AM, bool LEAN>
+void launch_stream_form(const bf16_t* x, int64_t ldx, const void* w, const void* bias, void* y,
+                        int m, int n, int out_fp32, float* bv, int* bi, int cand_rows, int row0,
+                        hipStream_t s) {
+  const size_t lds = static_cast<size_t>(MBS * 16) * WXS * sizeof(bf16_t);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_stream_kernel<MBS, AM, LEAN>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((linear_stream_kernel<MBS, AM, LEAN>), dim3(stream_grid()),
+                     dim3(STREAM_WAVES * 64), lds, s, x, ldx, (const bf16_t*)w,
+                     (const bf16_t*)bias, y, m, n, out_fp32, bv, bi, cand_rows, row0);
+}
+
 template <int MBS, bool AM>
 void launch_stream_mbs(const bf16_t* x, int64_t ldx, const void* w, const void* bias, void* y,
                        int m, int n, int out_fp32, float* bv, int* bi, int cand_rows, int row0,
                        hipStream_t s) {
-  const size_t lds = static_cast<size_t>(MBS * 16) * WXS * sizeof(bf16_t);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_stream_kernel<MBS, AM>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    attr_set = true;
+  if constexpr (AM) {
+    if (bias == nullptr && y == nullptr) {
+      launch_stream_form<MBS, AM, true>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, cand_rows,
+                                        row0, s);
+      return;
+    }
   }
-  hipLaunchKernelGGL((linear_stream_kernel<MBS, AM>), dim3(stream_grid()),
-                     dim3(STREAM_WAVES * 64), lds, s, x, ldx, (const bf16_t*)w,
-                     (const bf16_t*)bias, y, m, n, out_fp32, bv, bi, cand_rows, row0);
+  launch_stream_form<MBS, AM, false>(x, ldx, w, bias, y, m, n, out_fp32, bv, bi, cand_rows, row0,
+                                     s);
 }
 
 // One launch per 64-row group; group g reads x rows 64g.., writes y rows 64g.. and the
