@@ -111,3 +111,30 @@ def test_decode_graph_near_max_seq_len():
               flush=True)
         outs[graphs] = runner.forward(fb).clone()
     assert torch.equal(outs[True], outs[False])
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_decode_worker_launch_equals_grid(graphs, monkeypatch):
+    """A decode batch whose attention plan is an 8 x 2 grid with between half the CUs and
+    the CU count of non-empty segments runs stage 1 as one worker workgroup per CU
+    (stage1_workers); its logits are bitwise those of the same step with the grid launch."""
+    import sid.engine.model_runner as mr
+    lens = [2596, 2019, 1680, 1028, 1131, 410, 503, 344]
+    cfg = EngineConfig(mode=Mode.NONDET, kv_pool_tokens=16384, max_reqs=16, max_seq_len=4096,
+                       max_decode_batch=16, num_layers=2, seed=13, use_graphs=graphs)
+    runner = ModelRunner(cfg, "cuda")
+    reqs = _requests(runner, lens, seed=5)
+    fb = build_prefill_batch(reqs, runner.kv_cache, "cuda", invariant=False)
+    for r, t in zip(reqs, runner.sample(fb, runner.forward(fb)).tolist()):
+        r.output_ids.append(t)
+    fb = runner.prepare_decode(reqs, False)
+    if fb.decode_workers == 0:
+        pytest.skip(f"this device's CU count gives no worker plan for these lengths")
+    print(f"workers={fb.decode_workers} variant={fb.decode_variant} geom={fb.decode_geometry}",
+          flush=True)
+    worker = runner.forward(fb).clone()
+    monkeypatch.setattr(mr, "stage1_workers", lambda *a: 0)
+    fb = runner.prepare_decode(reqs, False)
+    assert fb.decode_workers == 0
+    grid = runner.forward(fb)
+    assert torch.equal(worker, grid)
