@@ -126,12 +126,15 @@ __host__ __device__ __forceinline__ bool segment_range(int seq_len, int n_splits
   return start < end;
 }
 
-// LDS of one stage-1 workgroup: the waves' softmax states, then the merge's scales.
+// LDS of one stage-1 workgroup: the waves' softmax states, then the merge's scales. The
+// accumulators come first and the struct is 16-byte aligned, so their stores and the merge's
+// reads are whole 16-byte LDS accesses (with a 4-byte-aligned struct the compiler splits
+// them into 4-byte pairs: one request of 1024 tokens took 9.3 -> 10.0 us).
 template <int NW>
-struct Stage1Lds {
+struct alignas(16) Stage1Lds {
+  float acc[NW][HQ][HEAD_DIM];
   float m[NW][HQ];
   float l[NW][HQ];
-  float acc[NW][HQ][HEAD_DIM];
   float sc[NW][HQ];
   float den[HQ];
   float mx[HQ];
@@ -529,19 +532,19 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                        num_splits, max_splits, fixed_split_size, seg, sm_scale, num_slots,
                        part_stride, part_o, part_lse, wg_order, batch, grid_slots);
   };
-  if (workers > 0 && !direct) {
-    switch (variant) {
-      case 1: worker(decode_stage1_worker_kernel<4, 1>, 4); break;
-      case 2: worker(decode_stage1_worker_kernel<8, 2>, 8); break;
-      case 3: worker(decode_stage1_worker_kernel<4, 2>, 4); break;
-      default: worker(decode_stage1_worker_kernel<4, 4>, 4); break;
-    }
-  } else {
+  if (workers == 0 || direct) {
     switch (variant) {
       case 1: stage1(decode_stage1_kernel<4, 1>, 4); break;
       case 2: stage1(decode_stage1_kernel<8, 2>, 8); break;
       case 3: stage1(decode_stage1_kernel<4, 2>, 4); break;
       default: stage1(decode_stage1_kernel<4, 4>, 4); break;
+    }
+  } else {
+    switch (variant) {
+      case 1: worker(decode_stage1_worker_kernel<4, 1>, 4); break;
+      case 2: worker(decode_stage1_worker_kernel<8, 2>, 8); break;
+      case 3: worker(decode_stage1_worker_kernel<4, 2>, 4); break;
+      default: worker(decode_stage1_worker_kernel<4, 4>, 4); break;
     }
   }
   int rc = check_launch("flash_decode_fwd stage1");
