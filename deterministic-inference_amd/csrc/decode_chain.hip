@@ -314,12 +314,15 @@ __global__ void __launch_bounds__(2 * PL * (NB / NBW) * 64) norm_silu_kernel(
   const int j0 = tile * 8 * NB;
   const int m0 = rg * ROWS;
 
-  // Norm weights and activation rows first: the norm waits only for them.
+  // Norm weights and activation rows first: the norm waits only for them. A wave's rows are
+  // held RB at a time (all of them up to 3 per wave; 64-row workgroups normalise 6 per wave
+  // in two batches, the second loaded once the first is in LDS).
+  constexpr int RB = RPW < 3 ? RPW : 3;
   uint4 nw[PL];
   norm_w_load<PL>(norm_w, lane, nw);
-  float v[RPW][PL][8];
+  float v[RB][PL][8];
 #pragma unroll
-  for (int q = 0; q < RPW; ++q) {
+  for (int q = 0; q < RB; ++q) {
     const int row = wave + NW * q;
     if (row < ROWS) norm_row_load<PL, F32>(src, min(m0 + row, M - 1), lane, v[q]);
   }
@@ -329,9 +332,20 @@ __global__ void __launch_bounds__(2 * PL * (NB / NBW) * 64) norm_silu_kernel(
     packed_load(wf[j], w, static_cast<int64_t>(tile) * NB + nb0 + j, c, NCH, lane);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int q = 0; q < RPW; ++q) {
-    const int row = wave + NW * q;
-    if (row < ROWS) norm_row_store<PL>(v[q], lane, nw, eps, sx, row);
+  for (int b0 = 0; b0 < RPW; b0 += RB) {
+    if (b0 > 0) {
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+        const int row = wave + NW * (b0 + q);
+        if (b0 + q < RPW && row < ROWS)
+          norm_row_load<PL, F32>(src, min(m0 + row, M - 1), lane, v[q]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int row = wave + NW * (b0 + q);
+      if (b0 + q < RPW && row < ROWS) norm_row_store<PL>(v[q], lane, nw, eps, sx, row);
+    }
   }
   __syncthreads();
   f32x4_v acc[MBS][NBW];
@@ -545,6 +559,9 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // per CU through L2; measured per layer at 96 rows 36.8 -> 31.1 us, at 128 37.2 -> 31.0; at
 // 64 rows the halved workgroup count loses, 26.7 -> 30.6).
 constexpr int64_t kWideMinRows = 96;
+// Above this many rows the gate_up workgroups take 64 rows (one round of workgroups where
+// 32-row ones need two).
+constexpr int64_t kDeepMinRows = 128;
 // Above 128 rows the 16-row qkv workgroups (and the 32-column o / down ones) number more than
 // the CUs hold at once, so the qkv workgroups take 32 rows and the o / down ones 64 columns:
 // per layer at 192 rows qkv 14.7 -> 11.9 us, down 12.9 -> 9.8; at 256 the chain 52.9 ->
@@ -602,10 +619,11 @@ extern "C" int sid_rmsnorm_linear_silu_mul(const void* src, int src_fp32, const 
                   (reinterpret_cast<uintptr_t>(out) & 3) == 0,
               "rmsnorm_linear_silu_mul: misaligned operand");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  // 16-row workgroups for a handful of rows, 32 rows beyond; from kWideMinRows rows each
-  // wave takes two column blocks (48 gate columns per workgroup), when they tile inter.
-  const int mbs = m <= 16 ? 1 : 2;
-  const bool wide = mbs == 2 && m >= kWideMinRows && inter % 48 == 0;
+  // 16-row workgroups for a handful of rows, 32 rows beyond, 64 above kDeepMinRows; from
+  // kWideMinRows rows each wave takes two column blocks (48 gate columns per workgroup), when
+  // they tile inter.
+  const int mbs = m <= 16 ? 1 : (m > kDeepMinRows && inter % 48 == 0 ? 4 : 2);
+  const bool wide = mbs >= 2 && m >= kWideMinRows && inter % 48 == 0;
   const int nb = wide ? 6 : 3;
   const int64_t R = (m + 16 * mbs - 1) / (16 * mbs);
   const int64_t tiles = inter / (8 * nb);
@@ -619,6 +637,7 @@ extern "C" int sid_rmsnorm_linear_silu_mul(const void* src, int src_fp32, const 
   const bool f = src_fp32 != 0;
 #define SID_NS(PL, F)                                                            \
   (mbs == 1 ? go(norm_silu_kernel<PL, F, 1, 3>, PL)                             \
+   : mbs == 4 ? go(norm_silu_kernel<PL, F, 4, 6, 2>, PL)                        \
             : (wide ? go(norm_silu_kernel<PL, F, 2, 6, 2>, PL) : go(norm_silu_kernel<PL, F, 2, 3>, PL)))
   if (pl == 1) {
     if (f) SID_NS(1, true); else SID_NS(1, false);
