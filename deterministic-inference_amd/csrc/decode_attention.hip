@@ -383,6 +383,9 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
 // workers], order[w + 2 workers], ... of the batch x grid_slots items (order: a permutation
 // of them all, empty slots included, dealt so the workers' token counts balance). Each item
 // is computed exactly as the grid form computes it, so only placement differs: the same bits.
+// Entries from `busy` on are known to hold no tokens (the caller orders the items heaviest
+// first): a worker marks all of its remaining ones empty in one pass of its threads, one
+// order load and one log-sum-exp store each, instead of one dependent round trip per item.
 // Every worker runs a bounded loop over its share and exits.
 template <int NW, int TPL>
 __global__ void __launch_bounds__(NW * 64) decode_stage1_worker_kernel(
@@ -391,10 +394,13 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_worker_kernel(
     const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ num_splits,
     int max_splits, int fixed_split, int seg, float sm_scale, int64_t num_slots, int part_stride,
     float* __restrict__ part_o, float* __restrict__ part_lse, const int32_t* __restrict__ order,
-    int batch, int grid_slots) {
+    int batch, int grid_slots, int busy) {
   __shared__ Stage1Lds<NW> sh;
   const int n_items = batch * grid_slots;
-  for (int i = blockIdx.x; i < n_items; i += gridDim.x) {
+  const int W = static_cast<int>(gridDim.x);
+  const int busy_end = min(busy, n_items);
+  int i = static_cast<int>(blockIdx.x);
+  for (; i < busy_end; i += W) {
     const int packed = order[i];
     const int b = packed >> kOrderSlotBits;
     const int y = packed & ((1 << kOrderSlotBits) - 1);
@@ -404,6 +410,15 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_worker_kernel(
                            part_o, part_lse, nullptr);
     }
     __syncthreads();  // the item's merge reads of the LDS are done before the next item's writes
+  }
+  // The worker's remaining items i, i + W, ...: HQ markers each, one per thread.
+  const int rest = i < n_items ? (n_items - i + W - 1) / W : 0;
+  for (int t = threadIdx.x; t < rest * HQ; t += NW * 64) {
+    const int packed = order[i + (t / HQ) * W];
+    const int b = packed >> kOrderSlotBits;
+    const int y = packed & ((1 << kOrderSlotBits) - 1);
+    if (b < batch && y < grid_slots)
+      part_lse[(static_cast<int64_t>(b) * HQ + t % HQ) * part_stride + y] = NEG_BIG;
   }
 }
 
@@ -518,7 +533,7 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
                   int max_splits, int batch, int64_t num_slots, int fixed_split_size, int seg,
                   int grid_slots, float sm_scale, float* part_o, float* part_lse, int part_stride, void* o,
-                  int variant, const int32_t* wg_order, int workers, hipStream_t s) {
+                  int variant, const int32_t* wg_order, int workers, int busy, hipStream_t s) {
   const bool direct = (grid_slots == 1);
   auto stage1 = [&](auto kern, int nw) {
     hipLaunchKernelGGL(kern, dim3(batch, grid_slots), dim3(nw * 64), 0, s, (const bf16_t*)q,
@@ -530,7 +545,8 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
     hipLaunchKernelGGL(kern, dim3(workers), dim3(nw * 64), 0, s, (const bf16_t*)q,
                        (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr, kv_indices,
                        num_splits, max_splits, fixed_split_size, seg, sm_scale, num_slots,
-                       part_stride, part_o, part_lse, wg_order, batch, grid_slots);
+                       part_stride, part_o, part_lse, wg_order, batch, grid_slots,
+                       busy < 0 ? batch * grid_slots : busy);
   };
   if (workers == 0 || direct) {
     switch (variant) {
@@ -590,7 +606,7 @@ extern "C" int sid_flash_decode_workers_fwd(
     int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
     int segment_size, int grid_slots, int variant, const int32_t* wg_order, float sm_scale,
     float* part_o, float* part_lse, int part_batch, int part_stride, void* o, int workers,
-    void* stream) {
+    int busy, void* stream) {
   SID_REQUIRE(batch >= 0, "flash_decode_fwd: negative batch");
   SID_REQUIRE(variant >= 0 && variant < kNumVariants, "flash_decode_fwd: unknown variant %d",
               variant);
@@ -617,7 +633,8 @@ extern "C" int sid_flash_decode_workers_fwd(
   }
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, max_splits, batch,
                        num_slots, fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       part_stride, o, variant, wg_order, workers, static_cast<hipStream_t>(stream));
+                       part_stride, o, variant, wg_order, workers, busy,
+                       static_cast<hipStream_t>(stream));
 }
 
 extern "C" int sid_flash_decode_segments_fwd(
@@ -630,7 +647,7 @@ extern "C" int sid_flash_decode_segments_fwd(
                                       batch, num_q_heads, num_kv_heads, head_dim, num_slots,
                                       max_splits, fixed_split_size, segment_size, grid_slots,
                                       variant, wg_order, sm_scale, part_o, part_lse, part_batch,
-                                      part_stride, o, 0, stream);
+                                      part_stride, o, 0, -1, stream);
 }
 
 extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -730,5 +747,5 @@ extern "C" int sid_flash_decode_segments_fwd_noalloc(
   // Stage 2 reads only the slots stage 1 wrote in this call, so nothing is cleared.
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, max_splits, batch,
                        num_slots, fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       grid_slots, o, variant, wg_order, 0, static_cast<hipStream_t>(stream));
+                       grid_slots, o, variant, wg_order, 0, -1, static_cast<hipStream_t>(stream));
 }

@@ -217,6 +217,7 @@ class ModelRunner:
         tokens = segment_tokens(fb.seq_lens_host, rows, splits, fixed, seg, slots)
         fb.decode_wg_order = None
         fb.decode_workers = 0
+        fb.decode_busy = -1
         cu = da.cu_count()
         nonempty = int(np.count_nonzero(tokens))
         workers = stage1_workers(nonempty, fb.decode_variant, slots, cu)
@@ -228,6 +229,9 @@ class ModelRunner:
         else:
             fb.decode_wg_order = torch.from_numpy(order).to(self.device)
         fb.decode_workers = workers
+        # With at most one non-empty item per worker, the heaviest-first dealing keeps them all
+        # in its first round (never reversed): the entries from `nonempty` on are empty.
+        fb.decode_busy = nonempty if workers and nonempty <= workers else -1
         return workers or 1
 
     def _pick_variant(self, fb: ForwardBatch, bs: int, max_len: int) -> tuple:

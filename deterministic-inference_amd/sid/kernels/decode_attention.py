@@ -377,7 +377,8 @@ class DecodeAttention:
                 max_seq_len: int, sm_scale: float, invariant: bool,
                 policy_batch: int | None = None, variant: int | None = None,
                 geometry: tuple | None = None,
-                wg_order: torch.Tensor | None = None, workers: int = 0) -> torch.Tensor:
+                wg_order: torch.Tensor | None = None, workers: int = 0,
+                busy: int = -1) -> torch.Tensor:
         """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync).
         policy_batch: real requests among the B rows (the rest are empty padding); variant:
         the stage-1 workgroup shape (stage1_variant; None: INVARIANT_VARIANT in batch_invariant
@@ -385,7 +386,8 @@ class DecodeAttention:
         plan_variant's nondet geometry for this batch (None: from the batch size and
         max_seq_len alone); wg_order: workgroup_order of this plan, on the device (None: the
         grid's own order); workers > 0: stage 1 by that many workgroups, each computing the
-        items of wg_order dealt to it (then a permutation of every (request, slot) item)."""
+        items of wg_order dealt to it (then a permutation of every (request, slot) item), the
+        entries from `busy` on known to be empty (-1: unknown)."""
         if variant is None:
             variant = INVARIANT_VARIANT if invariant else 0
         assert not invariant or variant == INVARIANT_VARIANT, \
@@ -405,5 +407,5 @@ class DecodeAttention:
         self.ext.flash_decode_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                   grid_splits, fixed, sm_scale, self.part_o, self.part_lse, o,
                                   segment_size=seg, grid_slots=slots, variant=variant,
-                                  wg_order=wg_order, workers=workers)
+                                  wg_order=wg_order, workers=workers, busy=busy)
         return o
