@@ -42,6 +42,7 @@ constexpr bool kNonTemporal = true;  // K/V rows are streamed once: +9% HBM thro
 constexpr int HEUR_TILE = 32;       // granularity of the heuristic split size
 constexpr float NEG_BIG = -1e30f;   // finite "minus infinity" for running maxima
 constexpr int kOrderSlotBits = 12;  // wg_order entries: request << 12 | slot
+constexpr int kOrderEmpty = 1 << 30;  // wg_order entry flag: the item holds no tokens
 
 __host__ __device__ __forceinline__ int kv_per_split(int seq_len, int n_splits, int fixed_split) {
   if (fixed_split > 0) return fixed_split;
@@ -369,7 +370,7 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
   int b = blockIdx.x;
   int y = blockIdx.y;
   if (wg_order != nullptr) {
-    const int packed = wg_order[blockIdx.x + blockIdx.y * gridDim.x];
+    const int packed = wg_order[blockIdx.x + blockIdx.y * gridDim.x] & ~kOrderEmpty;
     b = packed >> kOrderSlotBits;
     y = packed & ((1 << kOrderSlotBits) - 1);
     if (b >= static_cast<int>(gridDim.x) || y >= static_cast<int>(gridDim.y)) return;
@@ -383,9 +384,10 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_kernel(
 // workers], order[w + 2 workers], ... of the batch x grid_slots items (order: a permutation
 // of them all, empty slots included, dealt so the workers' token counts balance). Each item
 // is computed exactly as the grid form computes it, so only placement differs: the same bits.
-// Entries from `busy` on are known to hold no tokens (the caller orders the items heaviest
-// first): a worker marks all of its remaining ones empty in one pass of its threads, one
-// order load and one log-sum-exp store each, instead of one dependent round trip per item.
+// Entries with kOrderEmpty set are items known to hold no tokens, and in a worker's sequence
+// they follow all of its other entries: from its first one on, the worker marks all of its
+// remaining items empty in one pass of its threads (one order load and one log-sum-exp
+// store each) instead of one dependent round trip per item.
 // Every worker runs a bounded loop over its share and exits.
 template <int NW, int TPL>
 __global__ void __launch_bounds__(NW * 64) decode_stage1_worker_kernel(
@@ -394,14 +396,14 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_worker_kernel(
     const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ num_splits,
     int max_splits, int fixed_split, int seg, float sm_scale, int64_t num_slots, int part_stride,
     float* __restrict__ part_o, float* __restrict__ part_lse, const int32_t* __restrict__ order,
-    int batch, int grid_slots, int busy) {
+    int batch, int grid_slots) {
   __shared__ Stage1Lds<NW> sh;
   const int n_items = batch * grid_slots;
   const int W = static_cast<int>(gridDim.x);
-  const int busy_end = min(busy, n_items);
   int i = static_cast<int>(blockIdx.x);
-  for (; i < busy_end; i += W) {
-    const int packed = order[i];
+  for (; i < n_items; i += W) {
+    const int packed = order[i];  // workgroup-uniform
+    if (packed & kOrderEmpty) break;
     const int b = packed >> kOrderSlotBits;
     const int y = packed & ((1 << kOrderSlotBits) - 1);
     if (b < batch && y < grid_slots) {
@@ -411,10 +413,11 @@ __global__ void __launch_bounds__(NW * 64) decode_stage1_worker_kernel(
     }
     __syncthreads();  // the item's merge reads of the LDS are done before the next item's writes
   }
-  // The worker's remaining items i, i + W, ...: HQ markers each, one per thread.
+  // The worker's remaining items i, i + W, ... (flagged empty): HQ markers each, one per
+  // thread.
   const int rest = i < n_items ? (n_items - i + W - 1) / W : 0;
   for (int t = threadIdx.x; t < rest * HQ; t += NW * 64) {
-    const int packed = order[i + (t / HQ) * W];
+    const int packed = order[i + (t / HQ) * W] & ~kOrderEmpty;
     const int b = packed >> kOrderSlotBits;
     const int y = packed & ((1 << kOrderSlotBits) - 1);
     if (b < batch && y < grid_slots)
@@ -533,7 +536,7 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* num_splits,
                   int max_splits, int batch, int64_t num_slots, int fixed_split_size, int seg,
                   int grid_slots, float sm_scale, float* part_o, float* part_lse, int part_stride, void* o,
-                  int variant, const int32_t* wg_order, int workers, int busy, hipStream_t s) {
+                  int variant, const int32_t* wg_order, int workers, hipStream_t s) {
   const bool direct = (grid_slots == 1);
   auto stage1 = [&](auto kern, int nw) {
     hipLaunchKernelGGL(kern, dim3(batch, grid_slots), dim3(nw * 64), 0, s, (const bf16_t*)q,
@@ -545,8 +548,7 @@ int launch_decode(const void* q, const void* k_cache, const void* v_cache,
     hipLaunchKernelGGL(kern, dim3(workers), dim3(nw * 64), 0, s, (const bf16_t*)q,
                        (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_indptr, kv_indices,
                        num_splits, max_splits, fixed_split_size, seg, sm_scale, num_slots,
-                       part_stride, part_o, part_lse, wg_order, batch, grid_slots,
-                       busy < 0 ? batch * grid_slots : busy);
+                       part_stride, part_o, part_lse, wg_order, batch, grid_slots);
   };
   if (workers == 0 || direct) {
     switch (variant) {
@@ -606,7 +608,7 @@ extern "C" int sid_flash_decode_workers_fwd(
     int num_kv_heads, int head_dim, int64_t num_slots, int max_splits, int fixed_split_size,
     int segment_size, int grid_slots, int variant, const int32_t* wg_order, float sm_scale,
     float* part_o, float* part_lse, int part_batch, int part_stride, void* o, int workers,
-    int busy, void* stream) {
+    void* stream) {
   SID_REQUIRE(batch >= 0, "flash_decode_fwd: negative batch");
   SID_REQUIRE(variant >= 0 && variant < kNumVariants, "flash_decode_fwd: unknown variant %d",
               variant);
@@ -618,7 +620,7 @@ extern "C" int sid_flash_decode_workers_fwd(
   SID_REQUIRE(segment_size >= 0, "flash_decode_fwd: negative segment_size");
   SID_REQUIRE(grid_slots >= 1 && grid_slots <= kMaxGridSlots,
               "flash_decode_fwd: grid_slots %d out of range [1, %d]", grid_slots, kMaxGridSlots);
-  SID_REQUIRE(batch < (1 << (31 - kOrderSlotBits)) && kMaxGridSlots <= (1 << kOrderSlotBits),
+  SID_REQUIRE(batch < (1 << (30 - kOrderSlotBits)) && kMaxGridSlots <= (1 << kOrderSlotBits),
               "flash_decode_fwd: batch %d too large for the workgroup order", batch);
   SID_REQUIRE(workers >= 0 && workers <= (1 << 20), "flash_decode_fwd: workers %d out of range",
               workers);
@@ -633,7 +635,7 @@ extern "C" int sid_flash_decode_workers_fwd(
   }
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, max_splits, batch,
                        num_slots, fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       part_stride, o, variant, wg_order, workers, busy,
+                       part_stride, o, variant, wg_order, workers,
                        static_cast<hipStream_t>(stream));
 }
 
@@ -647,7 +649,7 @@ extern "C" int sid_flash_decode_segments_fwd(
                                       batch, num_q_heads, num_kv_heads, head_dim, num_slots,
                                       max_splits, fixed_split_size, segment_size, grid_slots,
                                       variant, wg_order, sm_scale, part_o, part_lse, part_batch,
-                                      part_stride, o, 0, -1, stream);
+                                      part_stride, o, 0, stream);
 }
 
 extern "C" int sid_flash_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -747,5 +749,5 @@ extern "C" int sid_flash_decode_segments_fwd_noalloc(
   // Stage 2 reads only the slots stage 1 wrote in this call, so nothing is cleared.
   return launch_decode(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits, max_splits, batch,
                        num_slots, fixed_split_size, segment_size, grid_slots, sm_scale, part_o, part_lse,
-                       grid_slots, o, variant, wg_order, 0, -1, static_cast<hipStream_t>(stream));
+                       grid_slots, o, variant, wg_order, 0, static_cast<hipStream_t>(stream));
 }

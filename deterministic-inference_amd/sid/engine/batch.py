@@ -67,7 +67,6 @@ class ForwardBatch:
     decode_geometry: Optional[tuple] = None  # decode, nondet: plan_variant's attention geometry
     decode_wg_order: Optional[torch.Tensor] = None  # decode: the attention's workgroup order
     decode_workers: int = 0  # decode: workgroups of a worker launch of the attention (0: grid)
-    decode_busy: int = -1  # decode, worker launches: non-empty items leading the order
 
     def build_indices(self) -> None:
         """Enqueue the deferred kv_indices build (a no-op when the builder already ran it).

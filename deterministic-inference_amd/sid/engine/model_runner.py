@@ -22,7 +22,7 @@ from sid.engine.kv_cache import KVCache
 from sid.engine.sampler import sample as _sample
 from sid.kernels.decode_attention import (INVARIANT_VARIANT, DecodeAttention, length_bucket,
                                           plan_variant, segment_tokens, stage1_workers,
-                                          workgroup_order)
+                                          worker_order, workgroup_order)
 from sid.kernels.matmul_persistent import linear_sample_supported
 from sid.model.loader import build_model_config, load_weights, random_weights
 from sid.model.qwen3 import Qwen3Model
@@ -217,21 +217,17 @@ class ModelRunner:
         tokens = segment_tokens(fb.seq_lens_host, rows, splits, fixed, seg, slots)
         fb.decode_wg_order = None
         fb.decode_workers = 0
-        fb.decode_busy = -1
         cu = da.cu_count()
         nonempty = int(np.count_nonzero(tokens))
         workers = stage1_workers(nonempty, fb.decode_variant, slots, cu)
         if workers == 0 and nonempty < cu:
             return 0
-        order = workgroup_order(tokens, workers or cu)
+        order = worker_order(tokens, workers) if workers else workgroup_order(tokens, cu)
         if self.graphs is not None:
             fb.decode_wg_order = self.graphs.decode_static.set_order(order)
         else:
             fb.decode_wg_order = torch.from_numpy(order).to(self.device)
         fb.decode_workers = workers
-        # With at most one non-empty item per worker, the heaviest-first dealing keeps them all
-        # in its first round (never reversed): the entries from `nonempty` on are empty.
-        fb.decode_busy = nonempty if workers and nonempty <= workers else -1
         return workers or 1
 
     def _pick_variant(self, fb: ForwardBatch, bs: int, max_len: int) -> tuple:

@@ -42,7 +42,7 @@ _SIGNATURES = {
                                       _i32, _vp, _vp],
     "sid_flash_decode_workers_fwd": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
                                      _i32, _i32, _i32, _i32, _i32, _vp, _f32, _vp, _vp, _i32,
-                                     _i32, _vp, _i32, _i32, _vp],
+                                     _i32, _vp, _i32, _vp],
     "sid_flash_decode_segments_fwd_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
                                               _i32, _i64, _i32, _i32, _i32, _i32, _i32, _vp,
                                               _f32, _vp, _vp],
@@ -124,12 +124,12 @@ class NativeLib:
                          max_splits: int, fixed_split_size: int, sm_scale: float,
                          part_o, part_lse, o, segment_size: int = 0,
                          grid_slots: int | None = None, variant: int = 0,
-                         wg_order=None, workers: int = 0, busy: int = -1) -> None:
+                         wg_order=None, workers: int = 0) -> None:
         """segment_size / grid_slots / variant / wg_order: see sid_flash_decode_segments_fwd
         (defaults: one segment per split, grid of max_splits slots = the reference's
         partition, the default workgroup shape, the grid's own order); workers > 0: stage 1
-        by that many workgroups over the items of wg_order (sid_flash_decode_workers_fwd), whose
-        entries from `busy` on hold no tokens (-1: visit every entry)."""
+        by that many workgroups over the items of wg_order (sid_flash_decode_workers_fwd; entries
+        flagged ORDER_EMPTY hold no tokens)."""
         _gpu(q, "q", torch.bfloat16)
         _check(q.dim() == 3, "q must be [B, HQ, D]")
         b, hq, d = q.shape
@@ -162,7 +162,7 @@ class NativeLib:
                    int(fixed_split_size), int(segment_size), slots, int(variant), order,
                    float(sm_scale),
                    part_o.data_ptr(), part_lse.data_ptr(), part_o.shape[0], part_o.shape[2],
-                   o.data_ptr(), int(workers), int(busy), _stream(q))
+                   o.data_ptr(), int(workers), _stream(q))
 
     def flash_decode_fwd_noalloc(self, q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                  max_splits: int, fixed_split_size: int, sm_scale: float, o,

@@ -238,6 +238,7 @@ def plan_variant(lengths, max_len: int, num_kv_heads: int, cu_count: int, max_kv
 
 
 ORDER_SLOT_BITS = 12  # sid_flash_decode_segments_fwd wg_order entries: request << 12 | slot
+ORDER_EMPTY = 1 << 30  # wg_order entry flag of a worker launch: the item holds no tokens
 
 
 def segment_tokens(lengths, rows: int, splits: int, fixed_split: int, seg: int,
@@ -315,6 +316,18 @@ def stage1_workers(nonempty: int, variant: int, slots: int, cu_count: int) -> in
     return 0
 
 
+def worker_order(tokens: np.ndarray, workers: int) -> np.ndarray:
+    """The wg_order of a worker launch: workgroup_order dealt over the workers, with the
+    entries of items that hold no tokens flagged ORDER_EMPTY when they all come after every
+    worker's non-empty ones (true when the non-empty items fit one round of the dealing,
+    which is never reversed), so each worker marks its empty tail in one pass."""
+    order = workgroup_order(tokens, workers)
+    nonempty = int(np.count_nonzero(tokens))
+    if nonempty <= workers:
+        order[nonempty:] |= ORDER_EMPTY
+    return order
+
+
 def workspace_slots(max_seq_len: int, max_kv_splits: int, invariant_split_size: int) -> int:
     """Partial slots per request the workspace must hold for any plan."""
     nondet = -(-max_seq_len // SEGMENT_SIZES[-1]) + max_kv_splits
@@ -377,8 +390,7 @@ class DecodeAttention:
                 max_seq_len: int, sm_scale: float, invariant: bool,
                 policy_batch: int | None = None, variant: int | None = None,
                 geometry: tuple | None = None,
-                wg_order: torch.Tensor | None = None, workers: int = 0,
-                busy: int = -1) -> torch.Tensor:
+                wg_order: torch.Tensor | None = None, workers: int = 0) -> torch.Tensor:
         """q: [B, HQ, D] bf16 -> o: [B, HQ, D] bf16 (max_seq_len is host-side, no sync).
         policy_batch: real requests among the B rows (the rest are empty padding); variant:
         the stage-1 workgroup shape (stage1_variant; None: INVARIANT_VARIANT in batch_invariant
@@ -386,8 +398,8 @@ class DecodeAttention:
         plan_variant's nondet geometry for this batch (None: from the batch size and
         max_seq_len alone); wg_order: workgroup_order of this plan, on the device (None: the
         grid's own order); workers > 0: stage 1 by that many workgroups, each computing the
-        items of wg_order dealt to it (then a permutation of every (request, slot) item), the
-        entries from `busy` on known to be empty (-1: unknown)."""
+        items of wg_order dealt to it (then a permutation of every (request, slot) item; see
+        worker_order)."""
         if variant is None:
             variant = INVARIANT_VARIANT if invariant else 0
         assert not invariant or variant == INVARIANT_VARIANT, \
@@ -407,5 +419,5 @@ class DecodeAttention:
         self.ext.flash_decode_fwd(q, k_cache, v_cache, kv_indptr, kv_indices, num_splits,
                                   grid_splits, fixed, sm_scale, self.part_o, self.part_lse, o,
                                   segment_size=seg, grid_slots=slots, variant=variant,
-                                  wg_order=wg_order, workers=workers, busy=busy)
+                                  wg_order=wg_order, workers=workers)
         return o

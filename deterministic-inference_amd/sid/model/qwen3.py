@@ -92,7 +92,7 @@ class Qwen3Model:
                                     fb.max_seq_len, self.sm_scale, invariant=fb.invariant,
                                     policy_batch=fb.real_rows, variant=fb.decode_variant,
                                     geometry=fb.decode_geometry, wg_order=fb.decode_wg_order,
-                                    workers=fb.decode_workers, busy=fb.decode_busy)
+                                    workers=fb.decode_workers)
         else:
             qo = fb.qo_indptr
             if qo is None:  # decode through the extend kernel: one query per request

@@ -120,12 +120,11 @@ int sid_flash_decode_segments_fwd(const void* q, const void* k_cache, const void
  * as the grid launch computes it, so the result is the same, bit for bit; the
  * caller deals the items so that the workers' token counts balance (ragged
  * batches, where the grid's workgroups cannot all be kept equally busy).
- * busy: entries of wg_order from index busy on hold no tokens (the caller
- * orders the items heaviest first); each worker then marks its remaining
- * items empty in one pass instead of visiting them one by one. A negative busy
- * means every entry is visited. If an entry past busy did hold tokens, its
- * tokens would be dropped from the result: busy is the count of non-empty
- * items, or -1.
+ * An entry with bit 30 set (SID_ORDER_EMPTY) is an item the caller knows to
+ * hold no tokens; in each worker's sequence such entries must follow all of its
+ * other entries. A worker marks them empty in one pass instead of visiting them
+ * one by one (a flagged item that did hold tokens would be dropped from the
+ * result). The grid launch ignores the flag.
  * workers == 0 is sid_flash_decode_segments_fwd. Ignored when grid_slots == 1.
  * Builds on sid_flash_decode_fwd (sid/csrc/flash_decode.cu:307-406): same
  * split geometry, partials and merge; the worker placement has no counterpart
@@ -138,8 +137,8 @@ int sid_flash_decode_workers_fwd(const void* q, const void* k_cache, const void*
                                  int max_splits, int fixed_split_size, int segment_size,
                                  int grid_slots, int variant, const int32_t* wg_order,
                                  float sm_scale, float* part_o, float* part_lse, int part_batch,
-                                 int part_stride, void* o, int workers, int busy,
-                                 void* stream);
+                                 int part_stride, void* o, int workers, void* stream);
+#define SID_ORDER_EMPTY (1 << 30)
 
 /*
  * No counterpart in the reference. For callers that cannot allocate device

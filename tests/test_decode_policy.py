@@ -339,3 +339,35 @@ def test_worker_dealing_covers_every_item_once():
                 loads[w] += tok[y, b]
         assert len(seen) == slots * rows
         assert loads.max() - loads.min() <= tok.max()
+
+
+def test_worker_order_flags_only_trailing_empty_items():
+    """worker_order flags the empty items (ORDER_EMPTY) when the non-empty ones fit one round
+    of the dealing; then in every worker's sequence (entries w, w + W, ...) the flagged
+    entries are exactly the empty items and come after all the others. With more non-empty
+    items than workers nothing is flagged."""
+    import numpy as np
+
+    from sid.kernels.decode_attention import (ORDER_EMPTY, ORDER_SLOT_BITS, worker_order,
+                                              workgroup_order)
+    rng = np.random.default_rng(4)
+    for trial in range(40):
+        slots, rows = int(rng.integers(1, 20)), int(rng.integers(1, 40))
+        tok = rng.integers(1, 500, size=(slots, rows))
+        tok[rng.random((slots, rows)) < rng.random()] = 0
+        workers = int(rng.integers(1, 300))
+        order = worker_order(tok, workers)
+        plain = workgroup_order(tok, workers)
+        assert ((order & ~ORDER_EMPTY) == plain).all()
+        nonempty = int(np.count_nonzero(tok))
+        flag = (order & ORDER_EMPTY) != 0
+        if nonempty > workers:
+            assert not flag.any()
+            continue
+        entry = order & ~ORDER_EMPTY
+        b, y = entry >> ORDER_SLOT_BITS, entry & ((1 << ORDER_SLOT_BITS) - 1)
+        assert (flag == (tok[y, b] == 0)).all()
+        for w in range(workers):
+            f = flag[w::workers]
+            if f.any():
+                assert f[int(np.argmax(f)):].all()

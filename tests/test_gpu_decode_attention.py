@@ -38,6 +38,17 @@ def _run(q, k, v, indptr, idx, num_splits, grid, fixed, seg=0, slots=None, varia
     return o
 
 
+def _run_ordered(q, k, v, indptr, idx, nst, grid, fixed, seg, slots, variant, order):
+    """A grid launch with a workgroup order, into NaN-prefilled workspaces."""
+    bs = q.shape[0]
+    part_o = torch.full((bs, HQ, slots, D), float("nan"), device="cuda")
+    part_lse = torch.full((bs, HQ, slots), float("nan"), device="cuda")
+    o = torch.empty_like(q)
+    _ext().flash_decode_fwd(q, k, v, indptr, idx, nst, grid, fixed, SCALE, part_o, part_lse, o,
+                            segment_size=seg, grid_slots=slots, variant=variant, wg_order=order)
+    return o
+
+
 def _slots(seq_lens, num_splits, fixed, seg):
     """Partial slots the segmented grid needs (max over requests of n_splits * sps)."""
     best = 1
@@ -198,7 +209,8 @@ def test_worker_launch_equals_grid(policy, variant):
     below, at and above the item count (ragged batch with an empty request and a one-token
     request; NaN-prefilled workspaces, so every partial the merge reads is written), and
     stays within the fp32 oracle's tolerance."""
-    from sid.kernels.decode_attention import segment_tokens, workgroup_order
+    from sid.kernels.decode_attention import (ORDER_EMPTY, segment_tokens, worker_order,
+                                              workgroup_order)
     ext = _ext()
     rng = np.random.default_rng(21)
     lens = [int(x) for x in np.minimum(rng.lognormal(np.log(400), 1.0, 24), 5000).astype(int)]
@@ -217,22 +229,24 @@ def test_worker_launch_equals_grid(policy, variant):
     plain = _run(q, k, v, indptr, idx, ns, grid, fixed, seg=seg, slots=slots, variant=variant)
     nst = torch.tensor(ns, dtype=torch.int32, device="cuda")
     items = len(lens) * slots
-    nonempty = int(np.count_nonzero(tok))
     for workers in (1, 7, cu, items + 5):
-        order = torch.from_numpy(workgroup_order(tok, workers)).cuda()
-        # busy = the non-empty count is a valid promise when the heaviest-first dealing keeps
-        # every non-empty item in its first, never reversed, round (or one item per round)
-        busies = [-1] + ([nonempty] if nonempty <= workers or workers == 1 else [])
-        for busy in busies:
+        # plain dealing, and worker_order's (empty items flagged when they all trail)
+        for order_np in (workgroup_order(tok, workers), worker_order(tok, workers)):
+            order = torch.from_numpy(order_np).cuda()
+            flagged = int((order_np & ORDER_EMPTY != 0).sum())
             print(f"policy={policy} variant={variant} slots={slots} workers={workers} "
-                  f"busy={busy}", flush=True)
+                  f"flagged={flagged}", flush=True)
             part_o = torch.full((len(lens), HQ, slots, D), float("nan"), device="cuda")
             part_lse = torch.full((len(lens), HQ, slots), float("nan"), device="cuda")
             o = torch.empty_like(q)
             ext.flash_decode_fwd(q, k, v, indptr, idx, nst, grid, fixed, SCALE, part_o,
                                  part_lse, o, segment_size=seg, grid_slots=slots,
-                                 variant=variant, wg_order=order, workers=workers, busy=busy)
-            assert torch.equal(o, plain), (workers, busy)
+                                 variant=variant, wg_order=order, workers=workers)
+            assert torch.equal(o, plain), (workers, flagged)
+    # the grid launch ignores the flag
+    order = torch.from_numpy(worker_order(tok, items + 5)).cuda()
+    o = _run_ordered(q, k, v, indptr, idx, nst, grid, fixed, seg, slots, variant, order)
+    assert torch.equal(o, plain)
     assert (o[5] == 0).all()
     assert_close_bf16(o, decode_attention_ref(q, k, v, indptr, idx, SCALE))
 

@@ -138,3 +138,45 @@ def test_decode_worker_launch_equals_grid(graphs, monkeypatch):
     assert fb.decode_workers == 0
     grid = runner.forward(fb)
     assert torch.equal(worker, grid)
+
+
+def test_decode_worker_graph_replays_follow_each_steps_order():
+    """Decode steps through a captured graph whose attention runs as a worker launch: the
+    order (with its empty-item flags) is refilled every step, so replays of one graph for
+    batches with different non-empty segments give the eager forward's logits bitwise."""
+    import numpy as np
+
+    from sid.kernels.decode_attention import ORDER_EMPTY
+    lens = [2596, 2019, 1680, 1028, 1131, 410, 503, 344]
+    logs, keys, flags = {}, {}, {}
+    for graphs in (False, True):
+        cfg = EngineConfig(mode=Mode.NONDET, kv_pool_tokens=16384, max_reqs=16,
+                           max_seq_len=4096, max_decode_batch=16, num_layers=2, seed=13,
+                           use_graphs=graphs)
+        runner = ModelRunner(cfg, "cuda")
+        reqs = _requests(runner, lens, seed=5)
+        fb = build_prefill_batch(reqs, runner.kv_cache, "cuda", invariant=False)
+        for r, t in zip(reqs, runner.sample(fb, runner.forward(fb)).tolist()):
+            r.output_ids.append(t)
+        logs[graphs], keys[graphs], flags[graphs] = [], [], []
+        for step in range(70):
+            fb = runner.prepare_decode(reqs, False)
+            keys[graphs].append((fb.graph_key, fb.decode_workers))
+            if fb.decode_workers:
+                order = fb.decode_wg_order.cpu().numpy()
+                flags[graphs].append(int((order & ORDER_EMPTY != 0).sum()))
+            lg = runner.forward(fb)
+            logs[graphs].append(lg.clone())
+            for r, t in zip(reqs, runner.sample(fb, lg).tolist()):
+                r.output_ids.append(t)
+    for a, b in zip(logs[True], logs[False]):
+        assert torch.equal(a, b)
+    used = [k for k in keys[True] if k[1]]
+    if not used:
+        pytest.skip("this device's CU count gives no worker plan for these lengths")
+    # one graph served steps with different sets of empty items
+    by_key = {}
+    for (k, w), f in zip(used, flags[True]):
+        by_key.setdefault(k, set()).add(f)
+    print({str(k)[:60]: sorted(v) for k, v in by_key.items()}, flush=True)
+    assert any(len(v) > 1 for v in by_key.values())
