@@ -1704,8 +1704,12 @@ static int64_t sample_ws_bytes(int64_t m) {
   return waves * m * 4 * 7;
 }
 
+// Rows one sid_linear_sample call takes: the streaming grouping up to kStreamMaxM, the
+// 128-column tiles up to this many (prefill / verify passes of large batches).
+constexpr int64_t kTiledSampleMaxM = 4096;
+
 extern "C" int64_t sid_linear_sample_workspace_bytes(int64_t m) {
-  if (m < 1 || m > kStreamMaxM) return 0;
+  if (m < 1 || m > kTiledSampleMaxM) return 0;
   return sample_ws_bytes(m);
 }
 
@@ -1745,9 +1749,12 @@ extern "C" int sid_linear_sample(const void* x, int64_t ldx, const void* w, int6
               "linear_sample: null pointer");
   int rc = check_shapes(x, ldx, w, m, n, k, "linear_sample");
   if (rc != SID_OK) return rc;
-  SID_REQUIRE(stream_shape_ok(m, n, k),
-              "linear_sample: needs 1 <= M <= %d and K == %d (got M=%lld, K=%lld)",
-              (int)kStreamMaxM, WIDE_K, (long long)m, (long long)k);
+  const bool tiled =
+      (flags & 2) != 0 || ((flags & 4) == 0 && (m > kStreamSampleMaxM || logits != nullptr));
+  SID_REQUIRE(stream_shape_ok(tiled ? 1 : m, n, k) && m <= kTiledSampleMaxM,
+              "linear_sample: needs K == %d and 1 <= M <= %d (%d with the 128-column tiles); "
+              "got M=%lld, K=%lld",
+              WIDE_K, (int)kStreamMaxM, (int)kTiledSampleMaxM, (long long)m, (long long)k);
   const int64_t need = sample_ws_bytes(m);
   SID_REQUIRE(workspace_bytes >= need, "linear_sample: workspace %lld bytes, need %lld",
               (long long)workspace_bytes, (long long)need);
@@ -1755,8 +1762,6 @@ extern "C" int sid_linear_sample(const void* x, int64_t ldx, const void* w, int6
               "linear_sample: workspace must be 16-byte aligned");
   SID_REQUIRE(!(flags & 4) || logits == nullptr,
               "linear_sample: the streaming grouping writes no logits");
-  const bool tiled =
-      (flags & 2) != 0 || ((flags & 4) == 0 && (m > kStreamSampleMaxM || logits != nullptr));
   const int stream_groups = stream_grid() * STREAM_WAVES;
   const int groups = tiled ? static_cast<int>((n + 127) / 128) : stream_groups;
   SID_REQUIRE(groups <= stream_groups, "linear_sample: N=%lld has more than %d column tiles",

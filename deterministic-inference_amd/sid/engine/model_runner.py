@@ -106,33 +106,44 @@ class ModelRunner:
                                   sample=sample, with_logits=with_logits)
 
     def _invariant_fused(self) -> bool:
-        """batch_invariant mode's one choice per engine (never per batch) for its rows
+        """batch_invariant mode's one choice per engine (never per batch) for its decode rows
         without top-k / top-p limits: the lm_head-fused sampler when every decode batch fits
-        it (max_decode_batch <= 256). The fused sampler and the sampler kernel agree except at
-        float near-ties of the scores (their softmax sums run in different orders), so a
-        row's path must follow from the row alone."""
-        return linear_sample_supported(self.cfg.max_decode_batch, self.mcfg.hidden_size)
+        its streaming grouping (max_decode_batch <= 256). The fused sampler and the sampler
+        kernel agree except at float near-ties of the scores (their softmax sums run in
+        different orders), so a row's path must follow from the row alone."""
+        return linear_sample_supported(self.cfg.max_decode_batch, self.mcfg.hidden_size,
+                                       tiles=False)
+
+    def _sampled_rows(self, fb: ForwardBatch) -> int:
+        return fb.input_ids.shape[0] if fb.sample_indices is None else fb.sample_indices.shape[0]
+
+    def _tiles_always(self, fb: ForwardBatch) -> bool:
+        """Prefill and verify passes draw every row without top-k / top-p limits in the
+        lm_head with 128-column tiles at every size (tokens independent of the pass's size
+        and makeup; a prefill batch has at most max_decode_batch rows, a verify pass G x W)."""
+        return fb.mode in (ForwardMode.PREFILL, ForwardMode.VERIFY) and linear_sample_supported(
+            self._sampled_rows(fb), self.mcfg.hidden_size, tiles=True)
 
     def fused_sample(self, fb: ForwardBatch) -> bool:
         """Whether a batch without top-k / top-p limits draws its tokens inside the lm_head
         (sid_linear_sample) instead of writing logits for the sampler kernel, and with which
         softmax-sum grouping (set on fb.sample_tiles; it is part of a row's result, see
         linear_sample):
-          * DVR verify passes: always, with 128-column tiles at every size (their tokens are
-            the committed ones and must not depend on the pass's size);
+          * prefill and verify passes: always, with 128-column tiles at every size (a
+            verify pass's tokens are the committed ones, a prefill's first tokens are
+            committed directly; neither may depend on the pass's size);
           * batch_invariant decode batches: the engine's one choice (_invariant_fused), with
             the streaming grouping at every size;
           * other decode batches: by speed, grouping by row count (T = 0.7, graph-timed:
             1 row 80 vs 178 us for logits + sampler kernel, 64: 120 vs 205, 128: 158 vs 231,
             256: 284 vs 329); dvr commits only the verifier's tokens, nondet is free."""
-        if not fb.untruncated or fb.mode == ForwardMode.PREFILL:
+        if not fb.untruncated:
             return False
-        if not linear_sample_supported(fb.input_ids.shape[0] if fb.sample_indices is None
-                                       else fb.sample_indices.shape[0], self.mcfg.hidden_size):
-            return False
-        if fb.mode == ForwardMode.VERIFY:
+        if fb.mode in (ForwardMode.PREFILL, ForwardMode.VERIFY):
             fb.sample_tiles = True
-            return True
+            return self._tiles_always(fb)
+        if not linear_sample_supported(self._sampled_rows(fb), self.mcfg.hidden_size):
+            return False
         if fb.invariant:
             fb.sample_tiles = False
             return self._invariant_fused()
@@ -144,20 +155,18 @@ class ModelRunner:
         lm_head + argmax path, a batch without top-k / top-p limits the fused lm_head +
         sampler where fused_sample says so (no logits written); the rest writes the logits
         and runs the sampler kernel over them. A batch that mixes rows with and without
-        limits and needs the fused sampler's tokens for the latter (a batch_invariant decode
-        batch on an engine whose choice is the fused sampler, or a verify pass) gets both:
-        the fused sampler's tokens for the rows without limits (as in any other batch), the
-        sampler kernel's for the others."""
+        limits and needs the fused sampler's tokens for the latter (a prefill or verify
+        pass, or a batch_invariant decode batch on an engine whose choice is the fused
+        sampler) gets both: the fused sampler's tokens for the rows without limits (as in
+        any other batch), the sampler kernel's for the others."""
         if fb.all_greedy:
             return self.forward(fb, greedy=True)
         if self.fused_sample(fb):
             return self.forward(fb, sample=True)
-        mixed_verify = fb.mode == ForwardMode.VERIFY and linear_sample_supported(
-            fb.sample_indices.shape[0] if fb.sample_indices is not None else fb.input_ids.shape[0],
-            self.mcfg.hidden_size)
+        mixed_tiles = self._tiles_always(fb)
         mixed_invariant = fb.mode == ForwardMode.DECODE and fb.invariant and self._invariant_fused()
-        if mixed_verify or mixed_invariant:
-            fb.sample_tiles = True if mixed_verify else False
+        if mixed_tiles or mixed_invariant:
+            fb.sample_tiles = True if mixed_tiles else False
             logits, fused = self.forward(fb, sample=True, with_logits=True)
             r = logits.shape[0]
             free = (fb.top_ks[:r] <= 0) & (fb.top_ps[:r] >= 1.0)

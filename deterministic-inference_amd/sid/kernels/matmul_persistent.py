@@ -105,9 +105,11 @@ def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Te
     return out
 
 
-def linear_sample_supported(m: int, k: int) -> bool:
-    """Shapes the fused lm_head + sampler kernel takes (M <= 256, K = 1024)."""
-    return 1 <= m <= 256 and k == 1024
+def linear_sample_supported(m: int, k: int, tiles: Optional[bool] = None) -> bool:
+    """Shapes the fused lm_head + sampler kernel takes for a grouping (see linear_sample):
+    K = 1024; M <= 256 for the streaming waves (tiles=False), M <= 4096 otherwise (above
+    64 rows tiles=None means the tiles)."""
+    return k == 1024 and 1 <= m <= (256 if tiles is False else 4096)
 
 
 def linear_sample(x: torch.Tensor, weight: torch.Tensor, temperatures: torch.Tensor,

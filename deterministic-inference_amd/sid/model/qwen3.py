@@ -144,10 +144,11 @@ class Qwen3Model:
                 sample: bool = False, with_logits: bool = False):
         """fp32 logits [R, vocab] for the sampled rows (bf16-rounded values); with
         greedy=True, the greedy tokens int64 [R] instead (argmax of those logits, fused into
-        the lm_head GEMM for decode-sized R); with sample=True (decode batches of at most 256
-        rows, no top-k / top-p limit), the sampled tokens int64 [R], drawn inside the lm_head
-        GEMM without writing the logits (with_logits=True: (logits, those tokens)); the
-        draw's grouping is fb.sample_tiles (see linear_sample; verify passes: tiles).
+        the lm_head GEMM for decode-sized R); with sample=True (rows without a top-k / top-p
+        limit, R within linear_sample_supported), the sampled tokens int64 [R], drawn inside
+        the lm_head GEMM without writing the logits (with_logits=True: (logits, those
+        tokens)); the draw's grouping is fb.sample_tiles (see linear_sample; prefill and
+        verify passes: tiles).
 
         Same op order as sid/model/qwen3.py:88-115; the residual add + RMSNorm that follows
         each o / down projection consumes the projection directly (fused), and the down

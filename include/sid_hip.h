@@ -434,7 +434,8 @@ int sid_linear_argmax(const void* x, int64_t ldx, const void* w, const void* bia
  * launches. Outputs: logits fp32 [R, vocab] and/or tokens int64 [R]
  * (R = num_samples, or num_tokens without sample_indices): the greedy argmax,
  * or with b->temperatures the fused sampler's draw (sid_linear_sample: rows
- * without a top-k / top-p limit; needs hidden 1024 and R <= 256).
+ * without a top-k / top-p limit; needs hidden 1024 and R <= 4096, R <= 256
+ * for the streaming grouping).
  */
 typedef struct {
   const void* input_ln;
@@ -504,14 +505,16 @@ int sid_qwen3_extend_forward(const sid_qwen3_model* m, const sid_extend_batch* b
 /*
  * lm_head + sampler without the logits: out[r] = the token the sampler
  * (sid/engine/sampler.py:32-69) draws from logits x[r] w^T (bf16 x [M, K] with
- * row stride ldx, w [N, K], K = 1024, 1 <= M <= 256, N a multiple of 16):
+ * row stride ldx, w [N, K], K = 1024, N a multiple of 16; 1 <= M <= 4096 with
+ * the 128-column tiles, M <= 256 with the streaming waves):
  * temperatures[r] <= 0: argmax (first index, NaN first); else
  * argmax_c log(softmax(l / T)_c + 1e-10) + gumbel(seeds[r], positions[r], c)
  * with the reference's hash, i.e. sample() with top_k <= 0 and top_p >= 1
  * (rows with a top-k / top-p limit need sid_sample_rows over the logits).
  * The logits have the bits of sid_linear's fp32 output; they are written to
  * `logits` (fp32 [M, N]) when it is not NULL. Workspace:
- * sid_linear_sample_workspace_bytes(M) bytes, 16-byte aligned. Replaces the
+ * sid_linear_sample_workspace_bytes(M) bytes (0 for an M out of range; about
+ * 57 KB per row on 256 CUs), 16-byte aligned. Replaces the
  * logits epilogue of Qwen3Model.forward (sid/model/qwen3.py:113-115) plus
  * sample() for untruncated rows. The softmax sum is accumulated over groups of
  * columns: streaming waves (up to 64 rows) or 128-column tiles (more rows, or

@@ -37,11 +37,11 @@ def _rows(m, seed):
 
 @pytest.mark.parametrize("m,tiles", [(1, None), (5, None), (64, None), (100, None),
                                      (5, True), (64, True), (128, None), (256, None),
-                                     (100, False), (256, False)])
+                                     (100, False), (256, False), (512, None), (600, True)])
 def test_fused_sample_equals_oracle(lm_head, m, tiles):
     """Streaming-wave groups up to 64 rows (tiles=None) or at any size (False); 128-column
     tile groups above 64 rows (None) or at any size (True: the grouping verify passes
-    use)."""
+    use; above 256 rows only these)."""
     from sid.kernels.matmul_persistent import linear, linear_sample
     x, temps, seeds, pos = _rows(m, 10 + m)
     print(f"fused sampler m={m} tiles={tiles}", flush=True)
@@ -72,7 +72,8 @@ def _assert_near_ties(got, want, logits, temps, seeds, pos):
         assert math.isfinite(a) and abs(a - b) < 1e-4, (r, int(got[r]), int(want[r]), a, b)
 
 
-@pytest.mark.parametrize("m,tiles", [(64, None), (64, True), (200, None), (200, False)])
+@pytest.mark.parametrize("m,tiles", [(64, None), (64, True), (200, None), (200, False),
+                                     (300, True)])
 def test_certificate_equals_full_recompute(lm_head, m, tiles):
     from sid.kernels.matmul_persistent import linear_sample
     x, temps, seeds, pos = _rows(m, 3)
@@ -114,10 +115,28 @@ def test_fused_sample_is_row_independent(lm_head, tiles):
     """A row's token does not depend on the other rows of the batch (or on its slot), for a
     fixed grouping (streaming waves or tiles, at any size)."""
     from sid.kernels.matmul_persistent import linear_sample
-    n = 200 if tiles else 80
+    n = 600 if tiles else 80
     x, temps, seeds, pos = _rows(n, 21)
     full = linear_sample(x, lm_head, temps, seeds, pos, tiles=tiles)
-    for j in (0, 17, 63, 64, 79, n - 1):
+    for j in (0, 17, 63, 64, 79, 300, n - 1):
+        if j >= n:
+            continue
         one = linear_sample(x[j:j + 1], lm_head, temps[j:j + 1], seeds[j:j + 1], pos[j:j + 1],
                             tiles=tiles)
         assert one.item() == full[j].item()
+
+
+def test_row_limits_per_grouping(lm_head):
+    """The streaming waves take at most 256 rows, the tiles at most 4096: beyond, the call
+    fails with an error (nothing launched) and the workspace query answers 0."""
+    from sid.kernels.jit import load_ext
+    from sid.kernels.matmul_persistent import linear_sample, linear_sample_supported
+    ext = load_ext()
+    assert ext.linear_sample_workspace_bytes(4096) > 0
+    assert ext.linear_sample_workspace_bytes(4097) == 0
+    assert linear_sample_supported(4096, K) and not linear_sample_supported(4097, K)
+    assert not linear_sample_supported(257, K, tiles=False)
+    x, temps, seeds, pos = _rows(257, 4)
+    ws = torch.empty(ext.linear_sample_workspace_bytes(257), dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="M <= 256"):
+        linear_sample(x, lm_head, temps, seeds, pos, workspace=ws, tiles=False)

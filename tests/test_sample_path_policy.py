@@ -3,8 +3,9 @@ the host: nothing here launches a kernel. The fused and the logits + sampler pat
 except at float near-ties, so in batch_invariant mode the choice must not depend on the
 batch (one answer per engine; a batch mixing rows with and without top-k / top-p limits
 still takes the fused path for the latter, tests/test_gpu_engine.py) and the grouping is
-fixed (streaming waves); nondet/dvr decode batches fuse up to the kernel's 256 rows with the
-grouping left to the row count; DVR verify passes always fuse, with 128-column tiles."""
+fixed (streaming waves); nondet/dvr decode batches fuse up to the kernel's 4096 rows with the
+grouping left to the row count; prefill and DVR verify passes always fuse, with 128-column
+tiles."""
 
 from __future__ import annotations
 
@@ -21,6 +22,8 @@ def _runner(max_decode_batch):
     r = SimpleNamespace(cfg=SimpleNamespace(max_decode_batch=max_decode_batch),
                         mcfg=SimpleNamespace(hidden_size=1024))
     r._invariant_fused = lambda: ModelRunner._invariant_fused(r)
+    r._sampled_rows = lambda fb: ModelRunner._sampled_rows(r, fb)
+    r._tiles_always = lambda fb: ModelRunner._tiles_always(r, fb)
     return r
 
 
@@ -44,24 +47,33 @@ def test_invariant_grouping_is_fixed():
         assert ModelRunner.fused_sample(r, fb) and fb.sample_tiles is False
 
 
-def test_nondet_fuses_up_to_256_rows():
+def test_nondet_fuses_up_to_the_kernels_rows():
     r = _runner(512)
-    for rows in (1, 128, 129, 256):
+    for rows in (1, 128, 129, 256, 512):
         fb = _fb(rows, False)
         assert ModelRunner.fused_sample(r, fb) and fb.sample_tiles is None
-    assert not ModelRunner.fused_sample(r, _fb(257, False))
+    assert not ModelRunner.fused_sample(r, _fb(4097, False))
 
 
-def test_verify_passes_fuse_with_tiles():
+@pytest.mark.parametrize("mode", [ForwardMode.VERIFY, ForwardMode.PREFILL])
+def test_verify_and_prefill_passes_fuse_with_tiles(mode):
     r = _runner(256)
-    for rows in (1, 32, 128, 256):
-        fb = _fb(rows, True, mode=ForwardMode.VERIFY)
-        assert ModelRunner.fused_sample(r, fb) and fb.sample_tiles is True
+    for rows in (1, 32, 128, 256, 512, 4096):
+        for invariant in (False, True):
+            fb = _fb(rows, invariant, mode=mode)
+            assert ModelRunner.fused_sample(r, fb) and fb.sample_tiles is True
 
 
-def test_truncated_or_prefill_batches_never_fuse():
+def test_prefill_rows_are_the_sampled_ones():
+    r = _runner(256)
+    fb = _fb(5000, False, mode=ForwardMode.PREFILL)  # 5000 prompt tokens, 3 sequences
+    fb.sample_indices = torch.tensor([99, 2999, 4999])
+    assert ModelRunner.fused_sample(r, fb) and fb.sample_tiles is True
+
+
+def test_truncated_batches_never_fuse():
     r = _runner(256)
     assert not ModelRunner.fused_sample(r, _fb(8, False, untruncated=False))
     assert not ModelRunner.fused_sample(r, _fb(8, True, untruncated=False))
-    assert not ModelRunner.fused_sample(r, _fb(8, True, untruncated=False, mode=ForwardMode.VERIFY))
-    assert not ModelRunner.fused_sample(r, _fb(8, False, mode=ForwardMode.PREFILL))
+    for mode in (ForwardMode.VERIFY, ForwardMode.PREFILL):
+        assert not ModelRunner.fused_sample(r, _fb(8, True, untruncated=False, mode=mode))
