@@ -355,13 +355,16 @@ def test_fixed256_is_batch_invariant():
         assert torch.equal(base, run(comp))
 
 
-@pytest.mark.parametrize("plan", [(0, 32, 0), (0, 32, 64), (256, 0, 64), (256, 0, 0), (0, 5, 32)],
-                         ids=["heur32", "heur32_seg64", "fixed256_seg64", "fixed256", "split5_seg32"])
+@pytest.mark.parametrize("plan", [(0, 32, 0), (0, 32, 64), (256, 0, 64), (256, 0, 0), (0, 5, 32),
+                                  (0, 6, 0), (0, 12, 0), (0, 16, 0), (0, 24, 0)],
+                         ids=["heur32", "heur32_seg64", "fixed256_seg64", "fixed256", "split5_seg32",
+                              "heur6", "heur12", "heur16", "heur24"])
 def test_stage2_latency_kernel_bits_equal_batch_kernel(plan):
     """Batches of at most 4 requests merge with the latency-oriented stage 2 and larger ones
-    with the throughput one; both fold the same slots in the same order, so a request's
-    output must be bitwise the same alone (B=1) and among 7 others (B=8), for 1 to 128 used
-    slots (more than one 32-slot load chunk)."""
+    with the throughput ones (grids of up to 32 slots: one load batch per workgroup, sized
+    4 / 8 / 12 / 16 / 24 / 32; more: the slot loop); all fold the same slots in the same
+    order, so a request's output must be bitwise the same alone (B=1) and among 7 others
+    (B=8), for 1 to 128 used slots (more than one 32-slot load chunk)."""
     fixed, max_splits, seg = plan
     g = torch.Generator().manual_seed(21)
     pool = 40000
