@@ -222,7 +222,7 @@ def attention_roofline(wl, reps):
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "kernel": f"decode_stage1_kernel (workgroup shape {VARIANT_NAMES[fb.decode_variant]}) "
-                      "+ decode_stage2_kernel (all-heads segments of <= 256 tokens, then the "
+                      "+ decode_stage2_fixed_kernel (all-heads segments of <= 256 tokens, then the "
                       "in-order merge)",
             "avg_launch_us": round(avg_ms * 1e3, 2), "bytes_per_launch": bytes_launch,
             "launches_timed": launches}
