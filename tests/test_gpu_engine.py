@@ -68,15 +68,20 @@ def test_batch_invariant_row_path_ignores_co_tenants_limits():
     """batch_invariant, T = 0.7: a request without top-k / top-p limits draws every token
     with the lm_head-fused sampler (the engine's choice at max_decode_batch <= 256) whether
     its co-tenants have limits or not; the rows with limits use the sampler kernel. The two
-    paths can disagree at float near-ties, so the path must follow from the row alone."""
+    paths can disagree at float near-ties, so the path must follow from the row alone. Its
+    first token (the prefill batch's) likewise: the lm_head-fused sampler with 128-column
+    tiles, with the logits also written when co-tenants have limits."""
     from sid.engine.model_runner import ModelRunner
     eng = _engine(Mode.BATCH_INVARIANT)
     calls = []
+    prefill_calls = []
     orig = ModelRunner.forward
 
     def spy(self, fb, greedy=False, sample=False, with_logits=False):
         if fb.mode.name == "DECODE":
             calls.append((sample, with_logits))
+        elif fb.mode.name == "PREFILL":
+            prefill_calls.append((sample, with_logits, fb.sample_tiles))
         return orig(self, fb, greedy, sample, with_logits)
 
     watched = _prompts(1, 101)[0]
@@ -91,12 +96,15 @@ def test_batch_invariant_row_path_ignores_co_tenants_limits():
                 top_k=20 if limits == "top_k" else -1,
                 top_p=0.9 if limits == "top_p" else 1.0) for i in range(len(fillers))]
             calls.clear()
+            prefill_calls.clear()
             tokens[limits] = eng.generate([watched] + fillers, params)[0].token_ids
             decode_calls = set(calls)
             if limits == "none":
                 assert decode_calls == {(True, False)}, decode_calls
+                assert set(prefill_calls) == {(True, False, True)}, prefill_calls
             else:
                 assert decode_calls == {(True, True)}, decode_calls
+                assert set(prefill_calls) == {(True, True, True)}, prefill_calls
     finally:
         ModelRunner.forward = orig
     assert tokens["none"] == tokens["top_k"] == tokens["top_p"]
