@@ -118,7 +118,21 @@ class EngineConfig:
     def __post_init__(self):
         self.mode = Mode(self.mode)
         self.decode_backend = decode_backend_kind(self.decode_backend)
+        # Prefill batches (at most max_decode_batch sequences) and verify passes (G x W
+        # rows) draw their untruncated rows inside the lm_head with one fixed grouping,
+        # which takes up to MAX_SAMPLED_ROWS rows per pass; larger passes would switch those
+        # rows to the sampler kernel, whose sums differ at float near-ties.
+        if self.max_decode_batch > MAX_SAMPLED_ROWS:
+            raise ValueError(f"max_decode_batch {self.max_decode_batch} exceeds "
+                             f"{MAX_SAMPLED_ROWS}")
+        if self.dvr_group_size * self.dvr_window_size > MAX_SAMPLED_ROWS:
+            raise ValueError(f"a verify pass of dvr_group_size x dvr_window_size = "
+                             f"{self.dvr_group_size * self.dvr_window_size} rows exceeds "
+                             f"{MAX_SAMPLED_ROWS}")
 
+
+# Rows one lm_head-fused sampling pass takes with 128-column tiles (sid_linear_sample).
+MAX_SAMPLED_ROWS = 4096
 
 _DECODE_BACKENDS = {"cuda": "hip", "hip": "hip", "triton": "extend", "extend": "extend"}
 

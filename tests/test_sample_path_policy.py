@@ -77,3 +77,17 @@ def test_truncated_batches_never_fuse():
     assert not ModelRunner.fused_sample(r, _fb(8, True, untruncated=False))
     for mode in (ForwardMode.VERIFY, ForwardMode.PREFILL):
         assert not ModelRunner.fused_sample(r, _fb(8, True, untruncated=False, mode=mode))
+
+
+def test_engine_config_bounds_sampled_rows():
+    """Prefill batches and verify passes larger than the fused sampler's 4096 rows would move
+    their untruncated rows to the sampler kernel: such configurations are refused."""
+    from sid.config import MAX_SAMPLED_ROWS, EngineConfig
+    from sid.kernels.matmul_persistent import linear_sample_supported
+    assert linear_sample_supported(MAX_SAMPLED_ROWS, 1024)
+    assert not linear_sample_supported(MAX_SAMPLED_ROWS + 1, 1024)
+    EngineConfig(max_decode_batch=MAX_SAMPLED_ROWS, dvr_group_size=128, dvr_window_size=32)
+    with pytest.raises(ValueError, match="max_decode_batch"):
+        EngineConfig(max_decode_batch=MAX_SAMPLED_ROWS + 1)
+    with pytest.raises(ValueError, match="verify pass"):
+        EngineConfig(dvr_group_size=256, dvr_window_size=32)
